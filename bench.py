@@ -1,0 +1,341 @@
+#!/usr/bin/env python3
+"""Benchmark: sparse conv3x3 us/layer + HBM GB/s at 99% spike sparsity.
+
+Default workload (N=1 GPU): the Spiking-ResNet50 layer1 3x3 conv shape at
+T=16, batch 32 (512 frames of 64x56x56 fp32 binary spikes, i.i.d.
+Bernoulli(0.01) = 99% sparsity) -> 64 channels, Kaiming-normal fp32 weights,
+through SparseConv2d (Stage-1 prescan + Stage-2 gather conv).  Inputs are
+resident in HBM before timing; data is synthetic.
+
+Prints ONE JSON line on stdout.  Extra per-config lines go to stderr and
+into the JSON's "extra" object.  Baselines: MIOpen (F.conv2d on the same
+GPU) and the CPU oracle (F.conv2d on host cores, bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+import torch  # noqa: E402
+
+METRIC = "sparse conv3x3 µs/layer + HBM GB/s at 99% spike sparsity, vs MIOpen & CPU"
+HBM_PEAK_GBS = 8000.0
+
+WORKLOADS = {
+    # name: (frames, C_in, H, W, C_out, k, s, generator, density, images)
+    "resnet50_layer1_conv3x3": (512, 64, 56, 56, 64, 3, 1, "iid", 0.01, 32),
+    "config1_conv3x3": (32, 64, 32, 32, 64, 3, 1, "iid", 0.02, 8),
+    "resnet50_layer2_conv3x3": (512, 128, 28, 28, 128, 3, 1, "iid", 0.01, 32),
+    "resnet50_layer3_conv3x3": (512, 256, 14, 14, 256, 3, 1, "iid", 0.01, 32),
+    "resnet50_layer2_0_conv3x3_s2": (512, 128, 56, 56, 128, 3, 2, "iid", 0.01, 32),
+    "resnet50_layer3_0_conv3x3_s2": (512, 256, 28, 28, 256, 3, 2, "iid", 0.01, 32),
+    "resnet50_layer4_0_conv3x3_s2": (512, 512, 14, 14, 512, 3, 2, "iid", 0.01, 32),
+    "config2_conv1x1": (512, 256, 56, 56, 64, 1, 1, "clustered", 0.0, 32),
+}
+LIF_WORKLOAD = "config4_conv3x3_lif"  # T=8, N=64, C 128->128, 28x28, Bernoulli(0.005)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_input(shape, gen, density, dev, seed=0):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    if gen == "iid":
+        return (torch.rand(shape, generator=g, device=dev) < density).float()
+    # Clustered: 16x16 blocks active with p=0.03,
+    # Bernoulli(0.3) inside active blocks.
+    n, c, h, w = shape
+    gh, gw = -(-h // 16), -(-w // 16)
+    gate = (torch.rand((n, c, gh, gw), generator=g, device=dev) < 0.03).float()
+    gate = gate.repeat_interleave(16, 2).repeat_interleave(16, 3)[:, :, :h, :w]
+    return gate * (torch.rand(shape, generator=g, device=dev) < 0.3).float()
+
+
+def make_conv(c_in, c_out, k, s, dev, half_weights=False):
+    torch.manual_seed(1)
+    conv = torch.nn.Conv2d(c_in, c_out, k, s, (k - 1) // 2, bias=False)
+    torch.nn.init.kaiming_normal_(conv.weight, mode="fan_out", nonlinearity="relu")
+    if half_weights:
+        conv = conv.half()
+    return conv.to(dev)
+
+
+def time_gpu(fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def kernel_times(fn, steps):
+    """Average per-launch duration of each library kernel, from HIP events
+    the library records on the launch stream around every kernel."""
+    from sparseflow_amd import _lib
+
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        for _ in range(steps):
+            fn()
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return {k: (cnt, ms / cnt) for k, (cnt, ms) in stats.items() if cnt > 0}
+
+
+def bench_conv(name, steps, warmup, dev, with_miopen=True):
+    from sparseflow_amd.Ops.sparse_conv2d import SparseConv2d
+
+    frames, c_in, h, w, c_out, k, s, gen, dens, images = WORKLOADS[name]
+    half_w = name.startswith("config2")
+    x = make_input((frames, c_in, h, w), gen, dens, dev)
+    conv = make_conv(c_in, c_out, k, s, dev, half_weights=half_w)
+    sp = SparseConv2d.from_dense(conv).to(dev)
+    sp.set_inference_mode(True)
+    h_out, w_out = (h + 2 * ((k - 1) // 2) - k) // s + 1, (w + 2 * ((k - 1) // 2) - k) // s + 1
+    x_bytes = x.numel() * 4
+    y_bytes = frames * c_out * h_out * w_out * 4
+    w_bytes = c_out * c_in * k * k * 4
+    alg_bytes = x_bytes + w_bytes + y_bytes
+
+    with torch.no_grad():
+        step = lambda: sp(x)  # noqa: E731
+        ms = time_gpu(step, steps, warmup)
+        kt = kernel_times(step, max(5, min(steps, 20)))
+        miopen_ms = None
+        if with_miopen:
+            torch.backends.cudnn.benchmark = True
+            wd = conv.weight.float()
+            dense = lambda: torch.nn.functional.conv2d(x, wd, None, s, (k - 1) // 2)  # noqa: E731
+            miopen_ms = time_gpu(dense, max(5, steps // 2), 3)
+    density = float(x.mean().item())
+    pack = kt.get("prescan_pack", (0, 0.0))[1]
+    convk = kt.get("conv_gather", (0, 0.0))[1]
+    res = {
+        "workload": name,
+        "us_per_layer": ms * 1e3,
+        "images_per_s": images / (ms * 1e-3),
+        "frames_per_s": frames / (ms * 1e-3),
+        "hbm_gbs": alg_bytes / (ms * 1e-3) / 1e9,
+        "hbm_frac": alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "alg_bytes": alg_bytes,
+        "input_density": density,
+        "kernels_us": {"prescan_pack": pack * 1e3, "conv_gather": convk * 1e3},
+        "kernel_bytes": {"prescan_pack": x_bytes, "conv_gather": y_bytes + w_bytes},
+        "miopen_us": None if miopen_ms is None else miopen_ms * 1e3,
+        "speedup_vs_miopen": None if miopen_ms is None else miopen_ms / ms,
+    }
+    del x, sp
+    return res
+
+
+def bench_lif(steps, warmup, dev, with_miopen=True):
+    from sparseflow_amd.Kernels.fused_conv_lif import sparse_fused_conv_lif_multistep
+    from sparseflow_amd import _lib
+
+    T, N, C, H, W, Co = 8, 64, 128, 28, 28, 128
+    x = make_input((T * N, C, H, W), "iid", 0.005, dev).reshape(T, N, C, H, W)
+    conv = make_conv(C, Co, 3, 1, dev)
+    wt = _lib.tap_major_weight(conv.weight)
+    ws = torch.empty(_lib.conv_lif_workspace_size(_lib.conv_desc(N, C, H, W, Co, H, W, 3, 1, 1, 0, 0), T),
+                     dtype=torch.uint8, device=dev)
+    alg = x.numel() * 4 + Co * C * 9 * 4 + T * N * Co * H * W * 4 + N * Co * H * W * 4
+    with torch.no_grad():
+        step = lambda: sparse_fused_conv_lif_multistep(x, conv.weight, None, w_tap=wt, workspace=ws)  # noqa: E731
+        ms = time_gpu(step, steps, warmup)
+        kt = kernel_times(step, max(5, min(steps, 20)))
+        miopen_ms = None
+        if with_miopen:
+            torch.backends.cudnn.benchmark = True
+            xf = x.reshape(T * N, C, H, W)
+
+            def dense():
+                cur = torch.nn.functional.conv2d(xf, conv.weight, None, 1, 1).reshape(T, N, Co, H, W)
+                v = torch.zeros(N, Co, H, W, device=dev)
+                for t in range(T):
+                    hmem = v + (cur[t] - v) / 2.0
+                    s_t = (hmem >= 1.0).float()
+                    v = torch.where(s_t.bool(), torch.zeros_like(hmem), hmem)
+                return v
+
+            miopen_ms = time_gpu(dense, max(5, steps // 2), 3)
+    return {
+        "workload": LIF_WORKLOAD,
+        "us_per_layer": ms * 1e3,
+        "images_per_s": N / (ms * 1e-3),
+        "hbm_gbs": alg / (ms * 1e-3) / 1e9,
+        "hbm_frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "alg_bytes": alg,
+        "kernels_us": {k: v[1] * 1e3 for k, v in kt.items()},
+        "miopen_us": None if miopen_ms is None else miopen_ms * 1e3,
+        "speedup_vs_miopen": None if miopen_ms is None else miopen_ms / ms,
+    }
+
+
+def cpu_baseline(name, target_seconds=12.0):
+    """The oracle's dense conv (F.conv2d in fp32 on host cores) -- the
+    reference's CPU fallback path -- on a bounded sample of the workload."""
+    from oracle.conv import conv2d_ref
+
+    frames, c_in, h, w, c_out, k, s, gen, dens, _ = WORKLOADS[name]
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    sample = min(frames, 64)
+    x = make_input((sample, c_in, h, w), gen, dens, torch.device("cpu"))
+    conv = make_conv(c_in, c_out, k, s, torch.device("cpu"))
+    wt = conv.weight.detach()
+    for _ in range(2):
+        conv2d_ref(x, wt, None, s, (k - 1) // 2, dtype=torch.float32)
+    times = []
+    t_end = time.perf_counter() + target_seconds
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        conv2d_ref(x, wt, None, s, (k - 1) // 2, dtype=torch.float32)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": med * (frames / sample) * 1e6,
+        "unit": "us/layer",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{sample} of {frames} frames of {name}, F.conv2d fp32 via oracle.conv.conv2d_ref, "
+                  f"median of {len(times)} runs after 2 warmup, scaled x{frames / sample:g}; "
+                  f"os.cpu_count()={os.cpu_count()}, cpu='{cpu_model}'",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="resnet50_layer1_conv3x3", choices=sorted(WORKLOADS))
+    ap.add_argument("--extra", default="all", help="'all', 'none' or comma-separated workload names (+ "
+                                                   f"{LIF_WORKLOAD})")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-miopen", action="store_true", help="skip the MIOpen baselines")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a device-to-device copy of known size (for PMC byte calibration)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: every box in this setup has a single MI355X and the "
+              "spike-sparse conv path needs no collective (frames shard independently). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    from sparseflow_amd import _lib
+
+    _lib.lib()  # fail loudly if the native library is missing
+
+    log(f"[bench] primary workload {args.workload}: steps={args.steps} warmup={args.warmup}")
+    main_res = bench_conv(args.workload, args.steps, args.warmup, dev, with_miopen=not args.no_miopen)
+    log(f"[bench] {json.dumps(main_res)}")
+
+    if args.copy_calibration:
+        n = 1 << 28  # 1 GiB of fp32
+        a = torch.empty(n, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: {n * 4} bytes read + {n * 4} bytes written per copy")
+        del a, b
+
+    extra = {}
+    names = []
+    if args.extra == "all":
+        names = [n for n in WORKLOADS if n != args.workload] + [LIF_WORKLOAD]
+    elif args.extra != "none":
+        names = [n.strip() for n in args.extra.split(",") if n.strip()]
+    for name in names:
+        torch.cuda.empty_cache()
+        steps = max(5, args.steps // 2)
+        if name == LIF_WORKLOAD:
+            r = bench_lif(steps, 3, dev, with_miopen=not args.no_miopen)
+        else:
+            r = bench_conv(name, steps, 3, dev, with_miopen=not args.no_miopen)
+        extra[name] = r
+        log(f"[bench] {json.dumps(r)}")
+
+    # Roofline of the dominant kernel (the one with the largest average launch
+    # duration) from the library's per-launch HIP events.
+    kus = main_res["kernels_us"]
+    dom = max(kus, key=lambda k: kus[k])
+    dom_bytes = main_res["kernel_bytes"][dom]
+    achieved = dom_bytes / (kus[dom] * 1e-6) / 1e9 if kus[dom] > 0 else 0.0
+    roofline = {
+        "bound": "hbm",
+        "kernel": dom,
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "avg_launch_us": round(kus[dom], 2),
+        "alg_bytes_per_launch": dom_bytes,
+    }
+    cpu = None if args.no_cpu else cpu_baseline(args.workload)
+    frames, c_in, h, w, c_out, k, s, gen, dens, images = WORKLOADS[args.workload]
+    line = {
+        "metric": METRIC,
+        "value": round(main_res["us_per_layer"], 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["us_per_layer"] / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: i.i.d. Bernoulli spikes generated on device, random Kaiming-normal weights",
+        "config": {
+            "workload": args.workload,
+            "frames": frames, "T": 16, "batch": images, "c_in": c_in, "h": h, "w": w, "c_out": c_out,
+            "kernel": k, "stride": s, "spike_density": round(main_res["input_density"], 5),
+        },
+        "hbm_gbs": round(main_res["hbm_gbs"], 1),
+        "hbm_frac": round(main_res["hbm_frac"], 4),
+        "images_per_s": round(main_res["images_per_s"], 1),
+        "miopen_us": None if main_res["miopen_us"] is None else round(main_res["miopen_us"], 2),
+        "speedup_vs_miopen": None if main_res["speedup_vs_miopen"] is None else round(main_res["speedup_vs_miopen"], 2),
+        "kernels_us": {k2: round(v, 2) for k2, v in kus.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,175 @@
+/*
+ * sparseflow.h -- C ABI of libsparseflow_hip.so, the MI355X (gfx950) kernels
+ * behind the SparseFlow spike-sparse convolution path.
+ *
+ * Every entry point takes raw device pointers, plain sizes and a hipStream_t
+ * passed as `void*` (NULL = the null stream).  Nothing here allocates device
+ * memory, synchronises the host, or depends on torch types.  All functions
+ * return an sf_status; on failure sf_last_error() describes the cause.
+ *
+ * Data layouts (all row-major, C-contiguous):
+ *   x       [n, c_in, h_in, w_in]          NCHW activations (f32 / f16 / bf16)
+ *   bits    [n, h_in*w_in, cwp] uint32     channel-packed spike bitmap: bit
+ *                                          (c & 31) of word (c >> 5) of pixel
+ *                                          p is 1 iff f16(|x[n,c,p]|) > f16(thr)
+ *                                          cwp = sf_bitmap_words_per_pixel(c_in)
+ *   flags   [n, ceil(h*w / chunk)] uint32  1 where a pixel chunk holds a value
+ *                                          outside {0, 1} (chunk is chosen by
+ *                                          the library from the shape)
+ *   wt      [c_in*k*k, c_out] f32          weights, tap-major: row
+ *                                          (ci*k + kh)*k + kw holds w[:,ci,kh,kw]
+ *   y       [n, c_out, h_out, w_out]       NCHW output, dtype = desc.out_dtype
+ *
+ * Determinism: every output element is produced by exactly one wavefront,
+ * summing bias first and then active taps in ascending (kh, kw, ci) order.
+ * Repeated calls on the same inputs are bit-identical.
+ */
+#ifndef SPARSEFLOW_H
+#define SPARSEFLOW_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum sf_status {
+  SF_OK = 0,
+  SF_ERR_INVALID = 1,      /* bad pointer, size or parameter */
+  SF_ERR_UNSUPPORTED = 2,  /* shape/pattern the kernels do not implement;
+                              callers fall back to a dense conv */
+  SF_ERR_WORKSPACE = 3,    /* workspace smaller than sf_*_workspace_size */
+  SF_ERR_HIP = 4           /* HIP runtime error (launch / event) */
+} sf_status;
+
+typedef enum sf_dtype { SF_F32 = 0, SF_F16 = 1, SF_BF16 = 2 } sf_dtype;
+
+/* Shape of one 2-D convolution over n frames (n = N, or T*N for 5-D input). */
+typedef struct sf_conv_desc {
+  int64_t n;
+  int32_t c_in, h_in, w_in;
+  int32_t c_out, h_out, w_out;
+  int32_t kernel, stride, pad;   /* supported: (3,1,1) (3,2,1) (1,1,0) (1,2,0) */
+  int32_t in_dtype, out_dtype;   /* sf_dtype */
+} sf_conv_desc;
+
+/* Multi-step LIF neuron (spikingjelly LIFNode semantics). */
+typedef struct sf_lif_params {
+  float tau;
+  float v_threshold;
+  float v_reset;        /* used when hard_reset != 0; 0.0 enters the decay otherwise */
+  int32_t hard_reset;   /* 1: v <- v_reset on spike; 0: v <- v - v_threshold */
+  int32_t decay_input;  /* 1: H = V + (I - (V - Vr))/tau; 0: H = V - (V - Vr)/tau + I */
+} sf_lif_params;
+
+/* ---- library / host utilities (no GPU needed) --------------------------- */
+
+/* Library ABI version (major*10000 + minor*100 + patch). */
+int sf_version(void);
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* sf_last_error(void);
+
+/* Smallest float c >= 0 such that f16(|v|) > f16(threshold) <=> |v| >= c for
+ * every non-NaN float v.  Restates the prescan comparison of an fp16 tensor
+ * against a Python float (Kernels/_prescan_common.py:188, `tile_max > thr`). */
+float sf_activity_cutoff(float threshold);
+
+/* uint32 words per pixel in the spike bitmap: next power of two of
+ * ceil(c/32), at least 1. */
+int sf_bitmap_words_per_pixel(int32_t c);
+
+/* Pixels per non-binary flag chunk for n frames of c x h x w (flag word
+ * f*cpf + j covers pixels [j*chunk, (j+1)*chunk) of frame f). */
+int32_t sf_prescan_chunk_pixels(int64_t n, int32_t c, int32_t h, int32_t w);
+
+/* Bytes of the bitmap and the chunk-flag array for n frames of c x h x w. */
+size_t sf_prescan_bitmap_bytes(int64_t n, int32_t c, int32_t h, int32_t w);
+size_t sf_prescan_flags_bytes(int64_t n, int32_t c, int32_t h, int32_t w);
+
+/* Workspace for sf_conv2d_forward (bitmap + flags over desc->n frames, in
+ * 256-byte aligned sections). */
+size_t sf_conv2d_workspace_size(const sf_conv_desc* desc);
+
+/* Workspace for sf_conv_lif_forward over T steps of desc->n samples. */
+size_t sf_conv_lif_workspace_size(const sf_conv_desc* desc, int32_t T);
+
+/* ---- Stage 1: prescan ---------------------------------------------------- */
+
+/* Stage 1a.  Stream x once (128-bit loads) and write the channel-packed
+ * spike bitmap plus per-chunk non-binary flags.
+ * Replaces the fp16 cast + group amax of the reference prescan
+ * (Kernels/conv2d.py:986, Kernels/_prescan_common.py:32-45,167). */
+int sf_prescan_pack(const void* x, int32_t dtype, int64_t n, int32_t c,
+                    int32_t h, int32_t w, float threshold, uint32_t* bits,
+                    uint32_t* flags, void* stream);
+
+/* Stage 1b.  For every output tile (n, gh, gw) of tile_h x tile_w output
+ * pixels, OR the bitmap over the tile's receptive field (kernel, stride,
+ * pad) and emit, each output optional (NULL skips it):
+ *   ch_mask    [tiles, cwp] uint32  active-channel mask (group size 1)
+ *   ch_count   [tiles]      int32   popcount of ch_mask
+ *   ch_list    [tiles, c]   int32   ascending active channel ids, compacted
+ *                                   through an LDS prefix sum; entries past
+ *                                   ch_count are left unwritten
+ *   ag_mask    [tiles]      int32   bit g = group g (group_size channels)
+ *                                   active; the reference's ag_mask
+ *   tile_class [tiles]      int32   0 zero / 1 sparse / 2 all groups active
+ * Tile index = (n*GH + gh)*GW + gw, GH = ceil(h_out/tile_h).
+ * Replaces _build_rf_prescan_metadata_impl / _prescan_2d_impl /
+ * _classify_tiles (Kernels/_prescan_common.py:231-275,153-189,57-109). */
+int sf_prescan_tiles(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in,
+                     int32_t w_in, int32_t h_out, int32_t w_out, int32_t kernel,
+                     int32_t stride, int32_t pad, int32_t tile_h, int32_t tile_w,
+                     int32_t group_size, uint32_t* ch_mask, int32_t* ch_count,
+                     int32_t* ch_list, int32_t* ag_mask, int32_t* tile_class,
+                     void* stream);
+
+/* ---- Stage 2: sparse convolution ----------------------------------------- */
+
+/* Sparse conv over a bitmap produced by sf_prescan_pack for the same x.
+ * Binary chunks add weight rows; chunks flagged non-binary read x and FMA.
+ * bias may be NULL.  Replaces sparse_conv3x3s1/s2 and conv1x1 NHWC kernels
+ * (Kernels/conv2d.py:237-361,564-886) and the persistent fused 1x1 kernel
+ * (Kernels/conv2d.py:364-460). */
+int sf_conv2d_sparse(const sf_conv_desc* desc, const uint32_t* bits,
+                     const uint32_t* flags, const void* x, const float* wt,
+                     const float* bias, void* y, void* stream);
+
+/* Stage 1a + Stage 2 in one call; the bitmap lives in `workspace`.
+ * Replaces sparse_conv2d_forward's device work (Kernels/conv2d.py:893-1178). */
+int sf_conv2d_forward(const sf_conv_desc* desc, const void* x, const float* wt,
+                      const float* bias, float threshold, void* workspace,
+                      size_t workspace_bytes, void* y, void* stream);
+
+/* Fused sparse conv + multi-step LIF.  x is [T, N, c_in, h, w] (desc->n = N),
+ * spikes [T, N, c_out, h_out, w_out] in desc->out_dtype, v_out [N, c_out,
+ * h_out, w_out] f32 = membrane after step T.  v_init (f32, same shape as
+ * v_out) may be NULL for V_0 = 0.  The membrane stays in registers across the
+ * T steps.  Replaces fused_bm_conv3x3_lif_8x8/8x16 + the module's T loop
+ * (Kernels/fused_conv_lif.py:63-303,310-484; Ops/sparse_fused_conv_lif.py:
+ * 184-225,271-293). */
+int sf_conv_lif_forward(const sf_conv_desc* desc, int32_t T, const void* x,
+                        const float* wt, const float* bias,
+                        const sf_lif_params* lif, float threshold,
+                        const float* v_init, void* spikes, float* v_out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- per-kernel timing (bench instrumentation) --------------------------- */
+
+/* When enabled, every kernel launched by the library is bracketed by a
+ * hipEvent pair on its stream.  sf_timing_collect synchronises those events
+ * and accumulates per-kernel totals; sf_timing_query reads them by name
+ * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif").  Returns the
+ * number of launches recorded for that kernel. */
+int sf_timing_enable(int32_t enable);
+int sf_timing_collect(void);
+int64_t sf_timing_query(const char* kernel, double* total_ms);
+void sf_timing_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSEFLOW_H */

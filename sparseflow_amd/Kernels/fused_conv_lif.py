@@ -1,0 +1,169 @@
+"""Fused sparse conv + LIF on MI355X (drop-in for Kernels/fused_conv_lif.py).
+
+The reference's fused path launches one Triton kernel per timestep and
+round-trips the membrane through HBM (Kernels/fused_conv_lif.py:310-484,
+Ops/sparse_fused_conv_lif.py:191-197); it is also unimportable as shipped
+(Kernels/fused_conv_lif.py:22).  Here one HIP launch runs all T steps: the
+membrane stays in VGPRs, spikes are written once per step and the final
+membrane once.
+
+LIF arithmetic follows the module's torch path operation for operation
+(Ops/sparse_fused_conv_lif.py:283-292), including decay_input=False and
+soft reset (v_reset=None), which the reference kernel ignores
+(Kernels/fused_conv_lif.py:451-452).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from .. import _lib
+from ..Utils.config import PRESCAN_ACTIVITY_EPS, SPARSE_DENSE_RATIO_THRESHOLD
+from .conv2d import _build_two_stage_metadata, _select_tile_sizes, choose_group_size, popcount_buf
+
+__all__ = [
+    "sparse_fused_conv_lif_forward",
+    "sparse_fused_conv_lif_multistep",
+    "lif_params",
+]
+
+FALLBACK_RATIO = SPARSE_DENSE_RATIO_THRESHOLD
+
+
+def lif_params(tau, v_threshold, v_reset, decay_input) -> _lib.LifParams:
+    hard = v_reset is not None
+    return _lib.LifParams(float(tau), float(v_threshold), float(v_reset) if hard else 0.0,
+                          1 if hard else 0, 1 if decay_input else 0)
+
+
+def _torch_lif_step(conv: torch.Tensor, v_prev: torch.Tensor, tau, v_threshold, v_reset, decay_input):
+    """One LIF step on host tensors, the module's fallback semantics
+    (Ops/sparse_fused_conv_lif.py:283-292)."""
+    vr = 0.0 if v_reset is None else float(v_reset)
+    if decay_input:
+        v_tmp = v_prev + (conv - (v_prev - vr)) / tau
+    else:
+        v_tmp = v_prev - (v_prev - vr) / tau + conv
+    spike = (v_tmp >= v_threshold).to(v_tmp.dtype)
+    if v_reset is None:
+        v_next = v_tmp - spike * v_threshold
+    else:
+        v_next = torch.where(spike.bool(), torch.full_like(v_tmp, float(v_reset)), v_tmp)
+    return spike, v_next
+
+
+def _check_pattern(kernel_size, stride, padding):
+    if (kernel_size, stride, padding) not in ((3, 1, 1), (1, 1, 0)):
+        raise _lib.UnsupportedError("fused conv-LIF supports 3x3 s1 p1 and 1x1 s1 p0")
+
+
+def sparse_fused_conv_lif_multistep(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor],
+    tau: float = 2.0,
+    v_threshold: float = 1.0,
+    v_reset: Optional[float] = 0.0,
+    decay_input: bool = True,
+    kernel_size: int = 3,
+    threshold: float = PRESCAN_ACTIVITY_EPS,
+    v_init: Optional[torch.Tensor] = None,
+    w_tap: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+    return_ms: bool = False,
+):
+    """x [T, N, C, H, W] -> (spikes [T, N, C_out, H, W] in x.dtype,
+    v_T [N, C_out, H, W] f32, ms).  One kernel launch for all T steps."""
+    if x.dim() != 5:
+        raise ValueError(f"expected [T, N, C, H, W], got {tuple(x.shape)}")
+    padding = 1 if kernel_size == 3 else 0
+    _check_pattern(kernel_size, 1, padding)
+    T, N, C, H, W = (int(v) for v in x.shape)
+    C_OUT = int(weight.shape[0])
+    H_OUT = H + 2 * padding - kernel_size + 1
+    W_OUT = W + 2 * padding - kernel_size + 1
+    if not x.is_cuda:
+        v = torch.zeros((N, C_OUT, H_OUT, W_OUT), dtype=torch.float32) if v_init is None else v_init.float()
+        outs = []
+        for t in range(T):
+            conv = F.conv2d(x[t], weight, bias, stride=1, padding=padding).float()
+            s, v = _torch_lif_step(conv, v, tau, v_threshold, v_reset, decay_input)
+            outs.append(s.to(x.dtype))
+        return torch.stack(outs, 0), v, 0.0
+
+    x = x.contiguous()
+    wt = w_tap if w_tap is not None else _lib.tap_major_weight(weight)
+    b = None if bias is None else bias.detach().to(torch.float32).contiguous()
+    vi = None if v_init is None else v_init.detach().to(torch.float32).contiguous()
+    if vi is not None and tuple(vi.shape) != (N, C_OUT, H_OUT, W_OUT):
+        raise ValueError(f"v_init shape {tuple(vi.shape)} != {(N, C_OUT, H_OUT, W_OUT)}")
+    code = _lib.dtype_code(x.dtype)
+    desc = _lib.conv_desc(N, C, H, W, C_OUT, H_OUT, W_OUT, kernel_size, 1, padding, code, code)
+    need = _lib.conv_lif_workspace_size(desc, T)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    spikes = torch.empty((T, N, C_OUT, H_OUT, W_OUT), dtype=x.dtype, device=x.device)
+    v_out = torch.empty((N, C_OUT, H_OUT, W_OUT), dtype=torch.float32, device=x.device)
+    ms = 0.0
+    if return_ms:
+        se, ee = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        se.record()
+    _lib.conv_lif_forward(desc, T, x, wt, b, lif_params(tau, v_threshold, v_reset, decay_input),
+                          threshold, vi, spikes, v_out, workspace)
+    if return_ms:
+        ee.record()
+        torch.cuda.synchronize(x.device)
+        ms = se.elapsed_time(ee)
+    return spikes, v_out, ms
+
+
+def sparse_fused_conv_lif_forward(
+    x,
+    v_prev,
+    weight,
+    bias,
+    tau=2.0,
+    v_threshold=1.0,
+    v_reset=0.0,
+    decay_input=True,
+    block_size=None,
+    kernel_size=3,
+    threshold=1e-6,
+    w_cl=None,
+    ag_mask_buf=None,
+    return_ms=False,
+    fallback_ratio=FALLBACK_RATIO,
+    return_avg_active_ratio=False,
+    **legacy_kwargs,
+):
+    """Single LIF step, same signature and returns as
+    Kernels/fused_conv_lif.py:310-329: (spike, v_next, ms[, ratio])."""
+    N, C, H, W = (int(v) for v in x.shape)
+    padding = 1 if kernel_size == 3 else 0
+    _check_pattern(kernel_size, 1, padding)
+    H_OUT = H + 2 * padding - kernel_size + 1
+    W_OUT = W + 2 * padding - kernel_size + 1
+    ratio = None
+    if x.is_cuda and (ag_mask_buf is not None or return_avg_active_ratio):
+        BH, BW = _select_tile_sizes(H_OUT, W_OUT)
+        GH, GW = -(-H_OUT // BH), -(-W_OUT // BW)
+        n_tiles = N * GH * GW
+        if ag_mask_buf is None or ag_mask_buf.numel() < n_tiles:
+            ag_mask_buf = torch.empty(max(n_tiles, 1), dtype=torch.int32, device=x.device)
+        tile_class = torch.empty(max(n_tiles, 1), dtype=torch.int32, device=x.device)
+        _, ng, _, _ = _build_two_stage_metadata(x.contiguous(), N, C, H, W, H_OUT, W_OUT, BH, BW, GH, GW,
+                                                kernel_size, 1, padding, threshold, ag_mask_buf, tile_class)
+        if return_avg_active_ratio:
+            ratio = popcount_buf(ag_mask_buf, n_tiles).float().mean().item() / max(ng, 1)
+    w_tap = w_cl if (w_cl is not None and w_cl.dtype == torch.float32 and w_cl.dim() == 2) else None
+    spikes, v_next, ms = sparse_fused_conv_lif_multistep(
+        x.unsqueeze(0), weight, bias, tau=tau, v_threshold=v_threshold, v_reset=v_reset,
+        decay_input=decay_input, kernel_size=kernel_size, threshold=threshold, v_init=v_prev,
+        w_tap=w_tap, return_ms=return_ms)
+    spike = spikes[0]
+    if return_avg_active_ratio:
+        return spike, v_next, ms, (1.0 if ratio is None else ratio)
+    return spike, v_next, ms

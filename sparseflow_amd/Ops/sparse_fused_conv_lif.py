@@ -1,0 +1,192 @@
+"""FusedSparseConvLIF: stateful conv + LIF module
+(drop-in for Ops/sparse_fused_conv_lif.py).
+
+Differences from the reference module, by design:
+  * 5-D input [T, B, C, H, W] runs all T steps in one HIP launch (the
+    reference loops in Python and launches per step,
+    Ops/sparse_fused_conv_lif.py:191-197); the membrane never leaves the
+    chip between steps.
+  * No spikingjelly dependency: the membrane is a plain attribute `v`
+    cleared by `reset()` (spikingjelly's MemoryModule protocol), so
+    functional.reset_net works on it.
+  * No runtime dense/sparse EMA switch: the fused kernel is always used on
+    device tensors.
+
+Host tensors follow the reference's torch fallback
+(Ops/sparse_fused_conv_lif.py:271-293).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import _lib
+from ..Kernels.fused_conv_lif import _torch_lif_step, sparse_fused_conv_lif_multistep
+
+
+def _pair(v):
+    return (int(v), int(v)) if isinstance(v, int) else tuple(int(t) for t in v)
+
+
+class FusedSparseConvLIF(nn.Module):
+    def __init__(
+        self,
+        in_channels,
+        out_channels,
+        kernel_size,
+        stride=1,
+        padding=0,
+        dilation=1,
+        groups=1,
+        bias=True,
+        tau: float = 2.0,
+        v_threshold: float = 1.0,
+        v_reset: Optional[float] = 0.0,
+        detach_reset: bool = False,
+        decay_input: bool = True,
+        backend: str = "torch",
+        threshold: float = 1e-6,
+        block_size=None,
+        return_ms: bool = False,
+    ):
+        super().__init__()
+        self.in_channels = int(in_channels)
+        self.out_channels = int(out_channels)
+        self.kernel_size = _pair(kernel_size)
+        self.stride = _pair(stride)
+        self.padding = _pair(padding)
+        self.dilation = _pair(dilation)
+        self.groups = int(groups)
+        self.tau = float(tau)
+        self.v_threshold = float(v_threshold)
+        self.v_reset = None if v_reset is None else float(v_reset)
+        self.detach_reset = bool(detach_reset)
+        self.decay_input = bool(decay_input)
+        self.backend = backend
+        self.threshold = float(threshold)
+        self.block_size = block_size
+        self.return_ms = bool(return_ms)
+
+        self.weight = nn.Parameter(torch.empty(self.out_channels, self.in_channels // self.groups, *self.kernel_size))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(self.out_channels))
+        else:
+            self.register_parameter("bias", None)
+        nn.init.kaiming_uniform_(self.weight, a=math.sqrt(5))
+        if self.bias is not None:
+            bound = 1 / math.sqrt(self.in_channels * self.kernel_size[0] * self.kernel_size[1])
+            nn.init.uniform_(self.bias, -bound, bound)
+
+        self.v: Optional[torch.Tensor] = None
+        self._last_sparse_ms = 0.0
+        self._w_tap = None
+        self._w_tap_key = None
+        self._workspace = None
+        self._last_diag = {}
+        self.collect_diag = False
+        self.profile_runtime = False
+        self._inference_mode = False
+        self.backend_family = "fused_sparse"
+        self.diag_path = "fused_conv_lif_hip"
+        self.fallback_reason = ""
+        self.meta_source = "measured"
+        self.diag_source = "measured"
+        self.support_status = "supported"
+        self.score_family = "conv"
+
+    # spikingjelly MemoryModule protocol
+    def reset(self):
+        self.v = None
+
+    def set_inference_mode(self, enabled: bool):
+        self._inference_mode = bool(enabled)
+        if enabled:
+            self.collect_diag = False
+            self.profile_runtime = False
+
+    @classmethod
+    def from_conv_and_lif(cls, conv: nn.Conv2d, lif_node, block_size=None, threshold: float = 1e-6,
+                          return_ms: bool = False):
+        mod = cls(
+            in_channels=conv.in_channels, out_channels=conv.out_channels, kernel_size=conv.kernel_size,
+            stride=conv.stride, padding=conv.padding, dilation=conv.dilation, groups=conv.groups,
+            bias=conv.bias is not None,
+            tau=float(getattr(lif_node, "tau", 2.0)),
+            v_threshold=float(getattr(lif_node, "v_threshold", 1.0)),
+            v_reset=getattr(lif_node, "v_reset", 0.0),
+            detach_reset=bool(getattr(lif_node, "detach_reset", False)),
+            decay_input=bool(getattr(lif_node, "decay_input", True)),
+            backend=str(getattr(lif_node, "backend", "torch")),
+            threshold=threshold, block_size=block_size, return_ms=return_ms,
+        )
+        with torch.no_grad():
+            mod.weight.copy_(conv.weight)
+            if conv.bias is not None:
+                mod.bias.copy_(conv.bias)
+        return mod.to(conv.weight.device)
+
+    def _conv_output_hw(self, h: int, w: int):
+        (kh, kw), (sh, sw), (ph, pw), (dh, dw) = self.kernel_size, self.stride, self.padding, self.dilation
+        return ((h + 2 * ph - dh * (kh - 1) - 1) // sh) + 1, ((w + 2 * pw - dw * (kw - 1) - 1) // sw) + 1
+
+    def _supports_fused(self, x) -> bool:
+        pattern = (self.kernel_size, self.stride, self.padding)
+        return (
+            x.is_cuda and self.groups == 1 and self.dilation == (1, 1)
+            and pattern in (((3, 3), (1, 1), (1, 1)), ((1, 1), (1, 1), (0, 0)))
+        )
+
+    def _get_w_tap(self):
+        key = (self.weight._version, self.weight.data_ptr(), self.weight.device)
+        if self._w_tap is None or self._w_tap_key != key:
+            self._w_tap = _lib.tap_major_weight(self.weight)
+            self._w_tap_key = key
+        return self._w_tap
+
+    def forward(self, x):
+        if x.dim() == 5:
+            return self._forward_multistep(x)
+        if x.dim() == 4:
+            return self._forward_multistep(x.unsqueeze(0))[0]
+        raise ValueError(f"Expected 4D or 5D input, got {x.dim()}D")
+
+    def _forward_multistep(self, x):
+        T, B, C, H, W = (int(v) for v in x.shape)
+        out_h, out_w = self._conv_output_hw(H, W)
+        state_shape = (B, self.out_channels, out_h, out_w)
+        if self.v is None or tuple(self.v.shape) != state_shape or self.v.device != x.device:
+            v_init = None  # V_0 = 0 (Ops/sparse_fused_conv_lif.py:202-203)
+        else:
+            v_init = self.v
+        if not self._supports_fused(x):
+            self.fallback_reason = "module_dense_path"
+            v = torch.zeros(state_shape, dtype=torch.float32, device=x.device) if v_init is None else v_init
+            outs = []
+            for t in range(T):
+                conv = F.conv2d(x[t], self.weight, self.bias, self.stride, self.padding, self.dilation,
+                                self.groups).float()
+                s, v = _torch_lif_step(conv, v, self.tau, self.v_threshold, self.v_reset, self.decay_input)
+                outs.append(s.to(x.dtype))
+            self.v = v
+            self._last_sparse_ms = 0.0
+            return torch.stack(outs, 0)
+        if self._workspace is None or self._workspace.device != x.device:
+            self._workspace = None
+        spikes, v_out, ms = sparse_fused_conv_lif_multistep(
+            x, self.weight, self.bias, tau=self.tau, v_threshold=self.v_threshold, v_reset=self.v_reset,
+            decay_input=self.decay_input, kernel_size=self.kernel_size[0], threshold=self.threshold,
+            v_init=v_init, w_tap=self._get_w_tap(), workspace=self._workspace, return_ms=self.return_ms)
+        self.v = v_out
+        self._last_sparse_ms = float(ms)
+        return spikes
+
+    def extra_repr(self):
+        bs = self.block_size if self.block_size is not None else "auto"
+        return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, stride={self.stride}, "
+                f"padding={self.padding}, tau={self.tau}, v_threshold={self.v_threshold}, "
+                f"v_reset={self.v_reset}, block_size={bs}, fused=True, backend=hip_t_loop")

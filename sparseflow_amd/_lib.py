@@ -1,0 +1,287 @@
+"""ctypes binding of libsparseflow_hip.so (the C ABI in include/sparseflow.h).
+
+This is the only module that talks to the native library.  Device tensors
+cross the boundary as raw pointers; the current torch stream is passed as the
+hipStream_t so library launches order with surrounding torch work.
+
+If the library is missing, every device entry point raises
+SparseFlowLibError: there is no silent fallback for ROCm tensors.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint32, c_void_p
+from pathlib import Path
+from typing import Optional, Tuple
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libsparseflow_hip.so"
+
+SF_OK = 0
+SF_ERR_INVALID = 1
+SF_ERR_UNSUPPORTED = 2
+SF_ERR_WORKSPACE = 3
+SF_ERR_HIP = 4
+
+SF_F32, SF_F16, SF_BF16 = 0, 1, 2
+_DTYPE_CODE = {torch.float32: SF_F32, torch.float16: SF_F16, torch.bfloat16: SF_BF16}
+
+# Every exported symbol of include/sparseflow.h with its ctypes signature.
+_P = c_void_p
+EXPORTS = {
+    "sf_version": (c_int, []),
+    "sf_last_error": (ctypes.c_char_p, []),
+    "sf_activity_cutoff": (c_float, [c_float]),
+    "sf_bitmap_words_per_pixel": (c_int, [c_int32]),
+    "sf_prescan_chunk_pixels": (c_int32, [c_int64, c_int32, c_int32, c_int32]),
+    "sf_prescan_bitmap_bytes": (c_size_t, [c_int64, c_int32, c_int32, c_int32]),
+    "sf_prescan_flags_bytes": (c_size_t, [c_int64, c_int32, c_int32, c_int32]),
+    "sf_conv2d_workspace_size": (c_size_t, [_P]),
+    "sf_conv_lif_workspace_size": (c_size_t, [_P, c_int32]),
+    "sf_prescan_pack": (c_int, [_P, c_int32, c_int64, c_int32, c_int32, c_int32, c_float, _P, _P, _P]),
+    "sf_prescan_tiles": (
+        c_int,
+        [_P, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+         c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P],
+    ),
+    "sf_conv2d_sparse": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "sf_conv2d_forward": (c_int, [_P, _P, _P, _P, c_float, _P, c_size_t, _P, _P]),
+    "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
+    "sf_timing_enable": (c_int, [c_int32]),
+    "sf_timing_collect": (c_int, []),
+    "sf_timing_query": (c_int64, [ctypes.c_char_p, ctypes.POINTER(c_double)]),
+    "sf_timing_reset": (None, []),
+}
+
+
+class SparseFlowLibError(RuntimeError):
+    """The native library is missing or a library call failed."""
+
+
+class UnsupportedError(SparseFlowLibError):
+    """The kernels do not implement this shape/pattern (SF_ERR_UNSUPPORTED)."""
+
+
+class ConvDesc(ctypes.Structure):
+    _fields_ = [
+        ("n", c_int64),
+        ("c_in", c_int32), ("h_in", c_int32), ("w_in", c_int32),
+        ("c_out", c_int32), ("h_out", c_int32), ("w_out", c_int32),
+        ("kernel", c_int32), ("stride", c_int32), ("pad", c_int32),
+        ("in_dtype", c_int32), ("out_dtype", c_int32),
+    ]
+
+
+class LifParams(ctypes.Structure):
+    _fields_ = [
+        ("tau", c_float), ("v_threshold", c_float), ("v_reset", c_float),
+        ("hard_reset", c_int32), ("decay_input", c_int32),
+    ]
+
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+_load_error: Optional[str] = None
+
+
+def _load() -> ctypes.CDLL:
+    global _lib, _load_error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            _load_error = (
+                f"{LIB_PATH.name} is not built; run `python -c 'import __graft_entry__ as g; g.build()'` "
+                "or `python sparseflow_amd/_build.py`"
+            )
+            raise SparseFlowLibError(_load_error)
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in EXPORTS.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+        return lib
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises SparseFlowLibError when it is not built."""
+    return _load()
+
+
+def available() -> bool:
+    try:
+        _load()
+        return True
+    except (SparseFlowLibError, OSError):
+        return False
+
+
+def _check(rc: int, what: str) -> None:
+    if rc == SF_OK:
+        return
+    msg = lib().sf_last_error().decode(errors="replace")
+    if rc == SF_ERR_UNSUPPORTED:
+        raise UnsupportedError(f"{what}: {msg}")
+    raise SparseFlowLibError(f"{what} failed (status {rc}): {msg}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise UnsupportedError(f"dtype {dtype} is not supported (float32/float16/bfloat16)") from None
+
+
+def _require_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise SparseFlowLibError(f"{name} must be a ROCm device tensor")
+
+
+# ---------------------------------------------------------------------------
+# Host utilities
+# ---------------------------------------------------------------------------
+
+def version() -> int:
+    return int(lib().sf_version())
+
+
+def activity_cutoff(threshold: float) -> float:
+    return float(lib().sf_activity_cutoff(float(threshold)))
+
+
+def words_per_pixel(c: int) -> int:
+    return int(lib().sf_bitmap_words_per_pixel(int(c)))
+
+
+def chunk_pixels(n: int, c: int, h: int, w: int) -> int:
+    return int(lib().sf_prescan_chunk_pixels(int(n), int(c), int(h), int(w)))
+
+
+def conv_desc(n, c_in, h_in, w_in, c_out, h_out, w_out, k, s, p, in_dtype, out_dtype) -> ConvDesc:
+    return ConvDesc(int(n), int(c_in), int(h_in), int(w_in), int(c_out), int(h_out), int(w_out),
+                    int(k), int(s), int(p), int(in_dtype), int(out_dtype))
+
+
+def conv2d_workspace_size(desc: ConvDesc) -> int:
+    return int(lib().sf_conv2d_workspace_size(ctypes.byref(desc)))
+
+
+def conv_lif_workspace_size(desc: ConvDesc, T: int) -> int:
+    return int(lib().sf_conv_lif_workspace_size(ctypes.byref(desc), int(T)))
+
+
+def tap_major_weight(weight: torch.Tensor) -> torch.Tensor:
+    """[C_out, C_in, k, k] -> f32 [C_in*k*k, C_out], row (ci*k + kh)*k + kw."""
+    c_out, c_in, kh, kw = weight.shape
+    return weight.detach().to(torch.float32).permute(1, 2, 3, 0).reshape(c_in * kh * kw, c_out).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Stage 1
+# ---------------------------------------------------------------------------
+
+def prescan_pack(x: torch.Tensor, threshold: float,
+                 bits: Optional[torch.Tensor] = None,
+                 flags: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x [n, c, h, w] (contiguous) -> (bits uint32 [n, h*w, cwp], flags uint32)."""
+    _require_device(x, "x")
+    if x.dim() != 4:
+        raise ValueError(f"prescan_pack expects a 4-D NCHW tensor, got {tuple(x.shape)}")
+    x = x.contiguous()
+    n, c, h, w = (int(v) for v in x.shape)
+    L = lib()
+    nbits = int(L.sf_prescan_bitmap_bytes(n, c, h, w)) // 4
+    nflags = int(L.sf_prescan_flags_bytes(n, c, h, w)) // 4
+    if bits is None:
+        bits = torch.empty(max(nbits, 1), dtype=torch.int32, device=x.device)
+    if flags is None:
+        flags = torch.empty(max(nflags, 1), dtype=torch.int32, device=x.device)
+    if bits.numel() < nbits or flags.numel() < nflags:
+        raise ValueError("bits/flags buffers are too small")
+    rc = L.sf_prescan_pack(_ptr(x), dtype_code(x.dtype), n, c, h, w, float(threshold),
+                           _ptr(bits), _ptr(flags), _stream(x.device))
+    _check(rc, "sf_prescan_pack")
+    return bits, flags
+
+
+def prescan_tiles(bits: torch.Tensor, n: int, c: int, h_in: int, w_in: int, h_out: int, w_out: int,
+                  kernel: int, stride: int, pad: int, tile_h: int, tile_w: int, group_size: int = 16,
+                  ch_mask: Optional[torch.Tensor] = None, ch_count: Optional[torch.Tensor] = None,
+                  ch_list: Optional[torch.Tensor] = None, ag_mask: Optional[torch.Tensor] = None,
+                  tile_class: Optional[torch.Tensor] = None) -> None:
+    """Fill whichever per-tile outputs are given (see sf_prescan_tiles)."""
+    _require_device(bits, "bits")
+    rc = lib().sf_prescan_tiles(
+        _ptr(bits), int(n), int(c), int(h_in), int(w_in), int(h_out), int(w_out), int(kernel),
+        int(stride), int(pad), int(tile_h), int(tile_w), int(group_size),
+        _ptr(ch_mask), _ptr(ch_count), _ptr(ch_list), _ptr(ag_mask), _ptr(tile_class), _stream(bits.device))
+    _check(rc, "sf_prescan_tiles")
+
+
+# ---------------------------------------------------------------------------
+# Stage 2 / fused
+# ---------------------------------------------------------------------------
+
+def conv2d_sparse(desc: ConvDesc, bits: torch.Tensor, flags: torch.Tensor, x: torch.Tensor,
+                  wt: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor) -> torch.Tensor:
+    rc = lib().sf_conv2d_sparse(ctypes.byref(desc), _ptr(bits), _ptr(flags), _ptr(x), _ptr(wt),
+                                _ptr(bias), _ptr(y), _stream(x.device))
+    _check(rc, "sf_conv2d_sparse")
+    return y
+
+
+def conv2d_forward(desc: ConvDesc, x: torch.Tensor, wt: torch.Tensor, bias: Optional[torch.Tensor],
+                   threshold: float, workspace: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+    rc = lib().sf_conv2d_forward(ctypes.byref(desc), _ptr(x), _ptr(wt), _ptr(bias), float(threshold),
+                                 _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                 _ptr(y), _stream(x.device))
+    _check(rc, "sf_conv2d_forward")
+    return y
+
+
+def conv_lif_forward(desc: ConvDesc, T: int, x: torch.Tensor, wt: torch.Tensor, bias: Optional[torch.Tensor],
+                     lif: LifParams, threshold: float, v_init: Optional[torch.Tensor],
+                     spikes: torch.Tensor, v_out: torch.Tensor, workspace: torch.Tensor) -> None:
+    rc = lib().sf_conv_lif_forward(
+        ctypes.byref(desc), int(T), _ptr(x), _ptr(wt), _ptr(bias), ctypes.byref(lif), float(threshold),
+        _ptr(v_init), _ptr(spikes), _ptr(v_out), _ptr(workspace),
+        workspace.numel() * workspace.element_size(), _stream(x.device))
+    _check(rc, "sf_conv_lif_forward")
+
+
+# ---------------------------------------------------------------------------
+# Per-kernel timing (bench instrumentation)
+# ---------------------------------------------------------------------------
+
+KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif")
+
+
+def timing_enable(on: bool) -> None:
+    lib().sf_timing_enable(1 if on else 0)
+
+
+def timing_reset() -> None:
+    lib().sf_timing_reset()
+
+
+def timing_collect() -> dict:
+    """Synchronise recorded launches; return {kernel: (launches, total_ms)}."""
+    _check(lib().sf_timing_collect(), "sf_timing_collect")
+    out = {}
+    for name in KERNEL_NAMES:
+        ms = c_double(0.0)
+        cnt = int(lib().sf_timing_query(name.encode(), ctypes.byref(ms)))
+        out[name] = (cnt, float(ms.value))
+    return out

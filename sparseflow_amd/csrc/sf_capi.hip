@@ -1,0 +1,439 @@
+// C ABI of libsparseflow_hip.so: argument validation, workspace layout,
+// launch sequencing and per-kernel event timing.  See include/sparseflow.h.
+#include <math.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "sf_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(int rc, const char* what) {
+  return fail(SF_ERR_HIP, std::string(what) + ": " + hipGetErrorString((hipError_t)rc));
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// ---- IEEE binary16 round-to-nearest-even, host side ------------------------
+
+uint16_t f32_to_f16_bits(float f) {
+  uint32_t x;
+  memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t exp = (x >> 23) & 0xffu;
+  uint32_t man = x & 0x7fffffu;
+  if (exp == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u : 0u));  // inf / NaN
+  const int e = (int)exp - 127 + 15;
+  if (e >= 31) return (uint16_t)(sign | 0x7c00u);  // overflow -> inf
+  if (e <= 0) {
+    // Subnormal (or zero) half: value = man_full * 2^(exp-150); unit 2^-24.
+    if (e < -10) return (uint16_t)sign;  // below half of the smallest subnormal
+    man |= 0x800000u;
+    const int shift = 14 - e;  // bits to drop so the unit becomes 2^-24
+    uint32_t q = man >> shift;
+    const uint32_t rem = man & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    return (uint16_t)(sign | q);
+  }
+  uint32_t h = sign | ((uint32_t)e << 10) | (man >> 13);
+  const uint32_t rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ++h;  // carries into the exponent correctly
+  return (uint16_t)h;
+}
+
+float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1fu;
+  const uint32_t man = h & 0x3ffu;
+  float out;
+  if (exp == 0) {
+    out = ldexpf((float)man, -24);
+    if (sign) out = -out;
+    return out;
+  }
+  if (exp == 31) {
+    uint32_t x = sign | 0x7f800000u | (man << 13);
+    memcpy(&out, &x, 4);
+    return out;
+  }
+  uint32_t x = sign | ((exp - 15 + 127) << 23) | (man << 13);
+  memcpy(&out, &x, 4);
+  return out;
+}
+
+float f16_round(float f) { return f16_bits_to_f32(f32_to_f16_bits(f)); }
+
+// ---- validation ------------------------------------------------------------
+
+bool dtype_ok(int d) { return d == SF_F32 || d == SF_F16 || d == SF_BF16; }
+
+int check_desc(const sf_conv_desc* d, bool allow_k1s2 = true) {
+  if (d == nullptr) return fail(SF_ERR_INVALID, "desc is NULL");
+  if (d->n < 0) return fail(SF_ERR_INVALID, "n < 0");
+  if (d->c_in < 1 || d->h_in < 1 || d->w_in < 1 || d->c_out < 1 || d->h_out < 1 || d->w_out < 1)
+    return fail(SF_ERR_INVALID, "non-positive dimension");
+  if (!dtype_ok(d->in_dtype) || !dtype_ok(d->out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (d->out_dtype != d->in_dtype && d->out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  const bool k3 = d->kernel == 3 && d->pad == 1 && (d->stride == 1 || d->stride == 2);
+  const bool k1 = d->kernel == 1 && d->pad == 0 && (d->stride == 1 || (allow_k1s2 && d->stride == 2));
+  if (!k3 && !k1) return fail(SF_ERR_UNSUPPORTED, "supported patterns: 3x3 s1/s2 p1, 1x1 s1 p0");
+  const int ho = (d->h_in + 2 * d->pad - d->kernel) / d->stride + 1;
+  const int wo = (d->w_in + 2 * d->pad - d->kernel) / d->stride + 1;
+  if (ho != d->h_out || wo != d->w_out) return fail(SF_ERR_INVALID, "h_out/w_out do not match the conv geometry");
+  if (sf::words_per_pixel(d->c_in) > 64) return fail(SF_ERR_UNSUPPORTED, "c_in > 2048");
+  if ((int64_t)d->h_in * d->w_in > (1 << 30) || (int64_t)d->c_in * d->kernel * d->kernel * d->c_out > (1ll << 31) - 1)
+    return fail(SF_ERR_UNSUPPORTED, "tensor too large for 32-bit in-frame offsets");
+  return SF_OK;
+}
+
+struct Workspace {
+  uint32_t* bits;
+  uint32_t* flags;
+  size_t bytes;
+};
+
+Workspace carve(void* ws, int64_t frames, int c, int h, int w) {
+  Workspace out{};
+  const size_t bits_b = align256(sf_prescan_bitmap_bytes(frames, c, h, w));
+  const size_t flags_b = align256(sf_prescan_flags_bytes(frames, c, h, w));
+  out.bits = static_cast<uint32_t*>(ws);
+  out.flags = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + bits_b);
+  out.bytes = bits_b + flags_b;
+  return out;
+}
+
+sf::PackArgs pack_args(const void* x, int64_t n, int c, int h, int w, float threshold, uint32_t* bits,
+                       uint32_t* flags) {
+  const sf::PackPlan pl = sf::make_pack_plan(n, c, h, w);
+  sf::PackArgs a{};
+  a.x = x;
+  a.bits = bits;
+  a.flags = flags;
+  a.n = n;
+  a.c = c;
+  a.hw = h * w;
+  a.cwp = pl.cwp;
+  a.csplit = pl.csplit;
+  a.vec = pl.vec;
+  a.chunks_per_frame = pl.chunks_per_frame;
+  a.total_chunks = pl.total_chunks;
+  a.cutoff = sf_activity_cutoff(threshold);
+  return a;
+}
+
+sf::ConvArgs conv_args(const sf_conv_desc* d, int64_t frames, const uint32_t* bits, const uint32_t* flags,
+                       const void* x, const float* wt, const float* bias, void* y, bool lif) {
+  const sf::PackPlan pl = sf::make_pack_plan(frames, d->c_in, d->h_in, d->w_in);
+  sf::ConvArgs a{};
+  a.bits = bits;
+  a.flags = flags;
+  a.x = x;
+  a.wt = wt;
+  a.bias = bias;
+  a.y = y;
+  a.n = d->n;
+  a.c_in = d->c_in;
+  a.h_in = d->h_in;
+  a.w_in = d->w_in;
+  a.c_out = d->c_out;
+  a.h_out = d->h_out;
+  a.w_out = d->w_out;
+  a.k = d->kernel;
+  a.s = d->stride;
+  a.p = d->pad;
+  a.cwp = pl.cwp;
+  a.chunk = pl.chunk;
+  a.chunks_per_frame = pl.chunks_per_frame;
+  a.T = 1;
+  sf::conv_geometry(a, lif);
+  a.total_groups = d->n * (int64_t)a.groups_per_frame;
+  return a;
+}
+
+// ---- timing -----------------------------------------------------------------
+
+struct TimingRec {
+  int id;
+  hipEvent_t start, end;
+};
+
+std::mutex g_tmu;
+bool g_timing = false;
+std::vector<TimingRec> g_pending;
+double g_total_ms[sf::K_COUNT] = {0, 0, 0, 0};
+int64_t g_count[sf::K_COUNT] = {0, 0, 0, 0};
+const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif"};
+
+}  // namespace
+
+namespace sf {
+
+void timing_begin(int kernel_id, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(g_tmu);
+  if (!g_timing) return;
+  TimingRec r{kernel_id, nullptr, nullptr};
+  if (hipEventCreate(&r.start) != hipSuccess) return;
+  (void)hipEventRecord(r.start, stream);
+  g_pending.push_back(r);
+}
+
+void timing_end(int kernel_id, hipStream_t stream) {
+  std::lock_guard<std::mutex> lk(g_tmu);
+  if (!g_timing) return;
+  for (auto it = g_pending.rbegin(); it != g_pending.rend(); ++it) {
+    if (it->id == kernel_id && it->end == nullptr) {
+      if (hipEventCreate(&it->end) == hipSuccess) (void)hipEventRecord(it->end, stream);
+      return;
+    }
+  }
+}
+
+}  // namespace sf
+
+extern "C" {
+
+int sf_version(void) { return 100; }
+
+const char* sf_last_error(void) { return g_last_error.c_str(); }
+
+float sf_activity_cutoff(float threshold) {
+  if (isnan(threshold)) return NAN;
+  const float th = f16_round(threshold);
+  if (isinf(th) && th > 0) return NAN;  // no half exceeds +inf: nothing is active
+  if (th < 0.f) return 0.f;              // every non-NaN |v| rounds to >= 0 > th
+  // Smallest non-negative float f with f16(f) > th; f16 rounding is monotone,
+  // so bisect over the ordered bit patterns of non-negative floats.
+  uint32_t lo = 0u, hi = 0x7f800000u;  // f16(+inf) = inf > th
+  while (lo < hi) {
+    const uint32_t mid = lo + (hi - lo) / 2;
+    float f;
+    memcpy(&f, &mid, 4);
+    if (f16_round(f) > th) hi = mid; else lo = mid + 1;
+  }
+  float out;
+  memcpy(&out, &lo, 4);
+  return out;
+}
+
+int sf_bitmap_words_per_pixel(int32_t c) { return c < 1 ? 0 : sf::words_per_pixel(c); }
+
+int32_t sf_prescan_chunk_pixels(int64_t n, int32_t c, int32_t h, int32_t w) {
+  if (n <= 0 || c < 1 || h < 1 || w < 1) return 0;
+  return sf::make_pack_plan(n, c, h, w).chunk;
+}
+
+size_t sf_prescan_bitmap_bytes(int64_t n, int32_t c, int32_t h, int32_t w) {
+  if (n <= 0 || c < 1 || h < 1 || w < 1) return 0;
+  return (size_t)n * (size_t)h * (size_t)w * (size_t)sf::words_per_pixel(c) * 4u;
+}
+
+size_t sf_prescan_flags_bytes(int64_t n, int32_t c, int32_t h, int32_t w) {
+  if (n <= 0 || c < 1 || h < 1 || w < 1) return 0;
+  return (size_t)sf::make_pack_plan(n, c, h, w).total_chunks * 4u;
+}
+
+size_t sf_conv2d_workspace_size(const sf_conv_desc* d) {
+  if (d == nullptr || d->n <= 0) return 0;
+  return align256(sf_prescan_bitmap_bytes(d->n, d->c_in, d->h_in, d->w_in)) +
+         align256(sf_prescan_flags_bytes(d->n, d->c_in, d->h_in, d->w_in));
+}
+
+size_t sf_conv_lif_workspace_size(const sf_conv_desc* d, int32_t T) {
+  if (d == nullptr || d->n <= 0 || T <= 0) return 0;
+  const int64_t frames = d->n * (int64_t)T;
+  return align256(sf_prescan_bitmap_bytes(frames, d->c_in, d->h_in, d->w_in)) +
+         align256(sf_prescan_flags_bytes(frames, d->c_in, d->h_in, d->w_in));
+}
+
+int sf_prescan_pack(const void* x, int32_t dtype, int64_t n, int32_t c, int32_t h, int32_t w, float threshold,
+                    uint32_t* bits, uint32_t* flags, void* stream) {
+  if (n < 0 || c < 1 || h < 1 || w < 1) return fail(SF_ERR_INVALID, "bad prescan shape");
+  if (!dtype_ok(dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (sf::words_per_pixel(c) > 64) return fail(SF_ERR_UNSUPPORTED, "c > 2048");
+  if ((int64_t)h * w > (1 << 30)) return fail(SF_ERR_UNSUPPORTED, "plane too large");
+  if (n == 0) return SF_OK;
+  if (x == nullptr || bits == nullptr || flags == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  const sf::PackArgs a = pack_args(x, n, c, h, w, threshold, bits, flags);
+  const int rc = sf::launch_pack(a, dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "prescan_pack launch");
+  return SF_OK;
+}
+
+int sf_prescan_tiles(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in, int32_t w_in, int32_t h_out,
+                     int32_t w_out, int32_t kernel, int32_t stride, int32_t pad, int32_t tile_h, int32_t tile_w,
+                     int32_t group_size, uint32_t* ch_mask, int32_t* ch_count, int32_t* ch_list, int32_t* ag_mask,
+                     int32_t* tile_class, void* stream) {
+  if (n < 0 || c < 1 || h_in < 1 || w_in < 1 || h_out < 1 || w_out < 1 || tile_h < 1 || tile_w < 1)
+    return fail(SF_ERR_INVALID, "bad tiles shape");
+  if (kernel < 1 || stride < 1 || pad < 0 || kernel < stride)
+    return fail(SF_ERR_UNSUPPORTED, "receptive field must be contiguous (kernel >= stride)");
+  if ((h_in + 2 * pad - kernel) / stride + 1 != h_out || (w_in + 2 * pad - kernel) / stride + 1 != w_out)
+    return fail(SF_ERR_INVALID, "h_out/w_out do not match the geometry");
+  const int cwp = sf::words_per_pixel(c);
+  if (cwp > 64) return fail(SF_ERR_UNSUPPORTED, "c > 2048");
+  const bool want_groups = ag_mask != nullptr || tile_class != nullptr;
+  int ngroups = 0;
+  if (want_groups) {
+    if (group_size < 16 || (group_size & (group_size - 1)) != 0)
+      return fail(SF_ERR_UNSUPPORTED, "group_size must be a power of two >= 16");
+    ngroups = (c + group_size - 1) / group_size;
+    if (ngroups > 32) return fail(SF_ERR_UNSUPPORTED, "more than 32 channel groups");
+  }
+  if (n == 0) return SF_OK;
+  if (bits == nullptr) return fail(SF_ERR_INVALID, "bits is NULL");
+  sf::TilesArgs a{};
+  a.bits = bits;
+  a.ch_mask = ch_mask;
+  a.ch_count = ch_count;
+  a.ch_list = ch_list;
+  a.ag_mask = ag_mask;
+  a.tile_class = tile_class;
+  a.n = n;
+  a.c = c;
+  a.cwp = cwp;
+  a.h_in = h_in;
+  a.w_in = w_in;
+  a.h_out = h_out;
+  a.w_out = w_out;
+  a.k = kernel;
+  a.s = stride;
+  a.p = pad;
+  a.th = tile_h;
+  a.tw = tile_w;
+  a.gh = (h_out + tile_h - 1) / tile_h;
+  a.gw = (w_out + tile_w - 1) / tile_w;
+  a.group_size = group_size;
+  a.ngroups = ngroups;
+  a.ntiles = n * (int64_t)a.gh * a.gw;
+  const int rc = sf::launch_tiles(a, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "prescan_tiles launch");
+  return SF_OK;
+}
+
+int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t* flags, const void* x,
+                     const float* wt, const float* bias, void* y, void* stream) {
+  int rc = check_desc(d);
+  if (rc != SF_OK) return rc;
+  if (d->n == 0) return SF_OK;
+  if (bits == nullptr || flags == nullptr || x == nullptr || wt == nullptr || y == nullptr)
+    return fail(SF_ERR_INVALID, "NULL pointer");
+  const sf::ConvArgs a = conv_args(d, d->n, bits, flags, x, wt, bias, y, false);
+  rc = sf::launch_conv(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "conv_gather launch");
+  return SF_OK;
+}
+
+int sf_conv2d_forward(const sf_conv_desc* d, const void* x, const float* wt, const float* bias, float threshold,
+                      void* workspace, size_t workspace_bytes, void* y, void* stream) {
+  int rc = check_desc(d);
+  if (rc != SF_OK) return rc;
+  if (d->n == 0) return SF_OK;
+  if (x == nullptr || wt == nullptr || y == nullptr || workspace == nullptr)
+    return fail(SF_ERR_INVALID, "NULL pointer");
+  if (workspace_bytes < sf_conv2d_workspace_size(d)) return fail(SF_ERR_WORKSPACE, "workspace too small");
+  const Workspace ws = carve(workspace, d->n, d->c_in, d->h_in, d->w_in);
+  rc = sf_prescan_pack(x, d->in_dtype, d->n, d->c_in, d->h_in, d->w_in, threshold, ws.bits, ws.flags, stream);
+  if (rc != SF_OK) return rc;
+  return sf_conv2d_sparse(d, ws.bits, ws.flags, x, wt, bias, y, stream);
+}
+
+int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const float* wt, const float* bias,
+                        const sf_lif_params* lif, float threshold, const float* v_init, void* spikes, float* v_out,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_desc(d, false);
+  if (rc != SF_OK) return rc;
+  if (d->stride != 1) return fail(SF_ERR_UNSUPPORTED, "fused conv-LIF supports stride 1");
+  if (lif == nullptr) return fail(SF_ERR_INVALID, "lif params NULL");
+  if (T < 1) return fail(SF_ERR_INVALID, "T < 1");
+  if (!(lif->tau != 0.f)) return fail(SF_ERR_INVALID, "tau must be non-zero");
+  if (d->n == 0) return SF_OK;
+  if (x == nullptr || wt == nullptr || spikes == nullptr || v_out == nullptr || workspace == nullptr)
+    return fail(SF_ERR_INVALID, "NULL pointer");
+  if (workspace_bytes < sf_conv_lif_workspace_size(d, T)) return fail(SF_ERR_WORKSPACE, "workspace too small");
+  const int64_t frames = d->n * (int64_t)T;
+  const Workspace ws = carve(workspace, frames, d->c_in, d->h_in, d->w_in);
+  rc = sf_prescan_pack(x, d->in_dtype, frames, d->c_in, d->h_in, d->w_in, threshold, ws.bits, ws.flags, stream);
+  if (rc != SF_OK) return rc;
+  // Flags/chunks are indexed by frame t*N + n over all T*N frames.
+  sf::ConvArgs a = conv_args(d, frames, ws.bits, ws.flags, x, wt, bias, spikes, true);
+  a.total_groups = d->n * (int64_t)a.groups_per_frame;
+  a.v_out = v_out;
+  a.v_init = v_init;
+  a.T = T;
+  a.tau = lif->tau;
+  a.v_th = lif->v_threshold;
+  a.v_reset = lif->v_reset;
+  a.hard_reset = lif->hard_reset != 0;
+  a.decay_input = lif->decay_input != 0;
+  rc = sf::launch_conv_lif(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "conv_lif launch");
+  return SF_OK;
+}
+
+int sf_timing_enable(int32_t enable) {
+  std::lock_guard<std::mutex> lk(g_tmu);
+  g_timing = enable != 0;
+  return SF_OK;
+}
+
+int sf_timing_collect(void) {
+  std::vector<TimingRec> recs;
+  {
+    std::lock_guard<std::mutex> lk(g_tmu);
+    recs.swap(g_pending);
+  }
+  int status = SF_OK;
+  for (auto& r : recs) {
+    if (r.end != nullptr && r.start != nullptr) {
+      if (hipEventSynchronize(r.end) == hipSuccess) {
+        float ms = 0.f;
+        if (hipEventElapsedTime(&ms, r.start, r.end) == hipSuccess) {
+          std::lock_guard<std::mutex> lk(g_tmu);
+          g_total_ms[r.id] += ms;
+          g_count[r.id] += 1;
+        } else {
+          status = SF_ERR_HIP;
+        }
+      } else {
+        status = SF_ERR_HIP;
+      }
+    }
+    if (r.start) (void)hipEventDestroy(r.start);
+    if (r.end) (void)hipEventDestroy(r.end);
+  }
+  return status;
+}
+
+int64_t sf_timing_query(const char* kernel, double* total_ms) {
+  std::lock_guard<std::mutex> lk(g_tmu);
+  for (int i = 0; i < sf::K_COUNT; ++i) {
+    if (kernel != nullptr && strcmp(kernel, g_names[i]) == 0) {
+      if (total_ms) *total_ms = g_total_ms[i];
+      return g_count[i];
+    }
+  }
+  if (total_ms) *total_ms = 0.0;
+  return -1;
+}
+
+void sf_timing_reset(void) {
+  std::lock_guard<std::mutex> lk(g_tmu);
+  for (int i = 0; i < sf::K_COUNT; ++i) {
+    g_total_ms[i] = 0.0;
+    g_count[i] = 0;
+  }
+}
+
+}  // extern "C"

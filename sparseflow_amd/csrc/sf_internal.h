@@ -1,0 +1,140 @@
+// Internal declarations shared by the prescan / conv translation units and
+// the C ABI.  gfx950 only: wave64, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#include "sparseflow.h"
+
+namespace sf {
+
+constexpr int kWave = 64;
+constexpr int kMaxLdsBytes = 160 * 1024;
+
+// ---------------------------------------------------------------------------
+// Pack plan: how Stage 1a tiles the pixel axis.  A "chunk" is the run of
+// consecutive pixels (within one frame) that one wavefront covers; the
+// non-binary flag array has one word per chunk.  The plan depends on the
+// shape only, so Stage 2 can recompute it to index the flags.
+// ---------------------------------------------------------------------------
+struct PackPlan {
+  int vec;                   // pixels per lane (4, 2 or 1)
+  int chunk;                 // pixels per chunk = 64 * vec
+  int csplit;                // waves sharing one chunk (split over words)
+  int cwp;                   // bitmap words per pixel
+  int64_t chunks_per_frame;  // ceil(h*w / chunk)
+  int64_t total_chunks;      // n * chunks_per_frame
+};
+
+PackPlan make_pack_plan(int64_t n, int c, int h, int w);
+int words_per_pixel(int c);
+
+// ---------------------------------------------------------------------------
+// Kernel argument blocks (passed by value).
+// ---------------------------------------------------------------------------
+struct PackArgs {
+  const void* x;
+  uint32_t* bits;
+  uint32_t* flags;
+  int64_t n;
+  int c, hw, cwp, csplit, vec;
+  int64_t chunks_per_frame, total_chunks;
+  float cutoff;
+};
+
+struct TilesArgs {
+  const uint32_t* bits;
+  uint32_t* ch_mask;
+  int32_t* ch_count;
+  int32_t* ch_list;
+  int32_t* ag_mask;
+  int32_t* tile_class;
+  int64_t n, ntiles;
+  int c, cwp, h_in, w_in, h_out, w_out, k, s, p;
+  int th, tw, gh, gw, group_size, ngroups;
+};
+
+struct ConvArgs {
+  const uint32_t* bits;
+  const uint32_t* flags;
+  const void* x;
+  const float* wt;
+  const float* bias;
+  void* y;             // conv output, or spikes for the fused LIF kernel
+  float* v_out;        // fused LIF only
+  const float* v_init; // fused LIF only (nullable)
+  int64_t n;           // frames of y (conv) / batch N (LIF)
+  int64_t total_groups;
+  int c_in, h_in, w_in, c_out, h_out, w_out, k, s, p, cwp;
+  int hw_in, hw_out, groups_per_frame;
+  int chunk;                 // flag chunk (pixels)
+  int64_t chunks_per_frame;
+  int cap;                   // entry-list capacity per wave
+  int fl;                    // pixels per staging flush
+  int wave_lds;              // LDS bytes per wave
+  int waves_per_block;
+  int T;                     // fused LIF: time steps
+  float tau, v_th, v_reset;
+  int hard_reset, decay_input;
+};
+
+// Launchers (return hipError_t as int).
+int launch_pack(const PackArgs& a, int dtype, hipStream_t stream);
+int launch_tiles(const TilesArgs& a, hipStream_t stream);
+int launch_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+int launch_conv_lif(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
+// Conv launch geometry shared by the ABI (workspace checks) and launchers.
+void conv_geometry(ConvArgs& a, bool lif);
+
+// Per-kernel event timing hooks used by the launchers.
+void timing_begin(int kernel_id, hipStream_t stream);
+void timing_end(int kernel_id, hipStream_t stream);
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_COUNT = 4 };
+
+// ---------------------------------------------------------------------------
+// Device helpers.
+// ---------------------------------------------------------------------------
+#if defined(__HIP_DEVICE_COMPILE__) || defined(__HIPCC__)
+
+// Order this wavefront's LDS traffic: writes issued before the call are
+// visible to reads issued after it by any lane of the same wavefront.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+template <typename T> __device__ __forceinline__ float to_f32(T v);
+template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f32<__half>(__half v) { return __half2float(v); }
+template <> __device__ __forceinline__ float to_f32<__hip_bfloat16>(__hip_bfloat16 v) {
+  return __bfloat162float(v);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ __half from_f32<__half>(float v) { return __float2half_rn(v); }
+template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(float v) {
+  return __float2bfloat16(v);
+}
+
+// Inclusive prefix sum across the 64 lanes of a wavefront.
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    int t = __shfl_up(v, off, kWave);
+    if (lane >= off) v += t;
+  }
+  return v;
+}
+
+#endif
+
+}  // namespace sf

@@ -1,0 +1,299 @@
+// Stage 1 of the spike-sparse convolution: prescan.
+//
+// k_pack   streams the NCHW activation tensor once with 128-bit loads and
+//          writes a channel-packed bitmap (one bit per element, 32 channels
+//          per word, words of a pixel contiguous) plus one non-binary flag
+//          word per pixel chunk.  Bit = f16(|x|) > f16(threshold), evaluated
+//          as |x| >= cutoff (see sf_activity_cutoff).  This is the element
+//          level form of the reference's fp16 cast + |.| + amax + "> thr"
+//          (Kernels/conv2d.py:986; Kernels/_prescan_common.py:32-45,188).
+//
+// k_tiles  reads the bitmap and, per output tile, ORs the words over the
+//          tile's receptive field -- the reference's RF max-pool followed by
+//          the ceil-mode tile max-pool (Kernels/_prescan_common.py:167-188)
+//          at group size 1 -- then derives the active-channel list (LDS
+//          compaction), the group bitmask and the tile class
+//          (Kernels/_prescan_common.py:48-109).
+#include "sf_internal.h"
+
+namespace sf {
+
+namespace {
+
+template <typename T, int VEC, bool ALIGNED>
+__device__ __forceinline__ void load_vec(const T* p, float (&v)[VEC]) {
+  if constexpr (ALIGNED && VEC == 4 && sizeof(T) == 4) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  } else if constexpr (ALIGNED && VEC == 2 && sizeof(T) == 4) {
+    const float2 q = *reinterpret_cast<const float2*>(p);
+    v[0] = q.x; v[1] = q.y;
+  } else if constexpr (ALIGNED && VEC == 4 && sizeof(T) == 2) {
+    const uint2 q = *reinterpret_cast<const uint2*>(p);
+    const uint32_t h[4] = {q.x & 0xffffu, q.x >> 16, q.y & 0xffffu, q.y >> 16};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      T t;
+      const uint16_t b = (uint16_t)h[i];
+      __builtin_memcpy(&t, &b, 2);
+      v[i] = to_f32<T>(t);
+    }
+  } else if constexpr (ALIGNED && VEC == 2 && sizeof(T) == 2) {
+    const uint32_t q = *reinterpret_cast<const uint32_t*>(p);
+    const uint16_t b0 = (uint16_t)(q & 0xffffu), b1 = (uint16_t)(q >> 16);
+    T t0, t1;
+    __builtin_memcpy(&t0, &b0, 2);
+    __builtin_memcpy(&t1, &b1, 2);
+    v[0] = to_f32<T>(t0);
+    v[1] = to_f32<T>(t1);
+  } else {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) v[i] = to_f32<T>(p[i]);
+  }
+}
+
+// One wavefront packs one chunk of 64*VEC consecutive pixels of one frame
+// over a contiguous range of bitmap words (all words when csplit == 1).  The
+// four wavefronts of a block cover 4/csplit chunks.
+template <typename T, int VEC, bool ALIGNED>
+__global__ __launch_bounds__(256) void k_pack(PackArgs a) {
+  __shared__ uint32_t s_nb[4];
+  const int wave = threadIdx.x >> 6;
+  const int lane = lane_id();
+  const int csplit = a.csplit;
+  const int lc = wave / csplit;
+  const int sp = wave - lc * csplit;
+  const int64_t gchunk = (int64_t)blockIdx.x * (4 / csplit) + lc;
+  const bool chunk_ok = gchunk < a.total_chunks;
+  const float cut = a.cutoff;
+  uint32_t nb = 0;
+
+  if (chunk_ok) {
+    const int64_t frame = gchunk / a.chunks_per_frame;
+    const int64_t chk = gchunk - frame * a.chunks_per_frame;
+    const int p0 = (int)(chk * (64 * VEC)) + lane * VEC;
+    if (p0 < a.hw) {
+      const int wps = a.cwp / csplit;
+      const int w0 = sp * wps;
+      const T* xf = static_cast<const T*>(a.x) + frame * (int64_t)a.c * a.hw + p0;
+      uint32_t* bf = a.bits + (frame * a.hw + p0) * (int64_t)a.cwp;
+      for (int cw = w0; cw < w0 + wps; ++cw) {
+        uint32_t word[VEC];
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) word[i] = 0u;
+        const int cbase = cw * 32;
+        if (cbase + 32 <= a.c) {
+          // Full word: 32 independent loads in flight per lane.
+          float v[32][VEC];
+#pragma unroll
+          for (int j = 0; j < 32; ++j) load_vec<T, VEC, ALIGNED>(xf + (int64_t)(cbase + j) * a.hw, v[j]);
+#pragma unroll
+          for (int j = 0; j < 32; ++j) {
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              word[i] |= (fabsf(v[j][i]) >= cut ? 1u : 0u) << j;
+              nb |= (v[j][i] != 0.f && v[j][i] != 1.f) ? 1u : 0u;
+            }
+          }
+        } else if (cbase < a.c) {
+          const int cnt = a.c - cbase;
+          for (int j = 0; j < cnt; ++j) {
+            float v[VEC];
+            load_vec<T, VEC, ALIGNED>(xf + (int64_t)(cbase + j) * a.hw, v);
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+              word[i] |= (fabsf(v[i]) >= cut ? 1u : 0u) << j;
+              nb |= (v[i] != 0.f && v[i] != 1.f) ? 1u : 0u;
+            }
+          }
+        }
+        if (a.cwp == 1) {
+          if constexpr (VEC == 4) {
+            *reinterpret_cast<uint4*>(bf) = make_uint4(word[0], word[1], word[2], word[3]);
+          } else if constexpr (VEC == 2) {
+            *reinterpret_cast<uint2*>(bf) = make_uint2(word[0], word[1]);
+          } else {
+            bf[0] = word[0];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) bf[(int64_t)i * a.cwp + cw] = word[i];
+        }
+      }
+    }
+  }
+
+  const uint64_t bal = __ballot(nb != 0u);
+  if (lane == 0) s_nb[wave] = bal != 0ull ? 1u : 0u;
+  __syncthreads();
+  if (chunk_ok && sp == 0 && lane == 0) {
+    uint32_t f = 0u;
+    for (int q = 0; q < csplit; ++q) f |= s_nb[lc * csplit + q];
+    a.flags[gchunk] = f;
+  }
+}
+
+// One wavefront per output tile.  Requires cwp <= 64 (a power of two), so
+// lane l always reads word (l % cwp) of the pixels it visits.
+__global__ __launch_bounds__(256) void k_tiles(TilesArgs a) {
+  extern __shared__ int32_t s_list_all[];
+  const int wave = threadIdx.x >> 6;
+  const int lane = lane_id();
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile >= a.ntiles) return;  // the kernel has no block-level barrier
+  int32_t* s_list = s_list_all + wave * a.c;
+
+  const int gwi = (int)(tile % a.gw);
+  const int64_t t2 = tile / a.gw;
+  const int ghi = (int)(t2 % a.gh);
+  const int64_t nn = t2 / a.gh;
+
+  const int oh0 = ghi * a.th;
+  const int oh1 = min(oh0 + a.th, a.h_out) - 1;
+  const int ow0 = gwi * a.tw;
+  const int ow1 = min(ow0 + a.tw, a.w_out) - 1;
+  const int ih0 = max(0, oh0 * a.s - a.p);
+  const int ih1 = min(a.h_in - 1, oh1 * a.s - a.p + a.k - 1);
+  const int iw0 = max(0, ow0 * a.s - a.p);
+  const int iw1 = min(a.w_in - 1, ow1 * a.s - a.p + a.k - 1);
+  const int rh = ih1 - ih0 + 1;
+  const int rw = iw1 - iw0 + 1;
+
+  const int cwp = a.cwp;
+  const int my_cw = lane & (cwp - 1);
+  const int px_step = kWave / cwp;
+  uint32_t acc = 0u;
+  if (rh > 0 && rw > 0) {
+    const int npx = rh * rw;
+    const uint32_t* base = a.bits + ((nn * a.h_in + ih0) * (int64_t)a.w_in + iw0) * cwp + my_cw;
+    for (int px = lane / cwp; px < npx; px += px_step) {
+      const int r = px / rw;
+      const int cc = px - r * rw;
+      acc |= base[((int64_t)r * a.w_in + cc) * cwp];
+    }
+  }
+  for (int off = kWave / 2; off >= cwp; off >>= 1) acc |= __shfl_xor(acc, off, kWave);
+  const bool own = lane < cwp;  // lane l now holds word l of the tile mask
+
+  if (a.ch_mask != nullptr && own) a.ch_mask[tile * cwp + lane] = acc;
+
+  const int pc = own ? __popc(acc) : 0;
+  const int incl = wave_inclusive_scan(pc);
+  const int total = __shfl(incl, kWave - 1, kWave);
+  if (a.ch_count != nullptr && lane == 0) a.ch_count[tile] = total;
+
+  if (a.ch_list != nullptr) {
+    // Compact: each word's owner writes its channel ids at its exclusive
+    // prefix into LDS, then the wavefront copies the list out coalesced.
+    int pos = incl - pc;
+    uint32_t wd = own ? acc : 0u;
+    while (wd != 0u) {
+      const int b = __builtin_ctz(wd);
+      wd &= wd - 1u;
+      s_list[pos++] = lane * 32 + b;
+    }
+    wave_lds_sync();
+    int32_t* out = a.ch_list + tile * (int64_t)a.c;
+    for (int i = lane; i < total; i += kWave) out[i] = s_list[i];
+  }
+
+  if (a.ag_mask != nullptr || a.tile_class != nullptr) {
+    uint32_t part = 0u;
+    if (own) {
+      if (a.group_size == 16) {
+        part = ((acc & 0xffffu) ? 1u : 0u) << (2 * lane);
+        part |= ((acc >> 16) ? 1u : 0u) << (2 * lane + 1);
+      } else {
+        const int wpg = a.group_size / 32;
+        part = (acc != 0u ? 1u : 0u) << (lane / wpg);
+      }
+    }
+    for (int off = kWave / 2; off >= 1; off >>= 1) part |= __shfl_xor(part, off, kWave);
+    if (lane == 0) {
+      const uint32_t full = a.ngroups >= 32 ? 0xffffffffu : ((1u << a.ngroups) - 1u);
+      if (a.ag_mask != nullptr) a.ag_mask[tile] = (int32_t)part;
+      if (a.tile_class != nullptr) a.tile_class[tile] = part == 0u ? 0 : (part == full ? 2 : 1);
+    }
+  }
+}
+
+template <typename T, int VEC>
+int launch_pack_t(const PackArgs& a, hipStream_t stream) {
+  const int cpb = 4 / a.csplit;
+  const int64_t blocks = (a.total_chunks + cpb - 1) / cpb;
+  if (blocks == 0) return (int)hipSuccess;
+  const uintptr_t align = (uintptr_t)a.x;
+  const bool aligned = (align % (sizeof(T) * VEC)) == 0;
+  if (aligned) {
+    hipLaunchKernelGGL((k_pack<T, VEC, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((k_pack<T, VEC, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  }
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+int launch_pack_v(const PackArgs& a, hipStream_t stream) {
+  switch (a.vec) {
+    case 4: return launch_pack_t<T, 4>(a, stream);
+    case 2: return launch_pack_t<T, 2>(a, stream);
+    default: return launch_pack_t<T, 1>(a, stream);
+  }
+}
+
+}  // namespace
+
+int words_per_pixel(int c) {
+  int w = (c + 31) / 32;
+  int p = 1;
+  while (p < w) p <<= 1;
+  return p;
+}
+
+PackPlan make_pack_plan(int64_t n, int c, int h, int w) {
+  PackPlan pl{};
+  const int hw = h * w;
+  pl.cwp = words_per_pixel(c);
+  // Widest vector that divides the plane (so every lane's pixels are valid),
+  // narrowed while the launch would leave CUs idle.
+  const int64_t want_waves = 4096;
+  int vec = (hw % 4 == 0) ? 4 : ((hw % 2 == 0) ? 2 : 1);
+  auto waves_for = [&](int v, int cs) {
+    const int64_t cpf = (hw + 64 * v - 1) / (64 * v);
+    return n * cpf * cs;
+  };
+  while (vec > 1 && waves_for(vec, 1) < want_waves) vec >>= 1;
+  int csplit = 1;
+  while (csplit < 4 && csplit < pl.cwp && waves_for(vec, csplit) < want_waves) csplit <<= 1;
+  pl.vec = vec;
+  pl.chunk = 64 * vec;
+  pl.csplit = csplit;
+  pl.chunks_per_frame = (hw + pl.chunk - 1) / pl.chunk;
+  pl.total_chunks = n * pl.chunks_per_frame;
+  return pl;
+}
+
+int launch_pack(const PackArgs& a, int dtype, hipStream_t stream) {
+  timing_begin(K_PACK, stream);
+  int rc;
+  switch (dtype) {
+    case SF_F16: rc = launch_pack_v<__half>(a, stream); break;
+    case SF_BF16: rc = launch_pack_v<__hip_bfloat16>(a, stream); break;
+    default: rc = launch_pack_v<float>(a, stream); break;
+  }
+  timing_end(K_PACK, stream);
+  return rc;
+}
+
+int launch_tiles(const TilesArgs& a, hipStream_t stream) {
+  const int64_t blocks = (a.ntiles + 3) / 4;
+  if (blocks == 0) return (int)hipSuccess;
+  const size_t lds = (a.ch_list != nullptr) ? (size_t)4 * a.c * sizeof(int32_t) : 0;
+  timing_begin(K_TILES, stream);
+  hipLaunchKernelGGL(k_tiles, dim3((unsigned)blocks), dim3(256), lds, stream, a);
+  const int rc = (int)hipGetLastError();
+  timing_end(K_TILES, stream);
+  return rc;
+}
+
+}  // namespace sf

@@ -1,0 +1,122 @@
+"""The C-ABI library: loads, exports the header, host utilities (CPU only).
+
+No call here launches a kernel: only host-side functions and argument
+validation paths that return before touching the device.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from sparseflow_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "sparseflow.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = header_functions()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in sparseflow.h but not exported"
+        assert name in _lib.EXPORTS, f"{name} has no ctypes signature in _lib.EXPORTS"
+    assert set(_lib.EXPORTS) == set(names)
+
+
+def test_version_and_empty_error():
+    assert _lib.version() == 100
+    assert isinstance(_lib.lib().sf_last_error(), bytes)
+
+
+@pytest.mark.parametrize("thr", [1e-6, 0.0, 5e-7, 1e-3, 0.3, 1.0, 65504.0, 1e-9, -1.0, 2.0 ** -25])
+def test_activity_cutoff_matches_fp16_semantics(thr):
+    c = _lib.activity_cutoff(thr)
+    # Oracle: |v| is active iff fp16(|v|) > fp16(thr).  Check around c.
+    probes = np.array([c, np.nextafter(np.float32(c), np.float32(0)), np.nextafter(np.float32(c), np.float32(np.inf)),
+                       0.0, 1e-9, 1e-6, 1.0, 7e4], dtype=np.float32)
+    with np.errstate(over="ignore"):
+        want = np.abs(probes.astype(np.float16)) > np.float16(thr)
+    got = np.abs(probes) >= np.float32(c)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_activity_cutoff_special_values():
+    assert np.isnan(_lib.activity_cutoff(float("nan")))
+    assert np.isnan(_lib.activity_cutoff(float("inf")))
+    assert _lib.activity_cutoff(-0.5) == 0.0
+    # f16(1e-6) = 17 * 2^-24; the boundary to 18 * 2^-24 ties to even (18).
+    assert _lib.activity_cutoff(1e-6) == np.float32(17.5 * 2.0 ** -24)
+
+
+def test_words_per_pixel_and_sizes():
+    assert [_lib.words_per_pixel(c) for c in (1, 3, 32, 33, 64, 65, 96, 128, 256, 512, 2048)] == \
+        [1, 1, 1, 2, 2, 4, 4, 4, 8, 16, 64]
+    L = _lib.lib()
+    assert L.sf_prescan_bitmap_bytes(32, 64, 32, 32) == 32 * 1024 * 2 * 4
+    chunk = _lib.chunk_pixels(32, 64, 32, 32)
+    assert chunk in (64, 128, 256)
+    assert L.sf_prescan_flags_bytes(32, 64, 32, 32) == 32 * (-(-1024 // chunk)) * 4
+    d = _lib.conv_desc(32, 64, 32, 32, 64, 32, 32, 3, 1, 1, 0, 0)
+    ws = _lib.conv2d_workspace_size(d)
+    assert ws >= L.sf_prescan_bitmap_bytes(32, 64, 32, 32) + L.sf_prescan_flags_bytes(32, 64, 32, 32)
+    assert ws % 256 == 0
+    assert _lib.conv_lif_workspace_size(d, 4) == _lib.conv2d_workspace_size(
+        _lib.conv_desc(128, 64, 32, 32, 64, 32, 32, 3, 1, 1, 0, 0))
+
+
+def _status(fn, *args):
+    return int(fn(*args))
+
+
+def test_validation_rejects_bad_descriptors_without_touching_the_device():
+    L = _lib.lib()
+    dummy = ctypes.c_void_p(16)
+    bad_pattern = _lib.conv_desc(1, 8, 8, 8, 8, 8, 8, 5, 1, 2, 0, 0)
+    assert _status(L.sf_conv2d_sparse, ctypes.byref(bad_pattern), dummy, dummy, dummy, dummy, None, dummy, None) \
+        == _lib.SF_ERR_UNSUPPORTED
+    assert b"supported patterns" in L.sf_last_error()
+    wrong_out = _lib.conv_desc(1, 8, 8, 8, 8, 7, 8, 3, 1, 1, 0, 0)
+    assert _status(L.sf_conv2d_sparse, ctypes.byref(wrong_out), dummy, dummy, dummy, dummy, None, dummy, None) \
+        == _lib.SF_ERR_INVALID
+    bad_dtype = _lib.conv_desc(1, 8, 8, 8, 8, 8, 8, 3, 1, 1, 7, 0)
+    assert _status(L.sf_conv2d_sparse, ctypes.byref(bad_dtype), dummy, dummy, dummy, dummy, None, dummy, None) \
+        == _lib.SF_ERR_INVALID
+    mixed = _lib.conv_desc(1, 8, 8, 8, 8, 8, 8, 3, 1, 1, 0, 1)  # f32 in -> f16 out
+    assert _status(L.sf_conv2d_sparse, ctypes.byref(mixed), dummy, dummy, dummy, dummy, None, dummy, None) \
+        == _lib.SF_ERR_UNSUPPORTED
+    too_wide = _lib.conv_desc(1, 4096, 8, 8, 8, 8, 8, 3, 1, 1, 0, 0)
+    assert _status(L.sf_conv2d_sparse, ctypes.byref(too_wide), dummy, dummy, dummy, dummy, None, dummy, None) \
+        == _lib.SF_ERR_UNSUPPORTED
+    ok = _lib.conv_desc(1, 8, 8, 8, 8, 8, 8, 3, 1, 1, 0, 0)
+    assert _status(L.sf_conv2d_sparse, ctypes.byref(ok), None, dummy, dummy, dummy, None, dummy, None) \
+        == _lib.SF_ERR_INVALID
+    assert _status(L.sf_conv2d_forward, ctypes.byref(ok), dummy, dummy, None, 1e-6, dummy, 16, dummy, None) \
+        == _lib.SF_ERR_WORKSPACE
+    # Fused conv-LIF: stride 2 unsupported, T < 1 invalid.
+    s2 = _lib.conv_desc(1, 8, 8, 8, 8, 4, 4, 3, 2, 1, 0, 0)
+    lif = _lib.LifParams(2.0, 1.0, 0.0, 1, 1)
+    assert _status(L.sf_conv_lif_forward, ctypes.byref(s2), 2, dummy, dummy, None, ctypes.byref(lif), 1e-6, None,
+                   dummy, dummy, dummy, 1 << 20, None) == _lib.SF_ERR_UNSUPPORTED
+    assert _status(L.sf_conv_lif_forward, ctypes.byref(ok), 0, dummy, dummy, None, ctypes.byref(lif), 1e-6, None,
+                   dummy, dummy, dummy, 1 << 20, None) == _lib.SF_ERR_INVALID
+    # Tiles: group size must be a power of two >= 16; kernel < stride rejected.
+    assert _status(L.sf_prescan_tiles, dummy, 1, 8, 8, 8, 8, 8, 3, 1, 1, 8, 8, 12, None, None, None, dummy, None,
+                   None) == _lib.SF_ERR_UNSUPPORTED
+    assert _status(L.sf_prescan_tiles, dummy, 1, 8, 8, 8, 4, 4, 1, 2, 0, 8, 8, 16, None, None, None, dummy, None,
+                   None) == _lib.SF_ERR_UNSUPPORTED
+
+
+def test_zero_frames_is_a_noop():
+    L = _lib.lib()
+    empty = _lib.conv_desc(0, 8, 8, 8, 8, 8, 8, 3, 1, 1, 0, 0)
+    assert _status(L.sf_conv2d_sparse, ctypes.byref(empty), None, None, None, None, None, None, None) == _lib.SF_OK
+    assert _status(L.sf_prescan_pack, None, 0, 0, 8, 8, 8, 1e-6, None, None, None) == _lib.SF_OK
