@@ -95,6 +95,21 @@ int check_desc(const sf_conv_desc* d, bool allow_k1s2 = true) {
   if (sf::words_per_pixel(d->c_in) > 64) return fail(SF_ERR_UNSUPPORTED, "c_in > 2048");
   if ((int64_t)d->h_in * d->w_in > (1 << 30) || (int64_t)d->c_in * d->kernel * d->kernel * d->c_out > (1ll << 31) - 1)
     return fail(SF_ERR_UNSUPPORTED, "tensor too large for 32-bit in-frame offsets");
+  // The per-wavefront entry list must hold a pixel's worst case in LDS.
+  sf::ConvArgs g{};
+  g.c_in = d->c_in;
+  g.h_in = d->h_in;
+  g.w_in = d->w_in;
+  g.c_out = d->c_out;
+  g.h_out = d->h_out;
+  g.w_out = d->w_out;
+  g.k = d->kernel;
+  g.cwp = sf::words_per_pixel(d->c_in);
+  sf::conv_geometry(g, true);
+  const int lif_lds = g.wave_lds;
+  sf::conv_geometry(g, false);
+  if (g.wave_lds > sf::kMaxLdsBytes || lif_lds > sf::kMaxLdsBytes)
+    return fail(SF_ERR_UNSUPPORTED, "c_in too wide for this kernel (per-wavefront LDS list exceeds 160 KB)");
   return SF_OK;
 }
 

@@ -39,22 +39,22 @@ def _check(spk, v, x, w, b, k, tau, v_th, v_reset, decay_input, v0=None):
 
 
 LIF_CASES = [
-    # (T, N, C, H, W, Co, k, density, tau, v_th, v_reset, decay_input, bias)
-    (4, 2, 64, 16, 16, 64, 3, 0.05, 2.0, 1.0, 0.0, True, True),
-    (6, 3, 32, 12, 10, 96, 3, 0.1, 1.5, 0.5, 0.0, False, False),
-    (5, 2, 48, 9, 9, 64, 3, 0.1, 2.0, 1.0, None, True, True),     # soft reset
-    (3, 2, 64, 10, 10, 130, 3, 0.05, 3.0, 0.8, -0.2, True, True),  # ragged C_out, v_reset != 0
-    (4, 2, 128, 14, 14, 64, 1, 0.05, 2.0, 1.0, 0.0, True, True),   # 1x1
+    # (T, N, C, H, W, Co, k, density, tau, v_th, v_reset, decay_input, bias, weight gain)
+    (4, 2, 64, 16, 16, 64, 3, 0.05, 2.0, 1.0, 0.0, True, True, 1.0),
+    (6, 3, 32, 12, 10, 96, 3, 0.1, 1.5, 0.5, 0.0, False, False, 1.0),
+    (5, 2, 48, 9, 9, 64, 3, 0.1, 2.0, 1.0, None, True, True, 1.0),     # soft reset
+    (3, 2, 64, 10, 10, 130, 3, 0.05, 3.0, 0.8, -0.2, True, True, 4.0),  # ragged C_out, v_reset != 0
+    (4, 2, 128, 14, 14, 64, 1, 0.05, 2.0, 1.0, 0.0, True, True, 3.0),   # 1x1
 ]
 
 
 @pytest.mark.parametrize("case", LIF_CASES)
 def test_fused_lif_matches_oracle(case):
-    T, N, C, H, W, Co, k, dens, tau, v_th, v_reset, decay_input, has_b = case
+    T, N, C, H, W, Co, k, dens, tau, v_th, v_reset, decay_input, has_b, gain = case
     announce(f"lif {case}")
     x = spikes((T, N, C, H, W), dens, seed=T * 100 + C)
     g = torch.Generator().manual_seed(C)
-    w = torch.randn(Co, C, k, k, generator=g) * (4.0 / (C * k * k)) ** 0.5
+    w = torch.randn(Co, C, k, k, generator=g) * (4.0 / (C * k * k)) ** 0.5 * gain
     b = torch.randn(Co, generator=g) * 0.2 if has_b else None
     spk, v, _ = sparse_fused_conv_lif_multistep(x.to(DEV), w.to(DEV), None if b is None else b.to(DEV), tau=tau,
                                                 v_threshold=v_th, v_reset=v_reset, decay_input=decay_input,
