@@ -93,8 +93,11 @@ int check_desc(const sf_conv_desc* d, bool allow_k1s2 = true) {
   const int wo = (d->w_in + 2 * d->pad - d->kernel) / d->stride + 1;
   if (ho != d->h_out || wo != d->w_out) return fail(SF_ERR_INVALID, "h_out/w_out do not match the conv geometry");
   if (sf::words_per_pixel(d->c_in) > 64) return fail(SF_ERR_UNSUPPORTED, "c_in > 2048");
-  if ((int64_t)d->h_in * d->w_in > (1 << 30) || (int64_t)d->c_in * d->kernel * d->kernel * d->c_out > (1ll << 31) - 1)
+  if ((int64_t)d->h_in * d->w_in > (1 << 30))
     return fail(SF_ERR_UNSUPPORTED, "tensor too large for 32-bit in-frame offsets");
+  // Stage-2 list entries pack a weight-row byte offset into 26 bits.
+  if ((int64_t)d->c_in * d->kernel * d->kernel * d->c_out * 4 > (1ll << 26))
+    return fail(SF_ERR_UNSUPPORTED, "weights larger than 64 MiB");
   // The per-wavefront entry list must hold a pixel's worst case in LDS.
   sf::ConvArgs g{};
   g.c_in = d->c_in;

@@ -6,40 +6,45 @@
 // NCHW) and produces every output channel for them.
 //
 //   Phase A (lane = pixel).  Each lane reads the bitmap words of its k*k
-//     receptive-field pixels, counts active (ci, kh, kw) taps, and after a
-//     wavefront prefix sum writes one entry per active tap -- the element
-//     offset of weight row (ci*k + kh)*k + kw -- into a per-wavefront LDS
-//     list.  Entries of a pixel are contiguous and ascending in (kh, kw, ci).
-//     Chunks flagged non-binary also store the activation value.
-//   Phase B (lane = output channel).  For each pixel in turn the wavefront
-//     walks that pixel's entries and adds the weight rows (binary spikes: the
-//     product is the weight itself) or FMAs value * weight, starting from the
-//     bias.  Results go through an LDS stage so the NCHW stores are
-//     contiguous runs per channel.
+//     receptive-field pixels and counts its active (ci, kh, kw) taps; a
+//     wavefront prefix sum places every pixel's entries, and each lane then
+//     writes one entry per active tap -- the byte offset of weight row
+//     (ci*k + kh)*k + kw and its pixel slot, packed as offset << 6 | slot --
+//     into a per-wavefront LDS list.  The list is sorted by pixel, and by
+//     (kh, kw, ci) within a pixel.
+//   Phase B (lane = output channel).  The wavefront walks the list linearly
+//     in blocks of 16 entries held in scalar registers: 16 independent
+//     weight-row buffer loads are issued before any is consumed, then summed
+//     in list order into a running per-pixel accumulator (restarting from the
+//     bias at each pixel) that is parked in the pixel's LDS stage slot.  Binary spikes add the weight
+//     itself; chunks flagged non-binary FMA value * weight, the value read
+//     from x.  The stage is then written out transposed (lane = pixel), so
+//     NCHW stores are contiguous runs per channel.
 //
-// No atomics: every output element is summed by one wavefront in a fixed
-// order, so results are deterministic.  This replaces the reference's
-// per-tile grouped tl.dot kernels (Kernels/conv2d.py:237-361, 364-460,
-// 564-886) and the fused conv-LIF kernels (Kernels/fused_conv_lif.py:63-303).
+// Every output element is bias + its taps summed by one wavefront in a fixed
+// order: results are deterministic and identical from run to run.  No
+// atomics.  This
+// replaces the reference's per-tile grouped tl.dot kernels
+// (Kernels/conv2d.py:237-361, 364-460, 564-886) and the fused conv-LIF kernels
+// (Kernels/fused_conv_lif.py:63-303).
 #include "sf_internal.h"
 
 namespace sf {
 
 namespace {
 
-// Per-wavefront LDS layout: [cap] int32 entries | [cap] f32 values | stage.
+constexpr int kBlock = 16;  // weight-row loads in flight per wavefront
+
 struct WaveLds {
-  int32_t* list;
-  float* vals;
-  float* stage;
+  int32_t* list;  // [cap] packed entries
+  float* stage;   // [64 channels][ld] per-pixel results
 };
 
 __device__ __forceinline__ WaveLds wave_lds(char* smem, const ConvArgs& a, int wave) {
   char* base = smem + (size_t)wave * a.wave_lds;
   WaveLds w;
   w.list = reinterpret_cast<int32_t*>(base);
-  w.vals = reinterpret_cast<float*>(base + (size_t)a.cap * 4);
-  w.stage = reinterpret_cast<float*>(base + (size_t)a.cap * 8);
+  w.stage = reinterpret_cast<float*>(base + (size_t)a.cap * 4);
   return w;
 }
 
@@ -81,9 +86,9 @@ __device__ __forceinline__ int count_taps(const ConvArgs& a, const uint32_t* fb,
 }
 
 // Phase A, pass 2: write this lane's entries starting at list[pos].
-template <int K, typename TIn>
-__device__ __forceinline__ void decode_taps(const ConvArgs& a, const uint32_t* fb, const TIn* xf, int oh, int ow,
-                                            int pos, bool value_path, const WaveLds& w) {
+template <int K>
+__device__ __forceinline__ void decode_taps(const ConvArgs& a, const uint32_t* fb, int oh, int ow, int slot, int pos,
+                                            int32_t* list) {
 #pragma unroll
   for (int kh = 0; kh < K; ++kh) {
     const int ih = oh * a.s - a.p + kh;
@@ -92,18 +97,14 @@ __device__ __forceinline__ void decode_taps(const ConvArgs& a, const uint32_t* f
     for (int kw = 0; kw < K; ++kw) {
       const int iw = ow * a.s - a.p + kw;
       if (iw < 0 || iw >= a.w_in) continue;
-      const int64_t pin = (int64_t)ih * a.w_in + iw;
-      const uint32_t* wp = fb + pin * a.cwp;
+      const uint32_t* wp = fb + ((int64_t)ih * a.w_in + iw) * a.cwp;
       for (int cw = 0; cw < a.cwp; ++cw) {
         uint32_t wd = wp[cw];
         while (wd != 0u) {
           const int b = __builtin_ctz(wd);
           wd &= wd - 1u;
-          const int ci = cw * 32 + b;
-          if (pos < a.cap) {
-            w.list[pos] = ((ci * K + kh) * K + kw) * a.c_out;
-            if (value_path) w.vals[pos] = to_f32<TIn>(xf[(int64_t)ci * a.hw_in + pin]);
-          }
+          const uint32_t row = (uint32_t)(((cw * 32 + b) * K + kh) * K + kw);
+          if (pos < a.cap) list[pos] = (int32_t)(((row * (uint32_t)a.c_out * 4u) << 6) | (uint32_t)slot);
           ++pos;
         }
       }
@@ -111,49 +112,97 @@ __device__ __forceinline__ void decode_taps(const ConvArgs& a, const uint32_t* f
   }
 }
 
-// Phase B inner loop: acc[j] (+)= sum over entries [st, st+ct) of the weight
-// rows at output channel co_j, in entry order.
-template <int CPL, bool VALUE>
-__device__ __forceinline__ void accumulate(const ConvArgs& a, const WaveLds& w, int st, int ct, int c0, int lane,
-                                           float (&acc)[CPL]) {
-  const int32_t* lp = w.list + st;
-  const float* vp = w.vals + st;
-  const float* wt = a.wt;
-  bool co_ok[CPL];
-  int co[CPL];
+// Buffer resource over the weight matrix: raw (stride 0) dword loads, so a
+// weight-row load is one buffer_load with the row's byte offset in soffset
+// (scalar) and the lane's column offset in voffset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const ConvArgs& a) {
+  const int bytes = a.c_in * a.k * a.k * a.c_out * 4;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.wt), (short)0, bytes, 0x00020000);
+}
+
+// Phase B: sum the weight rows of list entries [i0, i1) (sorted by slot) for
+// output channels co[j] into the LDS stage: stage_row[j][slot] ends as the
+// bias plus the slot's entries in list ((kh, kw, ci)) order.  The caller
+// initialises the stage with the bias for slots without entries.
+// Entries are read in blocks of 16 into scalar registers and all 16
+// weight-row loads are issued before the first is consumed; pixel (slot)
+// changes are uniform scalar branches, so the per-entry vector work is one
+// add per output channel.  Out-of-range channels read a clamped in-bounds
+// column whose result is never stored.  pin_base (per lane = slot) is the
+// flat input index of the slot's receptive-field origin (value path only).
+// One block of up to kBlock entries starting at list[ib]; FULL blocks have
+// exactly kBlock entries (no tail handling).  State (acc, cur) carries over.
+template <int K, int CPL, bool VALUE, bool FULL, typename TIn>
+__device__ __forceinline__ void walk_block(const ConvArgs& a, const __amdgpu_buffer_rsrc_t& wr, const int32_t* list,
+                                           int ib, int n, const int (&col_bytes)[CPL], const float (&bias)[CPL],
+                                           float* const (&stage_row)[CPL], const TIn* xf, int pin_base,
+                                           float (&acc)[CPL], int& cur) {
+  int ent[kBlock];
+#pragma unroll
+  for (int q = 0; q < kBlock; ++q) ent[q] = __builtin_amdgcn_readfirstlane(list[ib + (FULL ? q : min(q, n - 1))]);
+  float wv[kBlock][CPL];
+#pragma unroll
+  for (int q = 0; q < kBlock; ++q) {
+    const int off = (int)((uint32_t)ent[q] >> 6);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      wv[q][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(wr, col_bytes[j], off, 0));
+  }
+  float xv[kBlock];
+  if (VALUE) {
+#pragma unroll
+    for (int q = 0; q < kBlock; ++q) {
+      const int row = (int)(((uint32_t)ent[q] >> 6) / ((uint32_t)a.c_out * 4u));
+      const int slot = ent[q] & 63;
+      const int ci = row / (K * K);
+      const int tap = row - ci * (K * K);
+      const int kh = tap / K;
+      const int kw = tap - kh * K;
+      const int pin = __builtin_amdgcn_readlane(pin_base, slot) + kh * a.w_in + kw;
+      xv[q] = to_f32<TIn>(xf[(int64_t)ci * a.hw_in + pin]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < kBlock; ++q) {
+    if (FULL || q < n) {
+      const int slot = ent[q] & 63;
+      if (slot != cur) {
+        if (cur >= 0) {
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) stage_row[j][cur] = acc[j];
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc[j] = bias[j];
+        cur = slot;
+      }
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) acc[j] = VALUE ? fmaf(xv[q], wv[q][j], acc[j]) : acc[j] + wv[q][j];
+    }
+  }
+}
+
+template <int K, int CPL, bool VALUE, typename TIn>
+__device__ __forceinline__ void walk_entries(const ConvArgs& a, const int32_t* list, int i0, int i1,
+                                             const int (&co_eff)[CPL], const float (&bias)[CPL],
+                                             float* const (&stage_row)[CPL], const TIn* xf, int pin_base) {
+  const __amdgpu_buffer_rsrc_t wr = weight_rsrc(a);
+  int col_bytes[CPL];
+  float acc[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    co[j] = c0 + lane + 64 * j;
-    co_ok[j] = co[j] < a.c_out;
+    col_bytes[j] = co_eff[j] * 4;
+    acc[j] = bias[j];
   }
-  int k = 0;
-  for (; k + 8 <= ct; k += 8) {
-    int r[8];
-    float v[8];
+  int cur = -1;
+  int ib = i0;
+  for (; ib + kBlock <= i1; ib += kBlock)
+    walk_block<K, CPL, VALUE, true, TIn>(a, wr, list, ib, kBlock, col_bytes, bias, stage_row, xf, pin_base, acc, cur);
+  if (ib < i1)
+    walk_block<K, CPL, VALUE, false, TIn>(a, wr, list, ib, i1 - ib, col_bytes, bias, stage_row, xf, pin_base, acc,
+                                          cur);
+  if (cur >= 0) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) r[q] = lp[k + q];
-    if (VALUE) {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) v[q] = vp[k + q];
-    }
-    float wv[8][CPL];
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) wv[q][j] = co_ok[j] ? wt[r[q] + co[j]] : 0.f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) acc[j] = VALUE ? fmaf(v[q], wv[q][j], acc[j]) : acc[j] + wv[q][j];
-  }
-  for (; k < ct; ++k) {
-    const int r = lp[k];
-    const float v = VALUE ? vp[k] : 1.f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const float wv = co_ok[j] ? wt[r + co[j]] : 0.f;
-      acc[j] = VALUE ? fmaf(v, wv, acc[j]) : acc[j] + wv;
-    }
+    for (int j = 0; j < CPL; ++j) stage_row[j][cur] = acc[j];
   }
 }
 
@@ -165,7 +214,8 @@ __global__ __launch_bounds__(256) void k_conv_gather(ConvArgs a) {
   const int64_t gidx = (int64_t)blockIdx.x * a.waves_per_block + wave;
   if (gidx >= a.total_groups) return;  // wavefronts never wait on each other
   const WaveLds w = wave_lds(smem, a, wave);
-  const int flp = a.fl + 1;
+  constexpr int LD = 33;  // stage row stride (32 pixel slots + 1 pad word)
+  constexpr int CH = 64 * CPL;
 
   const int64_t frame = gidx / a.groups_per_frame;
   const int g = (int)(gidx - frame * a.groups_per_frame);
@@ -175,6 +225,7 @@ __global__ __launch_bounds__(256) void k_conv_gather(ConvArgs a) {
   const bool pvalid = lane < nvalid;
   const int oh = pix / a.w_out;
   const int ow = pix - oh * a.w_out;
+  const int pin_base = (oh * a.s - a.p) * a.w_in + (ow * a.s - a.p);
 
   const bool value_path = group_value_path<K>(a, frame, pix0, nvalid);
   const uint32_t* fb = a.bits + frame * (int64_t)a.hw_in * a.cwp;
@@ -192,48 +243,47 @@ __global__ __launch_bounds__(256) void k_conv_gather(ConvArgs a) {
     const uint64_t fit = __ballot(lane >= s && lane < nvalid && (incl - base) <= a.cap);
     int e = s + __popcll(fit);
     if (e == s) e = s + 1;
-    if (lane >= s && lane < e) decode_taps<K, TIn>(a, fb, xf, oh, ow, excl - base, value_path, w);
+    if (lane >= s && lane < e) decode_taps<K>(a, fb, oh, ow, lane, excl - base, w.list);
     wave_lds_sync();
 
-    for (int c0 = 0; c0 < a.c_out; c0 += 64 * CPL) {
+    for (int c0 = 0; c0 < a.c_out; c0 += CH) {
+      int co_eff[CPL];
       float bias[CPL];
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const int co = c0 + lane + 64 * j;
+        co_eff[j] = min(co, a.c_out - 1);
         bias[j] = (a.bias != nullptr && co < a.c_out) ? a.bias[co] : 0.f;
       }
-      int fs = s;
-      for (int p = s; p < e; ++p) {
-        const int st = __builtin_amdgcn_readlane(excl, p) - base;
-        const int ct = min(__builtin_amdgcn_readlane(cnt, p), a.cap - st);
-        float acc[CPL];
+      // Halves of 32 pixel slots share one stage.
+      for (int h0 = s; h0 < e;) {
+        const int sb = h0 & ~31;
+        const int h1 = min(e, sb + 32);
+        const int i0 = (h0 > 0 ? __builtin_amdgcn_readlane(incl, h0 - 1) : 0) - base;
+        const int i1 = min(__builtin_amdgcn_readlane(incl, h1 - 1) - base, a.cap);
+        float* stage_row[CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] = bias[j];
+        for (int j = 0; j < CPL; ++j) {
+          stage_row[j] = w.stage + (lane + 64 * j) * LD - sb;
+          for (int p = h0; p < h1; ++p) stage_row[j][p] = bias[j];
+        }
         if (value_path) {
-          accumulate<CPL, true>(a, w, st, ct, c0, lane, acc);
+          walk_entries<K, CPL, true, TIn>(a, w.list, i0, i1, co_eff, bias, stage_row, xf, pin_base);
         } else {
-          accumulate<CPL, false>(a, w, st, ct, c0, lane, acc);
+          walk_entries<K, CPL, false, TIn>(a, w.list, i0, i1, co_eff, bias, stage_row, xf, pin_base);
         }
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) w.stage[(lane + 64 * j) * flp + (p - fs)] = acc[j];
-        if (p - fs == a.fl - 1 || p == e - 1) {
-          wave_lds_sync();
-          const int m = p - fs + 1;
-          const int rows_per = kWave / a.fl;
-          const int ro = lane / a.fl;
-          const int px = lane - ro * a.fl;
-          if (px < m) {
-            for (int r = ro; r < 64 * CPL; r += rows_per) {
-              const int co = c0 + r;
-              if (co < a.c_out) yf[(int64_t)co * a.hw_out + fs + px] = from_f32<TOut>(w.stage[r * flp + px]);
-            }
+        wave_lds_sync();
+        // Transposed store: lanes 0-31 write channel r, lanes 32-63 channel r+1.
+        const int px = sb + (lane & 31);
+        if (px >= h0 && px < h1) {
+          for (int r = lane >> 5; r < CH; r += 2) {
+            if (c0 + r < a.c_out) yf[(int64_t)(c0 + r) * a.hw_out + px] = from_f32<TOut>(w.stage[r * LD + (px - sb)]);
           }
-          wave_lds_sync();
-          fs = p + 1;
         }
+        wave_lds_sync();
+        h0 = h1;
       }
     }
-    wave_lds_sync();
     s = e;
   }
 }
@@ -250,7 +300,7 @@ __global__ __launch_bounds__(256) void k_conv_lif(ConvArgs a) {
   const int64_t widx = (int64_t)blockIdx.x * a.waves_per_block + wave;
   if (widx >= a.total_groups * nco) return;
   const WaveLds w = wave_lds(smem, a, wave);
-  constexpr int FLP = 65;
+  constexpr int LD = 65;
 
   const int64_t gidx = widx / nco;
   const int cb = (int)(widx - gidx * nco) * 64;
@@ -262,6 +312,7 @@ __global__ __launch_bounds__(256) void k_conv_lif(ConvArgs a) {
   const bool pvalid = lane < nvalid;
   const int oh = pix / a.w_out;
   const int ow = pix - oh * a.w_out;
+  const int pin_base = (oh * a.s - a.p) * a.w_in + (ow * a.s - a.p);
 
   float v[64];
 #pragma unroll
@@ -271,8 +322,11 @@ __global__ __launch_bounds__(256) void k_conv_lif(ConvArgs a) {
                ? a.v_init[(n * a.c_out + co) * (int64_t)a.hw_out + pix]
                : 0.f;
   }
-  const float bias = (a.bias != nullptr && cb + lane < a.c_out) ? a.bias[cb + lane] : 0.f;
+  const int co = cb + lane;
+  const int co_eff[1] = {min(co, a.c_out - 1)};
+  const float bias[1] = {(a.bias != nullptr && co < a.c_out) ? a.bias[co] : 0.f};
   const float tau = a.tau, vth = a.v_th, vr = a.hard_reset ? a.v_reset : 0.f;
+  float* const stage_row[1] = {w.stage + lane * LD};
 
   for (int t = 0; t < a.T; ++t) {
     const int64_t frame = (int64_t)t * a.n + n;
@@ -284,24 +338,20 @@ __global__ __launch_bounds__(256) void k_conv_lif(ConvArgs a) {
     const int incl = wave_inclusive_scan(cnt);
     const int excl = incl - cnt;
 
+    for (int p = 0; p < nvalid; ++p) stage_row[0][p] = bias[0];
     int s = 0;
     while (s < nvalid) {
       const int base = s > 0 ? __builtin_amdgcn_readlane(incl, s - 1) : 0;
       const uint64_t fit = __ballot(lane >= s && lane < nvalid && (incl - base) <= a.cap);
       int e = s + __popcll(fit);
       if (e == s) e = s + 1;
-      if (lane >= s && lane < e) decode_taps<K, TIn>(a, fb, xf, oh, ow, excl - base, value_path, w);
+      if (lane >= s && lane < e) decode_taps<K>(a, fb, oh, ow, lane, excl - base, w.list);
       wave_lds_sync();
-      for (int p = s; p < e; ++p) {
-        const int st = __builtin_amdgcn_readlane(excl, p) - base;
-        const int ct = min(__builtin_amdgcn_readlane(cnt, p), a.cap - st);
-        float acc[1] = {bias};
-        if (value_path) {
-          accumulate<1, true>(a, w, st, ct, cb, lane, acc);
-        } else {
-          accumulate<1, false>(a, w, st, ct, cb, lane, acc);
-        }
-        w.stage[lane * FLP + p] = acc[0];
+      const int i1 = min(__builtin_amdgcn_readlane(incl, e - 1) - base, a.cap);
+      if (value_path) {
+        walk_entries<K, 1, true, TIn>(a, w.list, 0, i1, co_eff, bias, stage_row, xf, pin_base);
+      } else {
+        walk_entries<K, 1, false, TIn>(a, w.list, 0, i1, co_eff, bias, stage_row, xf, pin_base);
       }
       wave_lds_sync();
       s = e;
@@ -313,7 +363,7 @@ __global__ __launch_bounds__(256) void k_conv_lif(ConvArgs a) {
 #pragma unroll
     for (int c = 0; c < 64; ++c) {
       if (cb + c < a.c_out) {
-        const float cur = w.stage[c * FLP + lane];
+        const float cur = w.stage[c * LD + lane];
         const float vp = v[c];
         const float h = a.decay_input ? vp + (cur - (vp - vr)) / tau : (vp - (vp - vr) / tau) + cur;
         const bool spike = h >= vth;
@@ -348,12 +398,12 @@ int launch_conv_t(const ConvArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.waves_per_block * a.wave_lds;
   const dim3 grid((unsigned)blocks), block(64 * a.waves_per_block);
   const bool wide = a.c_out >= 128;
-#define SF_LAUNCH_CONV(KK, CC)                                        \
-  do {                                                                \
-    auto kern = k_conv_gather<TIn, TOut, KK, CC>;                     \
-    static bool attr_done = false;                                    \
-    if (!attr_done) { allow_full_lds(kern); attr_done = true; }       \
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, a);            \
+#define SF_LAUNCH_CONV(KK, CC)                                  \
+  do {                                                          \
+    auto kern = k_conv_gather<TIn, TOut, KK, CC>;               \
+    static bool attr_done = false;                              \
+    if (!attr_done) { allow_full_lds(kern); attr_done = true; } \
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, a);      \
   } while (0)
   if (a.k == 3) {
     if (wide) SF_LAUNCH_CONV(3, 2); else SF_LAUNCH_CONV(3, 1);
@@ -394,15 +444,25 @@ void conv_geometry(ConvArgs& a, bool lif) {
   a.groups_per_frame = (a.hw_out + kWave - 1) / kWave;
   // The list must hold the largest possible per-pixel entry count.
   const int per_pixel_max = a.k * a.k * a.cwp * 32;
-  a.cap = per_pixel_max > 512 ? per_pixel_max : 512;
-  const int cpl = (!lif && a.c_out >= 128) ? 2 : 1;
+  int cap = per_pixel_max > 1024 ? per_pixel_max : 1024;
+  a.cap = (cap + kBlock - 1) / kBlock * kBlock;
   a.fl = lif ? 64 : 32;
-  const int stage = 64 * cpl * (a.fl + 1) * 4;
-  a.wave_lds = ((a.cap * 8 + stage) + 15) / 16 * 16;
-  int wpb = kMaxLdsBytes / a.wave_lds;
-  if (wpb > 4) wpb = 4;
-  if (wpb < 1) wpb = 1;
-  a.waves_per_block = wpb;
+  const int cpl = (!lif && a.c_out >= 128) ? 2 : 1;
+  const int stage = 64 * cpl * (lif ? 65 : 33) * 4;
+  a.wave_lds = ((a.cap * 4 + stage) + 15) / 16 * 16;
+  // Blocks of up to 4 wavefronts; pick the size whose whole blocks keep the
+  // most wavefronts resident within one CU's LDS (ties -> larger blocks).
+  int per_cu = kMaxLdsBytes / a.wave_lds;
+  if (per_cu < 1) per_cu = 1;
+  int best = 1, best_res = per_cu;
+  for (int wpb = 2; wpb <= 4 && wpb <= per_cu; ++wpb) {
+    const int res = (per_cu / wpb) * wpb;
+    if (res >= best_res) {
+      best = wpb;
+      best_res = res;
+    }
+  }
+  a.waves_per_block = best;
 }
 
 int launch_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
