@@ -20,13 +20,17 @@ namespace sf {
 
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// x is streamed exactly once, so its loads are marked non-temporal.
 template <typename T, int VEC, bool ALIGNED>
 __device__ __forceinline__ void load_vec(const T* p, float (&v)[VEC]) {
   if constexpr (ALIGNED && VEC == 4 && sizeof(T) == 4) {
-    const float4 q = *reinterpret_cast<const float4*>(p);
+    const f32x4 q = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
     v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
   } else if constexpr (ALIGNED && VEC == 2 && sizeof(T) == 4) {
-    const float2 q = *reinterpret_cast<const float2*>(p);
+    const f32x2 q = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(p));
     v[0] = q.x; v[1] = q.y;
   } else if constexpr (ALIGNED && VEC == 4 && sizeof(T) == 2) {
     const uint2 q = *reinterpret_cast<const uint2*>(p);
@@ -254,17 +258,19 @@ PackPlan make_pack_plan(int64_t n, int c, int h, int w) {
   PackPlan pl{};
   const int hw = h * w;
   pl.cwp = words_per_pixel(c);
-  // Widest vector that divides the plane (so every lane's pixels are valid),
-  // narrowed while the launch would leave CUs idle.
-  const int64_t want_waves = 4096;
+  // Widest vector that divides the plane (so every lane's pixels are valid).
+  // Channel words are split across waves first (a wave then streams one or
+  // two words of 32 channels); the vector is narrowed only if the launch
+  // would still leave the chip short of waves.
+  const int64_t want_waves = 16384;
   int vec = (hw % 4 == 0) ? 4 : ((hw % 2 == 0) ? 2 : 1);
   auto waves_for = [&](int v, int cs) {
     const int64_t cpf = (hw + 64 * v - 1) / (64 * v);
     return n * cpf * cs;
   };
-  while (vec > 1 && waves_for(vec, 1) < want_waves) vec >>= 1;
   int csplit = 1;
-  while (csplit < 4 && csplit < pl.cwp && waves_for(vec, csplit) < want_waves) csplit <<= 1;
+  while (csplit < 4 && csplit < pl.cwp && (pl.cwp / csplit > 2 || waves_for(vec, csplit) < want_waves)) csplit <<= 1;
+  while (vec > 1 && waves_for(vec, csplit) < want_waves / 4) vec >>= 1;
   pl.vec = vec;
   pl.chunk = 64 * vec;
   pl.csplit = csplit;
