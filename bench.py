@@ -125,8 +125,8 @@ def bench_conv(name, steps, warmup, dev, with_miopen=True):
             dense = lambda: torch.nn.functional.conv2d(x, wd, None, s, (k - 1) // 2)  # noqa: E731
             miopen_ms = time_gpu(dense, max(5, steps // 2), 3)
     density = float(x.mean().item())
-    pack = kt.get("prescan_pack", (0, 0.0))[1]
-    convk = kt.get("conv_gather", (0, 0.0))[1]
+    kernels_us = {k2: v[1] * 1e3 for k2, v in kt.items()}
+    kernel_bytes = {k2: (x_bytes if k2.startswith("prescan") else y_bytes + w_bytes) for k2 in kt}
     res = {
         "workload": name,
         "us_per_layer": ms * 1e3,
@@ -136,8 +136,8 @@ def bench_conv(name, steps, warmup, dev, with_miopen=True):
         "hbm_frac": alg_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "alg_bytes": alg_bytes,
         "input_density": density,
-        "kernels_us": {"prescan_pack": pack * 1e3, "conv_gather": convk * 1e3},
-        "kernel_bytes": {"prescan_pack": x_bytes, "conv_gather": y_bytes + w_bytes},
+        "kernels_us": kernels_us,
+        "kernel_bytes": kernel_bytes,
         "miopen_us": None if miopen_ms is None else miopen_ms * 1e3,
         "speedup_vs_miopen": None if miopen_ms is None else miopen_ms / ms,
     }

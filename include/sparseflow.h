@@ -20,9 +20,10 @@
  *                                          (ci*k + kh)*k + kw holds w[:,ci,kh,kw]
  *   y       [n, c_out, h_out, w_out]       NCHW output, dtype = desc.out_dtype
  *
- * Determinism: every output element is produced by exactly one wavefront,
- * summing bias first and then active taps in ascending (kh, kw, ci) order.
- * Repeated calls on the same inputs are bit-identical.
+ * Determinism: every output element is produced by exactly one lane of one
+ * wavefront, summing bias first and then its active taps in an order fixed by
+ * the shape (no atomics).  Repeated calls on the same inputs are
+ * bit-identical.
  */
 #ifndef SPARSEFLOW_H
 #define SPARSEFLOW_H
@@ -130,7 +131,9 @@ int sf_prescan_tiles(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in,
 
 /* Sparse conv over a bitmap produced by sf_prescan_pack for the same x.
  * Binary chunks add weight rows; chunks flagged non-binary read x and FMA.
- * bias may be NULL.  Replaces sparse_conv3x3s1/s2 and conv1x1 NHWC kernels
+ * bias may be NULL.  3x3 stride-1 layers with c_in <= 64 on frames of width
+ * 32 or 56 run the row-tile scatter kernel ("conv_rows"); every other
+ * supported shape runs the gather kernel ("conv_gather").  Replaces sparse_conv3x3s1/s2 and conv1x1 NHWC kernels
  * (Kernels/conv2d.py:237-361,564-886) and the persistent fused 1x1 kernel
  * (Kernels/conv2d.py:364-460). */
 int sf_conv2d_sparse(const sf_conv_desc* desc, const uint32_t* bits,
@@ -161,7 +164,8 @@ int sf_conv_lif_forward(const sf_conv_desc* desc, int32_t T, const void* x,
 /* When enabled, every kernel launched by the library is bracketed by a
  * hipEvent pair on its stream.  sf_timing_collect synchronises those events
  * and accumulates per-kernel totals; sf_timing_query reads them by name
- * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif").  Returns the
+ * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_rows", "conv_lif").
+ * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);
 int sf_timing_collect(void);

@@ -190,9 +190,9 @@ struct TimingRec {
 std::mutex g_tmu;
 bool g_timing = false;
 std::vector<TimingRec> g_pending;
-double g_total_ms[sf::K_COUNT] = {0, 0, 0, 0};
-int64_t g_count[sf::K_COUNT] = {0, 0, 0, 0};
-const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif"};
+double g_total_ms[sf::K_COUNT] = {};
+int64_t g_count[sf::K_COUNT] = {};
+const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows"};
 
 }  // namespace
 
@@ -348,6 +348,11 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
   if (bits == nullptr || flags == nullptr || x == nullptr || wt == nullptr || y == nullptr)
     return fail(SF_ERR_INVALID, "NULL pointer");
   const sf::ConvArgs a = conv_args(d, d->n, bits, flags, x, wt, bias, y, false);
+  if (sf::rows_applicable(a)) {
+    rc = sf::launch_conv_rows(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
+    if (rc != hipSuccess) return hip_fail(rc, "conv_rows launch");
+    return SF_OK;
+  }
   rc = sf::launch_conv(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "conv_gather launch");
   return SF_OK;

@@ -87,13 +87,17 @@ int launch_tiles(const TilesArgs& a, hipStream_t stream);
 int launch_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 int launch_conv_lif(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Row-tile scatter Stage 2 (3x3 s1, C_in <= 64, frame width 32 or 56).
+bool rows_applicable(const ConvArgs& a);
+int launch_conv_rows(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
 
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_COUNT = 4 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_COUNT = 5 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

@@ -1,0 +1,251 @@
+// Stage 2, row-tile scatter formulation: 3x3 stride-1 convolutions whose
+// weights for 64 output channels fit in LDS (C_in <= 64) on frames of width
+// 32 or 56.
+//
+// One wavefront owns one output row of one frame for 64 output channels
+// (lane = output channel, one accumulator register per output pixel).  The
+// weights of the workgroup's 64-channel group stay in LDS for the whole
+// (persistent) launch.  The wavefront walks the spike bitmap of the three
+// input rows on the scalar unit: every active (ci, ih, iw) contributes weight
+// rows (ci, kh = ih - oh + 1, kw) to output columns iw + 1 - kw, and because
+// the input position is a compile-time loop index, every target accumulator
+// is a fixed register.  Each weight row is read from LDS at an immediate
+// offset.  The finished row is transposed in registers (DPP row shifts and
+// quad permutes) so that each store instruction writes whole frame rows of
+// 64/QP channels as float4 runs.
+//
+// Output element (co, oh, ow) = bias[co] + its taps summed by one lane in the
+// order (input row, input column, ci): deterministic from run to run.
+// Replaces the reference's sparse_conv3x3s1_nhwc_kernel_8x8/8x16
+// (Kernels/conv2d.py:564-724) for these shapes.
+#include "sf_internal.h"
+
+namespace sf {
+
+namespace {
+
+constexpr int kRowsWaves = 16;  // wavefronts per workgroup (one workgroup per CU)
+
+// Exchange lane bit S with quad-slot bit S over v[4 * QP] (a butterfly stage
+// of the register transpose).  Lanes with bit S set take the partner's upper
+// slot; lanes with it clear take the partner's lower slot.
+template <int S, int QP>
+__device__ __forceinline__ void butterfly(float (&v)[4 * QP], int lane) {
+#pragma unroll
+  for (int j = 0; j < QP; ++j) {
+    if (j & S) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int ai = __float_as_int(v[4 * j + e]);
+      const int bi = __float_as_int(v[4 * (j | S) + e]);
+      int na, nb;
+      if constexpr (S == 1 || S == 2) {
+        constexpr int qp = S == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+        const int pa = __builtin_amdgcn_mov_dpp(ai, qp, 0xf, 0xf, false);
+        const int pb = __builtin_amdgcn_mov_dpp(bi, qp, 0xf, 0xf, false);
+        const bool hi = (lane & S) != 0;
+        na = hi ? pb : ai;
+        nb = hi ? bi : pa;
+      } else {
+        // row_shl:S reads lane L+S, row_shr:S reads lane L-S; the bank mask
+        // restricts each to the lanes whose bit S is clear / set.
+        constexpr int shl = 0x100 | S, shr = 0x110 | S;
+        constexpr int lo_banks = S == 4 ? 0x5 : 0x3, hi_banks = S == 4 ? 0xa : 0xc;
+        nb = __builtin_amdgcn_update_dpp(bi, ai, shl, 0xf, lo_banks, false);
+        na = __builtin_amdgcn_update_dpp(ai, bi, shr, 0xf, hi_banks, false);
+      }
+      v[4 * j + e] = __int_as_float(na);
+      v[4 * (j | S) + e] = __int_as_float(nb);
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, float a, float b, float c, float d) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+  } else {
+    const T h0 = from_f32<T>(a), h1 = from_f32<T>(b), h2 = from_f32<T>(c), h3 = from_f32<T>(d);
+    uint16_t u0, u1, u2, u3;
+    __builtin_memcpy(&u0, &h0, 2);
+    __builtin_memcpy(&u1, &h1, 2);
+    __builtin_memcpy(&u2, &h2, 2);
+    __builtin_memcpy(&u3, &h3, 2);
+    *reinterpret_cast<uint2*>(p) = make_uint2((uint32_t)u0 | ((uint32_t)u1 << 16), (uint32_t)u2 | ((uint32_t)u3 << 16));
+  }
+}
+
+// Bitmap word type: both channel words of a pixel as one 64-bit value when
+// the bitmap has two words per pixel.
+template <int CWP> struct Word;
+template <> struct Word<1> { typedef uint32_t type; };
+template <> struct Word<2> { typedef uint64_t type; };
+
+template <typename M>
+__device__ __forceinline__ int lowest_bit(M m) {
+  if constexpr (sizeof(M) == 8) return __builtin_ctzll(m);
+  else return __builtin_ctz(m);
+}
+
+// Accumulate the spikes of input row ih (= oh - 1 + IA) into acc.
+template <int W, int QP, int CWP, int IA, bool VALUE, typename TIn>
+__device__ __forceinline__ void scatter_row(float (&acc)[4 * QP], const typename Word<CWP>::type* __restrict__ rp,
+                                            const char* wlb, const TIn* __restrict__ xrow, int hw_in) {
+  typedef typename Word<CWP>::type M;
+  constexpr int CH = 8;  // positions per scalar-load batch
+#pragma unroll
+  for (int ib0 = 0; ib0 < W; ib0 += CH) {
+    M mw[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) mw[u] = rp[ib0 + u];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int ib = ib0 + u;
+      M m = mw[u];
+      while (m) {
+        const int ci = lowest_bit(m);
+        m &= m - 1;
+        const char* base = wlb + (ci * 9 + IA * 3) * 256;
+        float xv = 1.f;
+        if constexpr (VALUE) xv = to_f32<TIn>(xrow[(size_t)ci * hw_in + ib]);
+#pragma unroll
+        for (int kw = 0; kw < 3; ++kw) {
+          const int x = ib + 1 - kw;
+          if (x < 0 || x >= W) continue;
+          const float wv = *reinterpret_cast<const float*>(base + kw * 256);
+          if constexpr (VALUE) acc[x] = fmaf(xv, wv, acc[x]);
+          else acc[x] += wv;
+        }
+      }
+    }
+  }
+}
+
+template <int W, int QP, int CWP, bool VALUE, typename TIn>
+__device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArgs& a, int64_t frame, int oh,
+                                             const char* wlb) {
+  typedef typename Word<CWP>::type M;
+  const M* __restrict__ fb = reinterpret_cast<const M*>(a.bits) + frame * (int64_t)a.hw_in;
+  const TIn* __restrict__ xf = static_cast<const TIn*>(a.x) + frame * (int64_t)a.c_in * a.hw_in;
+  if (oh >= 1)
+    scatter_row<W, QP, CWP, 0, VALUE, TIn>(acc, fb + (oh - 1) * W, wlb, xf + (oh - 1) * W, a.hw_in);
+  scatter_row<W, QP, CWP, 1, VALUE, TIn>(acc, fb + oh * W, wlb, xf + oh * W, a.hw_in);
+  if (oh + 1 < a.h_in)
+    scatter_row<W, QP, CWP, 2, VALUE, TIn>(acc, fb + (oh + 1) * W, wlb, xf + (oh + 1) * W, a.hw_in);
+}
+
+// OR of the non-binary chunk flags covering input rows oh-1 .. oh+1.
+__device__ __forceinline__ bool rows_value_path(const ConvArgs& a, int64_t frame, int oh) {
+  const int ih_a = max(0, oh - 1), ih_b = min(a.h_in - 1, oh + 1);
+  const int64_t c_a = ((int64_t)ih_a * a.w_in) / a.chunk;
+  const int64_t c_b = ((int64_t)ih_b * a.w_in + a.w_in - 1) / a.chunk;
+  const uint32_t* fl = a.flags + frame * a.chunks_per_frame;
+  uint32_t f = 0u;
+  for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
+  return f != 0u;
+}
+
+template <typename TIn, typename TOut, int W, int CWP>
+__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, int groups, int krows) {
+  constexpr int QP = W <= 32 ? 8 : 16;  // quad slots per row (power of two >= W/4)
+  extern __shared__ __align__(16) char smem[];
+  float* wl = reinterpret_cast<float*>(smem);
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = blockIdx.x % groups;
+  const int co0 = grp * 64;
+  for (int i = threadIdx.x; i < krows * 64; i += 64 * kRowsWaves) {
+    const int r = i >> 6, c = i & 63;
+    wl[i] = (co0 + c < a.c_out) ? a.wt[(int64_t)r * a.c_out + co0 + c] : 0.f;
+  }
+  __syncthreads();
+  const char* wlb = smem + lane * 4;
+  const float bias = (a.bias != nullptr && co0 + lane < a.c_out) ? a.bias[co0 + lane] : 0.f;
+  const int rows_total = (int)(a.n * a.h_out);
+  const int wpg = (int)(gridDim.x / groups) * kRowsWaves;
+  const int q = lane & (QP - 1);
+  const int cbase = lane & ~(QP - 1);
+  for (int t = (int)(blockIdx.x / groups) * kRowsWaves + wave; t < rows_total; t += wpg) {
+    const int frame = t / a.h_out;
+    const int oh = t - frame * a.h_out;
+    float acc[4 * QP];
+#pragma unroll
+    for (int i = 0; i < 4 * QP; ++i) acc[i] = i < W ? bias : 0.f;
+    if (rows_value_path(a, frame, oh)) scatter_tile<W, QP, CWP, true, TIn>(acc, a, frame, oh, wlb);
+    else scatter_tile<W, QP, CWP, false, TIn>(acc, a, frame, oh, wlb);
+    butterfly<1, QP>(acc, lane);
+    butterfly<2, QP>(acc, lane);
+    butterfly<4, QP>(acc, lane);
+    if constexpr (QP == 16) butterfly<8, QP>(acc, lane);
+    // Slot k of lane L now holds output channel (L & ~(QP-1)) | k, columns 4*(L & (QP-1)) .. +3.
+    if (4 * q < W) {
+      TOut* yr = static_cast<TOut*>(a.y) + ((int64_t)frame * a.c_out + co0 + cbase) * a.hw_out + oh * W + 4 * q;
+#pragma unroll
+      for (int k = 0; k < QP; ++k) {
+        if (co0 + cbase + k < a.c_out)
+          store4<TOut>(yr + (int64_t)k * a.hw_out, acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
+      }
+    }
+  }
+}
+
+int g_num_cus[64] = {0};
+
+int num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (g_num_cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    g_num_cus[dev] = v;
+  }
+  return g_num_cus[dev];
+}
+
+template <typename TIn, typename TOut, int W, int CWP>
+int launch_rows_t(const ConvArgs& a, hipStream_t stream) {
+  const int groups = (a.c_out + 63) / 64;
+  const int krows = a.c_in * 9;
+  const size_t lds = (size_t)krows * 64 * sizeof(float);
+  const int64_t rows_total = a.n * (int64_t)a.h_out;
+  const int64_t need = (rows_total + kRowsWaves - 1) / kRowsWaves;
+  const int per_group = (int)(need < num_cus() ? need : num_cus());
+  const int grid = groups * (per_group > 0 ? per_group : 1);
+  auto kern = k_conv_rows<TIn, TOut, W, CWP>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kMaxLdsBytes);
+    attr_done = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, groups, krows);
+  return (int)hipGetLastError();
+}
+
+template <typename TIn, typename TOut>
+int launch_rows_d(const ConvArgs& a, hipStream_t stream) {
+  if (a.w_out == 56) return a.cwp == 1 ? launch_rows_t<TIn, TOut, 56, 1>(a, stream) : launch_rows_t<TIn, TOut, 56, 2>(a, stream);
+  return a.cwp == 1 ? launch_rows_t<TIn, TOut, 32, 1>(a, stream) : launch_rows_t<TIn, TOut, 32, 2>(a, stream);
+}
+
+}  // namespace
+
+bool rows_applicable(const ConvArgs& a) {
+  return a.k == 3 && a.s == 1 && a.p == 1 && a.c_in <= 64 && a.cwp <= 2 && a.h_out == a.h_in &&
+         a.w_out == a.w_in && (a.w_out == 56 || a.w_out == 32) && a.n * (int64_t)a.h_out < (1ll << 30) &&
+         (int64_t)a.c_in * 9 * 64 * 4 <= kMaxLdsBytes;
+}
+
+int launch_conv_rows(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  timing_begin(K_ROWS, stream);
+  int rc;
+  if (in_dtype == SF_F32) rc = launch_rows_d<float, float>(a, stream);
+  else if (in_dtype == SF_F16) rc = out_dtype == SF_F32 ? launch_rows_d<__half, float>(a, stream)
+                                                        : launch_rows_d<__half, __half>(a, stream);
+  else rc = out_dtype == SF_F32 ? launch_rows_d<__hip_bfloat16, float>(a, stream)
+                                : launch_rows_d<__hip_bfloat16, __hip_bfloat16>(a, stream);
+  timing_end(K_ROWS, stream);
+  return rc;
+}
+
+}  // namespace sf

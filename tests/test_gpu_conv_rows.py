@@ -1,0 +1,135 @@
+"""Row-tile scatter Stage 2 (3x3 stride 1, C_in <= 64, frame width 32 or 56).
+
+Same bar as the gather kernel: fp32 within 1e-4 abs + 1e-4 rel of float64
+F.conv2d on the spike-masked input, fp16/bf16 within 1e-2, bit-identical
+repeats.  Every case also checks that the row kernel (and not the gather
+kernel) produced the result.
+"""
+
+import pytest
+import torch
+
+from oracle import conv as oconv
+from sparseflow_amd import _lib
+from sparseflow_amd.Kernels.conv2d import sparse_conv2d_forward
+from tests.gpu_helpers import DEV, announce, close, native_loaded, spikes
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = dict(atol=1e-4, rtol=1e-4)
+
+
+def _weights(c_out, c_in, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(c_out, c_in, 3, 3, generator=g) * (2.0 / (c_in * 9)) ** 0.5
+
+
+def _run(x, w, b, **kw):
+    """sparse_conv2d_forward with kernel timing on; returns (y, kernels)."""
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        y = sparse_conv2d_forward(x, w, b, kernel_size=3, stride=1, padding=1, **kw)[0]
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return y, {k: c for k, (c, _) in stats.items() if c > 0}
+
+
+CASES = [
+    # (N, C_in, H, W, C_out)
+    (4, 64, 56, 56, 64),    # ResNet50 layer1 shape
+    (8, 64, 32, 32, 64),    # BASELINE config 1 shape
+    (2, 1, 5, 32, 3),       # single input channel, few rows
+    (3, 17, 1, 56, 10),     # single row: no input row above or below
+    (2, 32, 2, 32, 64),     # one 32-bit word per pixel
+    (2, 33, 7, 56, 65),     # two words, second nearly empty; C_out one past a group
+    (2, 48, 9, 32, 200),    # several output-channel groups, ragged last group
+    (1, 64, 56, 56, 128),   # two full groups
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("density", [0.0, 0.01, 0.3])
+def test_rows_fp32_matches_dense(case, density):
+    N, C, H, W, Co = case
+    announce(f"rows {case} p={density}")
+    x = spikes((N, C, H, W), density, seed=N * 5 + C)
+    w = _weights(Co, C, seed=C + Co)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(3)) * 0.1
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert "conv_rows" in kernels and "conv_gather" not in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    assert native_loaded()
+
+
+def test_rows_all_ones_input():
+    # Every tap active: the scalar walk visits all 64 channel bits of every
+    # input position.
+    x = torch.ones(2, 64, 6, 56)
+    w = _weights(64, 64, seed=9)
+    announce("rows all-ones")
+    y, kernels = _run(x.to(DEV), w.to(DEV), None)
+    assert "conv_rows" in kernels
+    ok, err, _ = close(y, oconv.conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_rows_value_path_only_where_flagged():
+    # Non-binary values in a few rows of one frame: those tiles take the
+    # multiply path, the rest stay on the add path.
+    g = torch.Generator().manual_seed(4)
+    x = spikes((3, 64, 32, 32), 0.05, seed=6)
+    x[1, :, 10:12] = x[1, :, 10:12] * torch.randn(64, 2, 32, generator=g)
+    x[2, 5, 31, 31] = -2.5
+    x[0, 0, 0, 0] = 3e-7       # below the activity threshold: dropped
+    w = _weights(64, 64, seed=10)
+    announce("rows value path")
+    y, kernels = _run(x.to(DEV), w.to(DEV), None)
+    assert "conv_rows" in kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rows_half_activations(dtype):
+    x = spikes((4, 64, 8, 56), 0.05, seed=11)
+    w = _weights(64, 64, seed=12)
+    b = torch.linspace(-0.5, 0.5, 64)
+    announce(f"rows {dtype}")
+    y, kernels = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV))
+    assert "conv_rows" in kernels and y.dtype == dtype
+    ok, err, _ = close(y, oconv.conv2d_ref(x, w, b, 1, 1), atol=1e-2, rtol=1e-2)
+    assert ok, f"max abs err {err}"
+    y32, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), output_dtype=torch.float32)
+    assert y32.dtype == torch.float32
+    ok, err, _ = close(y32, oconv.conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_rows_deterministic_bitwise():
+    x = spikes((16, 64, 56, 56), 0.02, seed=13).to(DEV)
+    w = _weights(64, 64, seed=14).to(DEV)
+    announce("rows determinism")
+    y1, _ = _run(x, w, None)
+    y2, _ = _run(x, w, None)
+    assert torch.equal(y1, y2)
+
+
+def test_rows_and_gather_agree():
+    # The two Stage-2 kernels on the same bitmap: rows (W=56) vs gather
+    # (same data with one padding column, W=57, which the row kernel does not
+    # take) agree on the shared columns to fp32 rounding.
+    x = spikes((4, 64, 12, 56), 0.03, seed=15)
+    w = _weights(64, 64, seed=16)
+    announce("rows vs gather")
+    y_rows, k1 = _run(x.to(DEV), w.to(DEV), None)
+    xp = torch.nn.functional.pad(x, (0, 1))
+    y_gather, k2 = _run(xp.to(DEV), w.to(DEV), None)
+    assert "conv_rows" in k1 and "conv_gather" in k2
+    # Column 55 of the padded run sees the zero column 56 as its right
+    # neighbour, exactly like the unpadded frame edge.
+    assert torch.allclose(y_rows, y_gather[..., :56], atol=1e-5, rtol=1e-5)
