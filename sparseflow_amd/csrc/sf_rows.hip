@@ -122,11 +122,12 @@ __device__ __forceinline__ void scatter_row(float (&acc)[4 * QP], const typename
 }
 
 template <int W, int QP, int CWP, bool VALUE, typename TIn>
-__device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArgs& a, int64_t frame, int oh,
-                                             const char* wlb) {
+__device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArgs& a,
+                                             const typename Word<CWP>::type* __restrict__ bits,
+                                             const TIn* __restrict__ x, int64_t frame, int oh, const char* wlb) {
   typedef typename Word<CWP>::type M;
-  const M* __restrict__ fb = reinterpret_cast<const M*>(a.bits) + frame * (int64_t)a.hw_in;
-  const TIn* __restrict__ xf = static_cast<const TIn*>(a.x) + frame * (int64_t)a.c_in * a.hw_in;
+  const M* __restrict__ fb = bits + frame * (int64_t)a.hw_in;
+  const TIn* __restrict__ xf = x + frame * (int64_t)a.c_in * a.hw_in;
   if (oh >= 1)
     scatter_row<W, QP, CWP, 0, VALUE, TIn>(acc, fb + (oh - 1) * W, wlb, xf + (oh - 1) * W, a.hw_in);
   scatter_row<W, QP, CWP, 1, VALUE, TIn>(acc, fb + oh * W, wlb, xf + oh * W, a.hw_in);
@@ -135,18 +136,26 @@ __device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArg
 }
 
 // OR of the non-binary chunk flags covering input rows oh-1 .. oh+1.
-__device__ __forceinline__ bool rows_value_path(const ConvArgs& a, int64_t frame, int oh) {
+__device__ __forceinline__ bool rows_value_path(const ConvArgs& a, const uint32_t* __restrict__ flags, int64_t frame,
+                                                int oh) {
   const int ih_a = max(0, oh - 1), ih_b = min(a.h_in - 1, oh + 1);
   const int64_t c_a = ((int64_t)ih_a * a.w_in) / a.chunk;
   const int64_t c_b = ((int64_t)ih_b * a.w_in + a.w_in - 1) / a.chunk;
-  const uint32_t* fl = a.flags + frame * a.chunks_per_frame;
+  const uint32_t* __restrict__ fl = flags + frame * a.chunks_per_frame;
   uint32_t f = 0u;
   for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
   return f != 0u;
 }
 
+// The bitmap, flags, x and weights are passed as separate restrict-qualified
+// arguments so that their uniform loads compile to scalar (SMEM) loads.
 template <typename TIn, typename TOut, int W, int CWP>
-__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, int groups, int krows) {
+__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, const uint32_t* __restrict__ bits,
+                                                               const uint32_t* __restrict__ flags,
+                                                               const TIn* __restrict__ x, const float* __restrict__ wt,
+                                                               const float* __restrict__ bias_p, TOut* __restrict__ y,
+                                                               int groups, int krows) {
+  typedef typename Word<CWP>::type M;
   constexpr int QP = W <= 32 ? 8 : 16;  // quad slots per row (power of two >= W/4)
   extern __shared__ __align__(16) char smem[];
   float* wl = reinterpret_cast<float*>(smem);
@@ -156,11 +165,11 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, int g
   const int co0 = grp * 64;
   for (int i = threadIdx.x; i < krows * 64; i += 64 * kRowsWaves) {
     const int r = i >> 6, c = i & 63;
-    wl[i] = (co0 + c < a.c_out) ? a.wt[(int64_t)r * a.c_out + co0 + c] : 0.f;
+    wl[i] = (co0 + c < a.c_out) ? wt[(int64_t)r * a.c_out + co0 + c] : 0.f;
   }
   __syncthreads();
   const char* wlb = smem + lane * 4;
-  const float bias = (a.bias != nullptr && co0 + lane < a.c_out) ? a.bias[co0 + lane] : 0.f;
+  const float bias = (bias_p != nullptr && co0 + lane < a.c_out) ? bias_p[co0 + lane] : 0.f;
   const int rows_total = (int)(a.n * a.h_out);
   const int wpg = (int)(gridDim.x / groups) * kRowsWaves;
   const int q = lane & (QP - 1);
@@ -171,15 +180,16 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, int g
     float acc[4 * QP];
 #pragma unroll
     for (int i = 0; i < 4 * QP; ++i) acc[i] = i < W ? bias : 0.f;
-    if (rows_value_path(a, frame, oh)) scatter_tile<W, QP, CWP, true, TIn>(acc, a, frame, oh, wlb);
-    else scatter_tile<W, QP, CWP, false, TIn>(acc, a, frame, oh, wlb);
+    const M* mbits = reinterpret_cast<const M*>(bits);
+    if (rows_value_path(a, flags, frame, oh)) scatter_tile<W, QP, CWP, true, TIn>(acc, a, mbits, x, frame, oh, wlb);
+    else scatter_tile<W, QP, CWP, false, TIn>(acc, a, mbits, x, frame, oh, wlb);
     butterfly<1, QP>(acc, lane);
     butterfly<2, QP>(acc, lane);
     butterfly<4, QP>(acc, lane);
     if constexpr (QP == 16) butterfly<8, QP>(acc, lane);
     // Slot k of lane L now holds output channel (L & ~(QP-1)) | k, columns 4*(L & (QP-1)) .. +3.
     if (4 * q < W) {
-      TOut* yr = static_cast<TOut*>(a.y) + ((int64_t)frame * a.c_out + co0 + cbase) * a.hw_out + oh * W + 4 * q;
+      TOut* yr = y + ((int64_t)frame * a.c_out + co0 + cbase) * a.hw_out + oh * W + 4 * q;
 #pragma unroll
       for (int k = 0; k < QP; ++k) {
         if (co0 + cbase + k < a.c_out)
@@ -218,7 +228,8 @@ int launch_rows_t(const ConvArgs& a, hipStream_t stream) {
                               kMaxLdsBytes);
     attr_done = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, groups, krows);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, krows);
   return (int)hipGetLastError();
 }
 
