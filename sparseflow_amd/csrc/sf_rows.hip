@@ -212,6 +212,245 @@ int num_cus() {
   return g_num_cus[dev];
 }
 
+// ---------------------------------------------------------------------------
+// K-chunked variant for layers whose weights do not fit LDS (C_in > 64).
+//
+// Tile = TH full rows of a W-wide frame (TH*W <= 64 output pixels, contiguous
+// in the output plane), lane = output channel.  Weights are consumed in
+// chunks of one 32-channel bitmap word (32 ci x 9 taps x 64 co = 72 KB),
+// double-buffered in LDS: while the workgroup's 16 wavefronts walk chunk c
+// from one buffer, chunk c+1 streams into the other with direct global->LDS
+// loads.  One barrier per chunk.  With at most two chunks both stay resident
+// and the wavefronts never synchronise.
+// ---------------------------------------------------------------------------
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
+
+constexpr int kChunkBytes = 32 * 9 * 64 * 4;  // one chunk of weights: 72 KB = 72 units of 1 KB
+
+// Issue the direct-to-LDS loads of weight chunk c into `buf`.  Each 1 KB unit
+// (4 weight rows x 64 channels) is one wavefront instruction: lane l carries
+// row 4u + l/16, channels 4*(l%16) .. +3.  Rows past C_in and channels past
+// C_out read a valid but unrelated address; those values are never used.
+__device__ __forceinline__ void load_chunk(char* buf, const float* __restrict__ wt, int c, int krows, int c_out,
+                                           int co0, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < (kChunkBytes / 1024 + kRowsWaves - 1) / kRowsWaves; ++j) {
+    const int u = wave + kRowsWaves * j;
+    if (u < kChunkBytes / 1024) {
+      const int row = c * (32 * 9) + u * 4 + (lane >> 4);
+      const int col = co0 + 4 * (lane & 15);
+      const float* src = (row < krows && col < c_out) ? wt + (int64_t)row * c_out + col : wt;
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+    }
+  }
+}
+
+// OR of the non-binary chunk flags covering input rows ih_a .. ih_b (clamped
+// to the frame).
+__device__ __forceinline__ bool rows_value_path(const ConvArgs& a, const uint32_t* __restrict__ flags, int64_t frame,
+                                                int ih_a, int ih_b) {
+  ih_a = max(0, ih_a);
+  ih_b = min(a.h_in - 1, ih_b);
+  const int64_t c_a = ((int64_t)ih_a * a.w_in) / a.chunk;
+  const int64_t c_b = ((int64_t)ih_b * a.w_in + a.w_in - 1) / a.chunk;
+  const uint32_t* __restrict__ fl = flags + frame * a.chunks_per_frame;
+  uint32_t f = 0u;
+  for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
+  return f != 0u;
+}
+
+__device__ __forceinline__ float load_x(const void* __restrict__ x, int dtype, int64_t i) {
+  if (dtype == SF_F16) return __half2float(static_cast<const __half*>(x)[i]);
+  if (dtype == SF_BF16) return __bfloat162float(static_cast<const __hip_bfloat16*>(x)[i]);
+  return static_cast<const float*>(x)[i];
+}
+
+struct KcTile {
+  const uint32_t* rowbits;  // bitmap word `chunk` of input row oh0 - 1 (may lie outside the frame)
+  const void* x;            // x plane of the frame (value path)
+  int64_t xrow;             // element offset of input row oh0 - 1 within a channel plane
+  const char* wlb;          // LDS weight chunk + lane offset
+  int oh0, h, cwp, hw, in_dtype, c0;  // c0 = first channel of the chunk
+  bool value;               // tile reads non-binary inputs: multiply by x
+};
+
+// Spikes of halo position (IA, IB) (input row oh0-1+IA, column IB) whose
+// chunk word is m.  Every weight row lands in a compile-time accumulator;
+// binary tiles multiply by exactly 1.
+template <int TH, int W, int IA, int IB>
+__device__ __forceinline__ void kc_position(float (&acc)[64], uint32_t m, const KcTile& k) {
+  while (m) {
+    const int bit = __builtin_ctz(m);
+    m &= m - 1;
+    float xv = 1.f;
+    if (k.value) xv = load_x(k.x, k.in_dtype, (int64_t)(k.c0 + bit) * k.hw + k.xrow + IA * W + IB);
+    const char* base = k.wlb + bit * (9 * 256);
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+      const int r = IA - kh;
+      if (r < 0 || r >= TH) continue;
+#pragma unroll
+      for (int kw = 0; kw < 3; ++kw) {
+        const int xo = IB + 1 - kw;
+        if (xo < 0 || xo >= W) continue;
+        acc[r * W + xo] = fmaf(xv, *reinterpret_cast<const float*>(base + (kh * 3 + kw) * 256), acc[r * W + xo]);
+      }
+    }
+  }
+}
+
+template <int TH, int W, int IA, int B0, int U, int NB>
+__device__ __forceinline__ void kc_batch_walk(float (&acc)[64], const uint32_t (&mw)[8], const KcTile& k) {
+  if constexpr (U < NB) {
+    kc_position<TH, W, IA, B0 + U>(acc, mw[U], k);
+    kc_batch_walk<TH, W, IA, B0, U + 1, NB>(acc, mw, k);
+  }
+}
+
+template <int TH, int W, int IA, int B0>
+__device__ __forceinline__ void kc_row(float (&acc)[64], const uint32_t* __restrict__ rp, const KcTile& k) {
+  if constexpr (B0 < W) {
+    constexpr int NB = (W - B0) < 8 ? (W - B0) : 8;
+    uint32_t mw[8];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) mw[u] = rp[(B0 + u) * k.cwp];
+    kc_batch_walk<TH, W, IA, B0, 0, NB>(acc, mw, k);
+    kc_row<TH, W, IA, B0 + 8>(acc, rp, k);
+  }
+}
+
+template <int TH, int W, int IA>
+__device__ __forceinline__ void kc_rows(float (&acc)[64], const KcTile& k) {
+  if constexpr (IA < TH + 2) {
+    const int ih = k.oh0 - 1 + IA;
+    if (ih >= 0 && ih < k.h) kc_row<TH, W, IA, 0>(acc, k.rowbits + (int64_t)IA * W * k.cwp, k);
+    kc_rows<TH, W, IA + 1>(acc, k);
+  }
+}
+
+// Store the tile (flattened run of npx pixels starting at run0) after the
+// transpose: slot j of lane L holds channel (L & ~15) | j, pixels
+// 4*(L & 15) .. +3 of the run.
+template <typename TOut>
+__device__ __forceinline__ void kc_store(float (&acc)[64], void* __restrict__ y, const ConvArgs& a, int64_t frame,
+                                         int co0, int run0, int npx, int lane) {
+  const int q = lane & 15, cb = lane & ~15;
+  if (4 * q < npx) {
+    TOut* yr = static_cast<TOut*>(y) + ((int64_t)frame * a.c_out + co0 + cb) * a.hw_out + run0 + 4 * q;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (co0 + cb + j < a.c_out)
+        store4<TOut>(yr + (int64_t)j * a.hw_out, acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]);
+  }
+}
+
+template <int TH, int W>
+__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, const uint32_t* __restrict__ bits,
+                                                                  const uint32_t* __restrict__ flags,
+                                                                  const void* __restrict__ x,
+                                                                  const float* __restrict__ wt,
+                                                                  const float* __restrict__ bias_p,
+                                                                  void* __restrict__ y, int groups, int nchunks,
+                                                                  int in_dtype, int out_dtype) {
+  // Launched only for planes with h*w % 4 == 0, so every tile's run (TH*W, or
+  // an even number of 14-wide rows for the last tile) is whole quads.
+  static_assert(TH * W <= 64 && (TH * W) % 4 == 0, "tile must be a whole number of quads within 64 pixels");
+  extern __shared__ __align__(16) char smem[];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = blockIdx.x % groups;
+  const int co0 = grp * 64;
+  const int krows = a.c_in * 9;
+  const float bias = (bias_p != nullptr && co0 + lane < a.c_out) ? bias_p[co0 + lane] : 0.f;
+  const int h = a.h_in;
+  const int tpf = (h + TH - 1) / TH;
+  const int total = (int)a.n * tpf;
+  const int nblk = (int)(gridDim.x / groups);
+  const bool resident = nchunks <= 2;
+  const int in_size = in_dtype == SF_F32 ? 4 : 2;
+
+  if (resident) {
+    for (int c = 0; c < nchunks; ++c) load_chunk(smem + c * kChunkBytes, wt, c, krows, a.c_out, co0, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  // Passes of kRowsWaves tiles.  With more than two chunks every wavefront
+  // takes part in every barrier, including those of a pass past the end.
+  for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
+    const int t = pass * kRowsWaves + wave;
+    const bool valid = t < total;
+    const int frame = valid ? t / tpf : 0;
+    const int oh0 = valid ? (t - frame * tpf) * TH : 0;
+    float acc[64];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) acc[i] = i < TH * W ? bias : 0.f;
+    KcTile k;
+    k.oh0 = oh0;
+    k.h = h;
+    k.cwp = a.cwp;
+    k.hw = a.hw_in;
+    k.in_dtype = in_dtype;
+    k.x = static_cast<const char*>(x) + (int64_t)frame * a.c_in * a.hw_in * in_size;
+    k.xrow = (int64_t)(oh0 - 1) * W;
+    k.value = valid && rows_value_path(a, flags, frame, oh0 - 1, oh0 + TH);
+    if (!resident) {
+      __syncthreads();  // the previous pass is done with both buffers
+      load_chunk(smem, wt, 0, krows, a.c_out, co0, wave, lane);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    for (int c = 0; c < nchunks; ++c) {
+      // Stream chunk c+1 into the other buffer; it was last read during
+      // chunk c-1, which every wavefront finished before the last barrier.
+      if (!resident && c + 1 < nchunks)
+        load_chunk(smem + ((c + 1) & 1) * kChunkBytes, wt, c + 1, krows, a.c_out, co0, wave, lane);
+      if (valid) {
+        k.rowbits = bits + ((int64_t)frame * a.hw_in + (int64_t)(oh0 - 1) * W) * a.cwp + c;
+        k.c0 = c * 32;
+        k.wlb = smem + (c & 1) * kChunkBytes + lane * 4;
+        kc_rows<TH, W, 0>(acc, k);
+      }
+      if (!resident) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    }
+    if (valid) {
+      const int npx = min(TH, h - oh0) * W;
+      butterfly<1, 16>(acc, lane);
+      butterfly<2, 16>(acc, lane);
+      butterfly<4, 16>(acc, lane);
+      butterfly<8, 16>(acc, lane);
+      if (out_dtype == SF_F16) kc_store<__half>(acc, y, a, frame, co0, oh0 * W, npx, lane);
+      else if (out_dtype == SF_BF16) kc_store<__hip_bfloat16>(acc, y, a, frame, co0, oh0 * W, npx, lane);
+      else kc_store<float>(acc, y, a, frame, co0, oh0 * W, npx, lane);
+    }
+  }
+}
+
+template <int TH, int W>
+int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  const int groups = (a.c_out + 63) / 64;
+  const int nchunks = (a.c_in + 31) / 32;
+  const size_t lds = (size_t)2 * kChunkBytes;
+  const int64_t tiles = a.n * (int64_t)((a.h_out + TH - 1) / TH);
+  const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
+  const int per_group = (int)(need < num_cus() ? need : num_cus());
+  const int grid = groups * (per_group > 0 ? per_group : 1);
+  auto kern = k_conv_rows_kc<TH, W>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kMaxLdsBytes);
+    attr_done = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags, a.x, a.wt, a.bias,
+                     a.y, groups, nchunks, in_dtype, out_dtype);
+  return (int)hipGetLastError();
+}
+
 template <typename TIn, typename TOut, int W, int CWP>
 int launch_rows_t(const ConvArgs& a, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
@@ -245,6 +484,20 @@ bool rows_applicable(const ConvArgs& a) {
   return a.k == 3 && a.s == 1 && a.p == 1 && a.c_in <= 64 && a.cwp <= 2 && a.h_out == a.h_in &&
          a.w_out == a.w_in && (a.w_out == 56 || a.w_out == 32) && a.n * (int64_t)a.h_out < (1ll << 30) &&
          (int64_t)a.c_in * 9 * 64 * 4 <= kMaxLdsBytes;
+}
+
+bool rows_kc_applicable(const ConvArgs& a) {
+  return a.k == 3 && a.s == 1 && a.p == 1 && a.h_out == a.h_in && a.w_out == a.w_in &&
+         (a.w_out == 28 || a.w_out == 14) && a.c_out % 4 == 0 && a.hw_out % 4 == 0 &&
+         a.n * (int64_t)a.h_out < (1ll << 30);
+}
+
+int launch_conv_rows_kc(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  timing_begin(K_ROWS_KC, stream);
+  const int rc = a.w_out == 28 ? launch_kc_t<2, 28>(a, in_dtype, out_dtype, stream)
+                               : launch_kc_t<4, 14>(a, in_dtype, out_dtype, stream);
+  timing_end(K_ROWS_KC, stream);
+  return rc;
 }
 
 int launch_conv_rows(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
