@@ -1,0 +1,259 @@
+// Stage 2 for 1x1 stride-1 convolutions: flat 64-pixel tiles, lane = pixel.
+//
+// One wavefront owns 64 consecutive pixels of one frame (a flat run of the
+// h*w plane; no halo) for 64 output channels: lane = pixel, one accumulator
+// register per output channel.  Each lane walks the set bits of its own
+// pixel's bitmap words (a divergent loop: the wavefront runs as many rounds as
+// its busiest pixel) and adds weight row ci, 64 output channels read from LDS
+// as 16 x 16-byte pieces, to its accumulators.  No scalar-unit walk, no
+// register transpose: the finished tile is stored one output channel per
+// instruction, 64 consecutive pixels = one 256-byte run per channel plane.
+//
+// LDS layout: weight row ci of the workgroup's 64-channel group takes 512
+// bytes, the row's 16 pieces written twice and rotated by (ci mod 16) pieces,
+// so that a read of pieces k..k+15 (k = ci mod 16) returns the row in order
+// with plain immediate offsets while lanes reading different rows spread over
+// the LDS banks.  Chunks of 128 input channels (64 KB); with at most two
+// chunks (C_in <= 256) they stay resident for the whole persistent launch and
+// the wavefronts never synchronise, beyond that chunk c+1 streams into the
+// second buffer (direct global->LDS loads) while chunk c is walked.
+//
+// Output element (co, p) = bias[co] + its spikes summed by one lane in
+// increasing ci: deterministic from run to run.
+// Replaces the reference's sparse_conv1x1_nhwc_kernel_8x8/8x16
+// (Kernels/conv2d.py:237-361) and its fused persistent 1x1 path
+// (Kernels/conv2d.py:364-560) for these shapes.
+#include "sf_tile.h"
+
+namespace sf {
+
+namespace {
+
+constexpr int kPxChunkCh = 128;                            // input channels per weight chunk
+constexpr int kPxChunkWords = kPxChunkCh / 32;             // bitmap words per chunk
+constexpr int kPxRowBytes = 512;                           // one rotated, doubled weight row
+constexpr int kPxChunkBytes = kPxChunkCh * kPxRowBytes;    // 64 KB
+
+// Direct-to-LDS loads of weight chunk c (rows c*128 .. +127 of wt, channels
+// co0 .. co0+63).  Each 1 KB unit is two rotated rows, one wavefront
+// instruction: lane l carries row 2u + l/32, position q = l % 32 of that row,
+// which holds the 16-byte piece (q - row) mod 16 (channels 4 * piece .. +3).
+// Rows past C_in are skipped; channels past C_out read a valid but unrelated
+// address whose values are never stored.
+__device__ __forceinline__ void load_chunk_px(char* buf, const float* __restrict__ wt, int c, int c_in, int c_out,
+                                              int co0, int wave, int lane) {
+  const int rows = min(kPxChunkCh, c_in - c * kPxChunkCh);
+  const int units = (rows + 1) / 2;
+#pragma unroll
+  for (int j = 0; j < kPxChunkBytes / 1024 / kRowsWaves; ++j) {
+    const int u = wave + kRowsWaves * j;
+    if (u < units) {
+      const int r = 2 * u + (lane >> 5);
+      const int piece = ((lane & 31) - r) & 15;
+      const int row = c * kPxChunkCh + r;
+      const int col = co0 + 4 * piece;
+      const float* src = (row < c_in && col < c_out) ? wt + (int64_t)row * c_out + col : wt;
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+    }
+  }
+}
+
+// Bitmap words as a lane walks them: 64-bit (two channel words) except for
+// single-word pixels.
+template <int CW>
+struct PxWord {
+  typedef uint64_t type;
+  static constexpr int count = CW / 2;
+};
+template <>
+struct PxWord<1> {
+  typedef uint32_t type;
+  static constexpr int count = 1;
+};
+
+__device__ __forceinline__ int px_first_bit(uint32_t m) { return __builtin_ctz(m); }
+__device__ __forceinline__ int px_first_bit(uint64_t m) { return __builtin_ctzll(m); }
+
+// Add weight row r of the chunk, times xv, to the lane's 64 accumulators.
+__device__ __forceinline__ void px_add_row(float (&acc)[64], const char* chunk, int r, float xv) {
+  const float4* rp = reinterpret_cast<const float4*>(chunk + r * kPxRowBytes + ((r & 15) << 4));
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    // Groups of four pieces: the scheduler may not hoist more than 16
+    // loaded registers ahead of their use (the accumulators take 64).
+    if (s % 4 == 0) __builtin_amdgcn_sched_barrier(0);
+    const float4 v = rp[s];
+    acc[4 * s] = fmaf(xv, v.x, acc[4 * s]);
+    acc[4 * s + 1] = fmaf(xv, v.y, acc[4 * s + 1]);
+    acc[4 * s + 2] = fmaf(xv, v.z, acc[4 * s + 2]);
+    acc[4 * s + 3] = fmaf(xv, v.w, acc[4 * s + 3]);
+  }
+}
+
+// Store the lane's pixel for output channels 0 .. nco-1 of the group: one
+// channel plane per instruction, 64 lanes = 64 consecutive pixels.
+template <typename TOut>
+__device__ __forceinline__ void px_store(const float (&acc)[64], TOut* __restrict__ yp, int hw, int nco) {
+  if (nco >= 64) {
+#pragma unroll
+    for (int co = 0; co < 64; ++co) yp[(int64_t)co * hw] = from_f32<TOut>(acc[co]);
+  } else {
+#pragma unroll
+    for (int co = 0; co < 64; ++co)
+      if (co < nco) yp[(int64_t)co * hw] = from_f32<TOut>(acc[co]);
+  }
+}
+
+template <int CW, typename TIn>
+__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const uint32_t* __restrict__ bits,
+                                                               const uint32_t* __restrict__ flags,
+                                                               const TIn* __restrict__ x,
+                                                               const float* __restrict__ wt,
+                                                               const float* __restrict__ bias_p,
+                                                               void* __restrict__ y, int groups, int nchunks,
+                                                               int out_dtype) {
+  typedef typename PxWord<CW>::type WT;
+  constexpr int NW = PxWord<CW>::count;          // walk words per pixel and chunk
+  constexpr int BITS = 8 * (int)sizeof(WT);
+  extern __shared__ __align__(16) char smem[];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = blockIdx.x % groups;
+  const int co0 = grp * 64;
+  const int hw = a.hw_in;
+  const int tpf = (hw + 63) / 64;
+  const int total = (int)a.n * tpf;
+  const int nblk = (int)(gridDim.x / groups);
+  const bool resident = nchunks <= 2;
+
+  if (resident) {
+    for (int c = 0; c < nchunks; ++c)
+      load_chunk_px(smem + c * kPxChunkBytes, wt, c, a.c_in, a.c_out, co0, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  // Passes of kRowsWaves tiles.  With more than two chunks every wavefront
+  // takes part in every barrier, including those of a pass past the end.
+  for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
+    const int t = pass * kRowsWaves + wave;
+    const bool valid = t < total;
+    const int frame = valid ? t / tpf : 0;
+    const int p0 = valid ? (t - frame * tpf) * 64 : 0;
+    const int npx = min(64, hw - p0);
+    const bool mine = valid && lane < npx;  // this lane's pixel exists
+    // Per-channel values (bias, store offsets) are formed in every pass,
+    // not kept live across the loop: the accumulators need the registers.
+    const float* __restrict__ bias_t = bias_p;
+    int hw_t = hw, c_out_t = a.c_out;
+    asm volatile("" : "+s"(bias_t), "+s"(hw_t), "+s"(c_out_t));
+    float acc[64];
+#pragma unroll
+    for (int co = 0; co < 64; ++co) acc[co] = (bias_t != nullptr && co0 + co < c_out_t) ? bias_t[co0 + co] : 0.f;
+    bool value = false;
+    if (valid) {
+      const int64_t c_a = p0 / a.chunk, c_b = (p0 + npx - 1) / a.chunk;
+      const uint32_t* __restrict__ fl = flags + (int64_t)frame * a.chunks_per_frame;
+      uint32_t f = 0u;
+      for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
+      value = f != 0u;
+    }
+    const TIn* xp = x + (int64_t)frame * a.c_in * hw + p0 + lane;  // this lane's pixel, channel 0
+    if (!resident) {
+      __syncthreads();  // the previous pass is done with both buffers
+      load_chunk_px(smem, wt, 0, a.c_in, a.c_out, co0, wave, lane);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    for (int c = 0; c < nchunks; ++c) {
+      // Stream chunk c+1 into the other buffer; it was last read during
+      // chunk c-1, which every wavefront finished before the last barrier.
+      if (!resident && c + 1 < nchunks)
+        load_chunk_px(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, lane);
+      if (mine) {
+        WT w[NW];
+        const WT* __restrict__ bp =
+            reinterpret_cast<const WT*>(bits + ((int64_t)frame * hw + p0 + lane) * a.cwp + c * CW);
+#pragma unroll
+        for (int j = 0; j < NW; ++j) w[j] = bp[j];
+        const char* chunk = smem + (c & 1) * kPxChunkBytes;
+#pragma unroll
+        for (int j = 0; j < NW; ++j) {
+          WT m = w[j];
+          // One loop body for both paths (binary tiles multiply by exactly
+          // 1): a second copy of the accumulator updates would double their
+          // live ranges.
+          while (m) {
+            const int r = j * BITS + px_first_bit(m);
+            m &= m - 1;
+            float xv = 1.f;
+            if (value) xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * hw]);
+            px_add_row(acc, chunk, r, xv);
+          }
+        }
+      }
+      if (!resident) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    }
+    if (mine) {
+      const int64_t yb = ((int64_t)frame * c_out_t + co0) * hw_t + p0 + lane;
+      const int nco = min(64, c_out_t - co0);
+      if (out_dtype == SF_F16) px_store(acc, static_cast<__half*>(y) + yb, hw_t, nco);
+      else if (out_dtype == SF_BF16) px_store(acc, static_cast<__hip_bfloat16*>(y) + yb, hw_t, nco);
+      else px_store(acc, static_cast<float*>(y) + yb, hw_t, nco);
+    }
+  }
+}
+
+template <int CW, typename TIn>
+int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+  const int groups = (a.c_out + 63) / 64;
+  const int nchunks = CW < kPxChunkWords ? 1 : a.cwp / kPxChunkWords;
+  // Resident: the chunks up to the last one's used 1 KB units; streamed: two
+  // full buffers.
+  const int last_units = (min(kPxChunkCh, a.c_in - (nchunks - 1) * kPxChunkCh) + 1) / 2;
+  const size_t lds = nchunks <= 2 ? (size_t)(nchunks - 1) * kPxChunkBytes + (size_t)last_units * 1024
+                                  : (size_t)2 * kPxChunkBytes;
+  const int64_t tiles = a.n * (int64_t)((a.hw_in + 63) / 64);
+  const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
+  const int per_group = (int)(need < num_cus() ? need : num_cus());
+  const int grid = groups * (per_group > 0 ? per_group : 1);
+  auto kern = k_conv_flat<CW, TIn>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kMaxLdsBytes);
+    attr_done = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype);
+  return (int)hipGetLastError();
+}
+
+template <typename TIn>
+int launch_flat_d(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+  switch (a.cwp) {
+    case 1: return launch_flat_t<1, TIn>(a, out_dtype, stream);
+    case 2: return launch_flat_t<2, TIn>(a, out_dtype, stream);
+    default: return launch_flat_t<4, TIn>(a, out_dtype, stream);
+  }
+}
+
+}  // namespace
+
+bool flat_applicable(const ConvArgs& a) {
+  return a.k == 1 && a.s == 1 && a.p == 0 && a.h_out == a.h_in && a.w_out == a.w_in && a.c_out % 4 == 0 &&
+         a.n * (int64_t)((a.hw_in + 63) / 64) < (1ll << 30);
+}
+
+int launch_conv_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  timing_begin(K_FLAT, stream);
+  const int rc = in_dtype == SF_F16    ? launch_flat_d<__half>(a, out_dtype, stream)
+                 : in_dtype == SF_BF16 ? launch_flat_d<__hip_bfloat16>(a, out_dtype, stream)
+                                       : launch_flat_d<float>(a, out_dtype, stream);
+  timing_end(K_FLAT, stream);
+  return rc;
+}
+
+}  // namespace sf

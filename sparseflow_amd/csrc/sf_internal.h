@@ -95,13 +95,17 @@ int launch_conv_rows(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t
 bool rows_kc_applicable(const ConvArgs& a);
 int launch_conv_rows_kc(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Flat-tile Stage 2 for 1x1 stride-1 convolutions (any C_in, C_out % 4 == 0).
+bool flat_applicable(const ConvArgs& a);
+int launch_conv_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
 
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_COUNT = 6 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_COUNT = 7 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

@@ -18,74 +18,12 @@
 // order (input row, input column, ci): deterministic from run to run.
 // Replaces the reference's sparse_conv3x3s1_nhwc_kernel_8x8/8x16
 // (Kernels/conv2d.py:564-724) for these shapes.
-#include "sf_internal.h"
+#include "sf_tile.h"
 
 namespace sf {
 
 namespace {
 
-constexpr int kRowsWaves = 16;  // wavefronts per workgroup (one workgroup per CU)
-
-// Exchange lane bit S with quad-slot bit S over v[4 * QP] (a butterfly stage
-// of the register transpose).  Lanes with bit S set take the partner's upper
-// slot; lanes with it clear take the partner's lower slot.
-template <int S, int QP>
-__device__ __forceinline__ void butterfly(float (&v)[4 * QP], int lane) {
-#pragma unroll
-  for (int j = 0; j < QP; ++j) {
-    if (j & S) continue;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int ai = __float_as_int(v[4 * j + e]);
-      const int bi = __float_as_int(v[4 * (j | S) + e]);
-      int na, nb;
-      if constexpr (S == 1 || S == 2) {
-        constexpr int qp = S == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
-        const int pa = __builtin_amdgcn_mov_dpp(ai, qp, 0xf, 0xf, false);
-        const int pb = __builtin_amdgcn_mov_dpp(bi, qp, 0xf, 0xf, false);
-        const bool hi = (lane & S) != 0;
-        na = hi ? pb : ai;
-        nb = hi ? bi : pa;
-      } else {
-        // row_shl:S reads lane L+S, row_shr:S reads lane L-S; the bank mask
-        // restricts each to the lanes whose bit S is clear / set.
-        constexpr int shl = 0x100 | S, shr = 0x110 | S;
-        constexpr int lo_banks = S == 4 ? 0x5 : 0x3, hi_banks = S == 4 ? 0xa : 0xc;
-        nb = __builtin_amdgcn_update_dpp(bi, ai, shl, 0xf, lo_banks, false);
-        na = __builtin_amdgcn_update_dpp(ai, bi, shr, 0xf, hi_banks, false);
-      }
-      v[4 * j + e] = __int_as_float(na);
-      v[4 * (j | S) + e] = __int_as_float(nb);
-    }
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void store4(T* p, float a, float b, float c, float d) {
-  if constexpr (sizeof(T) == 4) {
-    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
-  } else {
-    const T h0 = from_f32<T>(a), h1 = from_f32<T>(b), h2 = from_f32<T>(c), h3 = from_f32<T>(d);
-    uint16_t u0, u1, u2, u3;
-    __builtin_memcpy(&u0, &h0, 2);
-    __builtin_memcpy(&u1, &h1, 2);
-    __builtin_memcpy(&u2, &h2, 2);
-    __builtin_memcpy(&u3, &h3, 2);
-    *reinterpret_cast<uint2*>(p) = make_uint2((uint32_t)u0 | ((uint32_t)u1 << 16), (uint32_t)u2 | ((uint32_t)u3 << 16));
-  }
-}
-
-// Bitmap word type: both channel words of a pixel as one 64-bit value when
-// the bitmap has two words per pixel.
-template <int CWP> struct Word;
-template <> struct Word<1> { typedef uint32_t type; };
-template <> struct Word<2> { typedef uint64_t type; };
-
-template <typename M>
-__device__ __forceinline__ int lowest_bit(M m) {
-  if constexpr (sizeof(M) == 8) return __builtin_ctzll(m);
-  else return __builtin_ctz(m);
-}
 
 // Accumulate the spikes of input row ih (= oh - 1 + IA) into acc.
 template <int W, int QP, int CWP, int IA, bool VALUE, typename TIn>
@@ -199,19 +137,6 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, const
   }
 }
 
-int g_num_cus[64] = {0};
-
-int num_cus() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (g_num_cus[dev] == 0) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    g_num_cus[dev] = v;
-  }
-  return g_num_cus[dev];
-}
-
 // ---------------------------------------------------------------------------
 // K-chunked variant for layers whose weights do not fit LDS (C_in > 64).
 //
@@ -223,9 +148,6 @@ int num_cus() {
 // loads.  One barrier per chunk.  With at most two chunks both stay resident
 // and the wavefronts never synchronise.
 // ---------------------------------------------------------------------------
-
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
 constexpr int kChunkBytes = 32 * 9 * 64 * 4;  // one chunk of weights: 72 KB = 72 units of 1 KB
 
@@ -245,26 +167,6 @@ __device__ __forceinline__ void load_chunk(char* buf, const float* __restrict__ 
       __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
     }
   }
-}
-
-// OR of the non-binary chunk flags covering input rows ih_a .. ih_b (clamped
-// to the frame).
-__device__ __forceinline__ bool rows_value_path(const ConvArgs& a, const uint32_t* __restrict__ flags, int64_t frame,
-                                                int ih_a, int ih_b) {
-  ih_a = max(0, ih_a);
-  ih_b = min(a.h_in - 1, ih_b);
-  const int64_t c_a = ((int64_t)ih_a * a.w_in) / a.chunk;
-  const int64_t c_b = ((int64_t)ih_b * a.w_in + a.w_in - 1) / a.chunk;
-  const uint32_t* __restrict__ fl = flags + frame * a.chunks_per_frame;
-  uint32_t f = 0u;
-  for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
-  return f != 0u;
-}
-
-__device__ __forceinline__ float load_x(const void* __restrict__ x, int dtype, int64_t i) {
-  if (dtype == SF_F16) return __half2float(static_cast<const __half*>(x)[i]);
-  if (dtype == SF_BF16) return __bfloat162float(static_cast<const __hip_bfloat16*>(x)[i]);
-  return static_cast<const float*>(x)[i];
 }
 
 struct KcTile {
@@ -327,22 +229,6 @@ __device__ __forceinline__ void kc_rows(float (&acc)[64], const KcTile& k) {
     const int ih = k.oh0 - 1 + IA;
     if (ih >= 0 && ih < k.h) kc_row<TH, W, IA, 0>(acc, k.rowbits + (int64_t)IA * W * k.cwp, k);
     kc_rows<TH, W, IA + 1>(acc, k);
-  }
-}
-
-// Store the tile (flattened run of npx pixels starting at run0) after the
-// transpose: slot j of lane L holds channel (L & ~15) | j, pixels
-// 4*(L & 15) .. +3 of the run.
-template <typename TOut>
-__device__ __forceinline__ void kc_store(float (&acc)[64], void* __restrict__ y, const ConvArgs& a, int64_t frame,
-                                         int co0, int run0, int npx, int lane) {
-  const int q = lane & 15, cb = lane & ~15;
-  if (4 * q < npx) {
-    TOut* yr = static_cast<TOut*>(y) + ((int64_t)frame * a.c_out + co0 + cb) * a.hw_out + run0 + 4 * q;
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      if (co0 + cb + j < a.c_out)
-        store4<TOut>(yr + (int64_t)j * a.hw_out, acc[4 * j], acc[4 * j + 1], acc[4 * j + 2], acc[4 * j + 3]);
   }
 }
 
@@ -423,9 +309,9 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
       butterfly<2, 16>(acc, lane);
       butterfly<4, 16>(acc, lane);
       butterfly<8, 16>(acc, lane);
-      if (out_dtype == SF_F16) kc_store<__half>(acc, y, a, frame, co0, oh0 * W, npx, lane);
-      else if (out_dtype == SF_BF16) kc_store<__hip_bfloat16>(acc, y, a, frame, co0, oh0 * W, npx, lane);
-      else kc_store<float>(acc, y, a, frame, co0, oh0 * W, npx, lane);
+      if (out_dtype == SF_F16) tile_store<__half>(acc, y, a, frame, co0, oh0 * W, npx, lane);
+      else if (out_dtype == SF_BF16) tile_store<__hip_bfloat16>(acc, y, a, frame, co0, oh0 * W, npx, lane);
+      else tile_store<float>(acc, y, a, frame, co0, oh0 * W, npx, lane);
     }
   }
 }
@@ -479,6 +365,21 @@ int launch_rows_d(const ConvArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+namespace {
+int g_num_cus[64] = {0};
+}  // namespace
+
+int num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (g_num_cus[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    g_num_cus[dev] = v;
+  }
+  return g_num_cus[dev];
+}
 
 bool rows_applicable(const ConvArgs& a) {
   return a.k == 3 && a.s == 1 && a.p == 1 && a.c_in <= 64 && a.cwp <= 2 && a.h_out == a.h_in &&
