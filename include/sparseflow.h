@@ -132,9 +132,10 @@ int sf_prescan_tiles(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in,
 /* Sparse conv over a bitmap produced by sf_prescan_pack for the same x.
  * Binary chunks add weight rows; chunks flagged non-binary read x and FMA.
  * bias may be NULL.  Kernel choice, by shape: 3x3 stride 1 with c_in <= 64
- * on frames of width 32 or 56 runs the row-tile scatter kernel
- * ("conv_rows"); 3x3 stride 1 on frames of width 28 or 14 with c_out and h*w
- * multiples of 4 runs the K-chunked row-tile kernel ("conv_rows_kc"); 1x1
+ * on frames of width 32 runs the row-tile scatter kernel ("conv_rows"); 3x3
+ * stride 1 on frames of width 28 or 14 with c_out and h*w multiples of 4 runs
+ * the K-chunked row-tile kernel ("conv_rows_kc"); other 3x3 (stride 1 or 2)
+ * with c_out a multiple of 4 runs the pixel-tile kernel ("conv_px3"); 1x1
  * stride 1 with c_out a multiple of 4 runs the flat-tile kernel
  * ("conv_flat"); every other supported shape runs the gather kernel
  * ("conv_gather").  Replaces sparse_conv3x3s1/s2 and conv1x1 NHWC kernels
@@ -169,7 +170,7 @@ int sf_conv_lif_forward(const sf_conv_desc* desc, int32_t T, const void* x,
  * hipEvent pair on its stream.  sf_timing_collect synchronises those events
  * and accumulates per-kernel totals; sf_timing_query reads them by name
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
- * "conv_rows_kc", "conv_flat").
+ * "conv_rows_kc", "conv_flat", "conv_px3").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

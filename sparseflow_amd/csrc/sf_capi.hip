@@ -193,7 +193,7 @@ std::vector<TimingRec> g_pending;
 double g_total_ms[sf::K_COUNT] = {};
 int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
-                                     "conv_rows_kc", "conv_flat"};
+                                     "conv_rows_kc", "conv_flat", "conv_px3"};
 
 }  // namespace
 
@@ -357,6 +357,11 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
   if (sf::rows_kc_applicable(a)) {
     rc = sf::launch_conv_rows_kc(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
     if (rc != hipSuccess) return hip_fail(rc, "conv_rows_kc launch");
+    return SF_OK;
+  }
+  if (sf::px3_applicable(a)) {
+    rc = sf::launch_conv_px3(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
+    if (rc != hipSuccess) return hip_fail(rc, "conv_px3 launch");
     return SF_OK;
   }
   if (sf::flat_applicable(a)) {

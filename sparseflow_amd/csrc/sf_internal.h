@@ -99,13 +99,17 @@ int launch_conv_rows_kc(const ConvArgs& a, int in_dtype, int out_dtype, hipStrea
 bool flat_applicable(const ConvArgs& a);
 int launch_conv_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Pixel-tile Stage 2 for 3x3 convolutions (stride 1 or 2, C_out % 4 == 0).
+bool px3_applicable(const ConvArgs& a);
+int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
 
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_COUNT = 7 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_COUNT = 8 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

@@ -1,0 +1,284 @@
+// Stage 2 for 3x3 convolutions (stride 1 or 2, padding 1): 64-pixel output
+// tiles, lane = output pixel.
+//
+// One wavefront owns 64 consecutive output pixels of one frame (a flat run of
+// the h_out*w_out plane) for 64 output channels: lane = output pixel, one
+// accumulator register per output channel.  Input channels are taken in
+// chunks of 32 (one bitmap word per input pixel).  For a chunk, each lane
+// loads the word of each of its 9 input taps (0 outside the frame) and then
+// walks its own spikes in (tap, ci) order with a per-lane cursor: a divergent
+// loop whose round count is the busiest pixel's spike count.  Every spike adds
+// weight row (ci, tap) -- 64 output channels, read from LDS as 16 x 16-byte
+// pieces at immediate offsets -- to the lane's accumulators.  The finished
+// tile is stored one output channel per instruction (64 consecutive pixels =
+// one 256-byte run of the channel plane).
+//
+// LDS: a chunk is 288 weight rows (32 ci x 9 taps) of 64 output channels,
+// each row padded to 272 bytes so that lanes reading different rows spread
+// over the banks (77 KB per chunk).  With at most two chunks (C_in <= 64) the
+// weights stay resident for the whole persistent launch and the wavefronts
+// never synchronise; beyond that chunk c+1 streams into the second buffer
+// (direct global->LDS loads) while chunk c is walked.
+//
+// Output element (co, oh, ow) = bias[co] + its active taps summed by one lane
+// in (chunk, tap, ci) order: deterministic from run to run.
+// Replaces the reference's sparse_conv3x3s1_nhwc_kernel_8x8/8x16 and
+// sparse_conv3x3s2 kernels (Kernels/conv2d.py:564-886) for these shapes.
+#include "sf_tile.h"
+
+namespace sf {
+
+namespace {
+
+constexpr int kPx3Ch = 32;                              // input channels per chunk (one bitmap word)
+constexpr int kPx3Rows = kPx3Ch * 9;                    // weight rows per chunk
+constexpr int kPx3Pieces = 17;                          // 16-byte pieces per padded row (16 + pad)
+constexpr int kPx3Units = (kPx3Rows * kPx3Pieces + 63) / 64;  // 1 KB load units per chunk (77)
+constexpr int kPx3ChunkBytes = kPx3Units * 1024;        // 77 KB
+
+// Direct-to-LDS loads of weight chunk c.  The chunk is an array of 16-byte
+// pieces, row r piece s at position 17 r + s (position 17 r + 16 is padding).
+// Unit u fills positions 64 u .. 64 u + 63, lane l position 64 u + l.  Pads,
+// rows past C_in and channels past C_out read a valid but unrelated address
+// whose values are never used.
+__device__ __forceinline__ void load_chunk_px3(char* buf, const float* __restrict__ wt, int c, int krows,
+                                               int c_out, int co0, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < (kPx3Units + kRowsWaves - 1) / kRowsWaves; ++j) {
+    const int u = wave + kRowsWaves * j;
+    if (u < kPx3Units) {
+      const int pos = u * 64 + lane;
+      const int r = pos / kPx3Pieces;
+      const int s = pos - r * kPx3Pieces;
+      const int row = c * kPx3Rows + r;
+      const int col = co0 + 4 * s;
+      const float* src =
+          (s < 16 && r < kPx3Rows && row < krows && col < c_out) ? wt + (int64_t)row * c_out + col : wt;
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+    }
+  }
+}
+
+// Add padded weight row r of the chunk, times xv, to the 64 accumulators.
+__device__ __forceinline__ void px3_add_row(float (&acc)[64], const char* chunk, int r, float xv) {
+  static_assert(kPx3Pieces * 16 == 272, "row stride is 256 + 16 bytes");
+  const float4* rp = reinterpret_cast<const float4*>(chunk + (r << 8) + (r << 4));
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    // Groups of four pieces: the scheduler may not hoist more than 16
+    // loaded registers ahead of their use (the accumulators take 64).
+    if (s % 4 == 0) __builtin_amdgcn_sched_barrier(0);
+    const float4 v = rp[s];
+    acc[4 * s] = fmaf(xv, v.x, acc[4 * s]);
+    acc[4 * s + 1] = fmaf(xv, v.y, acc[4 * s + 1]);
+    acc[4 * s + 2] = fmaf(xv, v.z, acc[4 * s + 2]);
+    acc[4 * s + 3] = fmaf(xv, v.w, acc[4 * s + 3]);
+  }
+}
+
+// Word of tap t among the lane's nine: a per-lane 9-way multiplexer on the
+// bits of t (eight selects).
+__device__ __forceinline__ uint32_t px3_select(const uint32_t (&w)[9], int t) {
+  const uint32_t v0 = w[0], v1 = w[1], v2 = w[2], v3 = w[3], v4 = w[4], v5 = w[5], v6 = w[6], v7 = w[7], v8 = w[8];
+  const bool b0 = t & 1, b1 = t & 2, b2 = t & 4, b3 = t & 8;
+  const uint32_t a0 = b0 ? v1 : v0, a1 = b0 ? v3 : v2;
+  const uint32_t a2 = b0 ? v5 : v4, a3 = b0 ? v7 : v6;
+  const uint32_t c0 = b1 ? a1 : a0, c1 = b1 ? a3 : a2;
+  const uint32_t d0 = b2 ? c1 : c0;
+  return b3 ? v8 : d0;
+}
+
+// Bitmap word c of each of the lane's nine input taps (0 outside the frame).
+// Branch-free with 32-bit offsets from the frame's bitmap base: taps outside
+// the frame read pixel 0 and are zeroed, so all nine loads are in flight
+// together.
+__device__ __forceinline__ void px3_load_words(uint32_t (&w)[9], const uint32_t* __restrict__ bf,
+                                               const ConvArgs& a, int ih0, int iw0, int c) {
+  uint32_t v[9];
+#pragma unroll
+  for (int tp = 0; tp < 9; ++tp) {
+    const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
+    const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
+    const uint32_t off = (uint32_t)(in ? ih * a.w_in + iw : 0) * (uint32_t)a.cwp + (uint32_t)c;
+    v[tp] = bf[off];
+  }
+#pragma unroll
+  for (int tp = 0; tp < 9; ++tp) {
+    const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
+    const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
+    w[tp] = in ? v[tp] : 0u;
+  }
+}
+
+template <typename TOut>
+__device__ __forceinline__ void px3_store(const float (&acc)[64], TOut* __restrict__ yp, int hw, int nco) {
+  if (nco >= 64) {
+#pragma unroll
+    for (int co = 0; co < 64; ++co) yp[(int64_t)co * hw] = from_f32<TOut>(acc[co]);
+  } else {
+#pragma unroll
+    for (int co = 0; co < 64; ++co)
+      if (co < nco) yp[(int64_t)co * hw] = from_f32<TOut>(acc[co]);
+  }
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const uint32_t* __restrict__ bits,
+                                                              const uint32_t* __restrict__ flags,
+                                                              const TIn* __restrict__ x,
+                                                              const float* __restrict__ wt,
+                                                              const float* __restrict__ bias_p,
+                                                              void* __restrict__ y, int groups, int nchunks,
+                                                              int out_dtype) {
+  extern __shared__ __align__(16) char smem[];
+  const int lane0 = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = blockIdx.x % groups;
+  const int co0 = grp * 64;
+  const int krows = a.c_in * 9;
+  const int hwo = a.hw_out;
+  const int tpf = (hwo + 63) / 64;
+  const int total = (int)a.n * tpf;
+  const int nblk = (int)(gridDim.x / groups);
+  const bool resident = nchunks <= 2;
+
+  if (resident) {
+    for (int c = 0; c < nchunks; ++c)
+      load_chunk_px3(smem + c * kPx3ChunkBytes, wt, c, krows, a.c_out, co0, wave, lane0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  // Passes of kRowsWaves tiles.  With more than two chunks every wavefront
+  // takes part in every barrier, including those of a pass past the end.
+  for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
+    // Lane-dependent addresses are recomputed in every pass rather than kept
+    // live across the loop (the accumulators need the registers).
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int t = pass * kRowsWaves + wave;
+    const bool valid = t < total;
+    const int frame = valid ? t / tpf : 0;
+    const int p0 = valid ? (t - frame * tpf) * 64 : 0;
+    const int npx = min(64, hwo - p0);
+    const bool mine = valid && lane < npx;
+    // This lane's output pixel and the top-left corner of its input window.
+    const int q = p0 + min(lane, npx - 1);
+    const int oh = q / a.w_out, ow = q - (q / a.w_out) * a.w_out;
+    const int ih0 = oh * a.s - 1, iw0 = ow * a.s - 1;
+    // Per-channel values (bias, store offsets) are formed in every pass,
+    // not kept live across the loop: the accumulators need the registers.
+    const float* __restrict__ bias_t = bias_p;
+    int hwo_t = hwo, c_out_t = a.c_out;
+    asm volatile("" : "+s"(bias_t), "+s"(hwo_t), "+s"(c_out_t));
+    float acc[64];
+#pragma unroll
+    for (int co = 0; co < 64; ++co) acc[co] = (bias_t != nullptr && co0 + co < c_out_t) ? bias_t[co0 + co] : 0.f;
+    bool value = false;
+    if (valid) {
+      const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
+      value = rows_value_path(a, flags, frame, oh_a * a.s - 1, oh_b * a.s + 1);
+    }
+    const uint32_t* __restrict__ bf = bits + (int64_t)frame * a.hw_in * a.cwp;
+    const TIn* __restrict__ xf = x + (int64_t)frame * a.c_in * a.hw_in;
+    uint32_t wn[9];
+    if (mine) px3_load_words(wn, bf, a, ih0, iw0, 0);
+    if (!resident) {
+      __syncthreads();  // the previous pass is done with both buffers
+      load_chunk_px3(smem, wt, 0, krows, a.c_out, co0, wave, lane);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    for (int c = 0; c < nchunks; ++c) {
+      // Stream chunk c+1 into the other buffer; it was last read during
+      // chunk c-1, which every wavefront finished before the last barrier.
+      if (!resident && c + 1 < nchunks)
+        load_chunk_px3(smem + ((c + 1) & 1) * kPx3ChunkBytes, wt, c + 1, krows, a.c_out, co0, wave, lane);
+      if (mine) {
+        // This chunk's words were loaded during the previous chunk's walk;
+        // start the next chunk's loads now.
+        uint32_t w[9];
+#pragma unroll
+        for (int tp = 0; tp < 9; ++tp) w[tp] = wn[tp];
+        // Opaque to the optimiser: a select between two array elements would
+        // otherwise be folded into an indexed load, which keeps the array in
+        // scratch memory.
+        asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]),
+                     "+v"(w[7]), "+v"(w[8]));
+        if (c + 1 < nchunks) px3_load_words(wn, bf, a, ih0, iw0, c + 1);
+        uint32_t nz = 0u;
+#pragma unroll
+        for (int tp = 0; tp < 9; ++tp) nz |= (w[tp] != 0u ? 1u : 0u) << tp;
+        const char* chunk = smem + (c & 1) * kPx3ChunkBytes;
+        uint32_t m = 0u;
+        int tap = 0;
+        // Per-lane cursor over (tap, ci): the wavefront loops while any lane
+        // has spikes left.
+        while ((m | nz) != 0u) {
+          if (m == 0u) {
+            tap = __builtin_ctz(nz);
+            nz &= nz - 1u;
+            m = px3_select(w, tap);
+          }
+          const int bit = __builtin_ctz(m);
+          m &= m - 1u;
+          float xv = 1.f;
+          if (value) {
+            const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+            xv = to_f32<TIn>(xf[(int64_t)(c * kPx3Ch + bit) * a.hw_in + ih * a.w_in + iw]);
+          }
+          px3_add_row(acc, chunk, bit * 9 + tap, xv);
+        }
+      }
+      if (!resident) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+    }
+    if (mine) {
+      const int64_t yb = ((int64_t)frame * c_out_t + co0) * hwo_t + p0 + lane;
+      const int nco = min(64, c_out_t - co0);
+      if (out_dtype == SF_F16) px3_store(acc, static_cast<__half*>(y) + yb, hwo_t, nco);
+      else if (out_dtype == SF_BF16) px3_store(acc, static_cast<__hip_bfloat16*>(y) + yb, hwo_t, nco);
+      else px3_store(acc, static_cast<float*>(y) + yb, hwo_t, nco);
+    }
+  }
+}
+
+template <typename TIn>
+int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+  const int groups = (a.c_out + 63) / 64;
+  const int nchunks = (a.c_in + kPx3Ch - 1) / kPx3Ch;
+  const size_t lds = (size_t)(nchunks < 2 ? nchunks : 2) * kPx3ChunkBytes;
+  const int64_t tiles = a.n * (int64_t)((a.hw_out + 63) / 64);
+  const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
+  const int per_group = (int)(need < num_cus() ? need : num_cus());
+  const int grid = groups * (per_group > 0 ? per_group : 1);
+  auto kern = k_conv_px3<TIn>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kMaxLdsBytes);
+    attr_done = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+bool px3_applicable(const ConvArgs& a) {
+  return a.k == 3 && a.p == 1 && (a.s == 1 || a.s == 2) && a.c_out % 4 == 0 && a.cwp <= 64 &&
+         a.n * (int64_t)((a.hw_out + 63) / 64) < (1ll << 30);
+}
+
+int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  timing_begin(K_PX3, stream);
+  const int rc = in_dtype == SF_F16    ? launch_px3_t<__half>(a, out_dtype, stream)
+                 : in_dtype == SF_BF16 ? launch_px3_t<__hip_bfloat16>(a, out_dtype, stream)
+                                       : launch_px3_t<float>(a, out_dtype, stream);
+  timing_end(K_PX3, stream);
+  return rc;
+}
+
+}  // namespace sf

@@ -1,6 +1,7 @@
 // Stage 2, row-tile scatter formulation: 3x3 stride-1 convolutions whose
 // weights for 64 output channels fit in LDS (C_in <= 64) on frames of width
-// 32 or 56.
+// 32 (the small-frame case, where one 64-pixel pixel tile per wavefront would
+// leave most of the chip idle).
 //
 // One wavefront owns one output row of one frame for 64 output channels
 // (lane = output channel, one accumulator register per output pixel).  The
@@ -360,7 +361,6 @@ int launch_rows_t(const ConvArgs& a, hipStream_t stream) {
 
 template <typename TIn, typename TOut>
 int launch_rows_d(const ConvArgs& a, hipStream_t stream) {
-  if (a.w_out == 56) return a.cwp == 1 ? launch_rows_t<TIn, TOut, 56, 1>(a, stream) : launch_rows_t<TIn, TOut, 56, 2>(a, stream);
   return a.cwp == 1 ? launch_rows_t<TIn, TOut, 32, 1>(a, stream) : launch_rows_t<TIn, TOut, 32, 2>(a, stream);
 }
 
@@ -383,7 +383,7 @@ int num_cus() {
 
 bool rows_applicable(const ConvArgs& a) {
   return a.k == 3 && a.s == 1 && a.p == 1 && a.c_in <= 64 && a.cwp <= 2 && a.h_out == a.h_in &&
-         a.w_out == a.w_in && (a.w_out == 56 || a.w_out == 32) && a.n * (int64_t)a.h_out < (1ll << 30) &&
+         a.w_out == a.w_in && a.w_out == 32 && a.n * (int64_t)a.h_out < (1ll << 30) &&
          (int64_t)a.c_in * 9 * 64 * 4 <= kMaxLdsBytes;
 }
 

@@ -1,0 +1,151 @@
+"""Pixel-tile Stage 2 for 3x3 convolutions (stride 1 or 2, padding 1, C_out % 4 == 0).
+
+Same bar as the gather kernel: fp32 within 1e-4 abs + 1e-4 rel of float64
+F.conv2d on the spike-masked input, fp16/bf16 within 1e-2, bit-identical
+repeats.  Every case also checks which Stage-2 kernel produced the result:
+weights resident for C_in <= 64, streamed in 32-channel chunks through two
+LDS buffers beyond.
+"""
+
+import pytest
+import torch
+
+from oracle import conv as oconv
+from sparseflow_amd import _lib
+from sparseflow_amd.Kernels.conv2d import sparse_conv2d_forward
+from tests.gpu_helpers import DEV, announce, close, native_loaded, spikes
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = dict(atol=1e-4, rtol=1e-4)
+
+
+def _weights(c_out, c_in, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(c_out, c_in, 3, 3, generator=g) * (2.0 / (c_in * 9)) ** 0.5
+
+
+def _run(x, w, b, stride, **kw):
+    """sparse_conv2d_forward with kernel timing on; returns (y, kernels)."""
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        y = sparse_conv2d_forward(x, w, b, kernel_size=3, stride=stride, padding=1, **kw)[0]
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return y, {k: c for k, (c, _) in stats.items() if c > 0}
+
+
+CASES = [
+    # (N, C_in, H, W, C_out, stride); stride-1 frames of width 32 / 28 / 14
+    # go to the row kernels and are covered by their own tests.
+    (4, 64, 56, 56, 64, 1),     # ResNet50 layer1 conv2 shape (resident weights)
+    (8, 64, 30, 30, 64, 1),     # config-1-like, width 30
+    (4, 128, 27, 27, 128, 1),   # layer2-like (four chunks, streamed)
+    (3, 256, 13, 13, 256, 1),   # layer3-like (eight chunks)
+    (2, 512, 7, 7, 128, 1),     # layer4 conv2 (16 chunks, 49-pixel planes)
+    (2, 128, 56, 56, 128, 2),   # layer2.0 conv2, stride 2
+    (2, 256, 28, 28, 64, 2),    # layer3.0 conv2, stride 2
+    (2, 512, 14, 14, 64, 2),    # layer4.0 conv2, stride 2
+    (2, 64, 15, 13, 8, 2),      # odd input, stride 2
+    (2, 1, 5, 7, 4, 1),         # one channel
+    (3, 17, 1, 56, 12, 1),      # single row
+    (2, 33, 7, 9, 68, 1),       # two words, second nearly empty; ragged second group
+    (1, 300, 6, 10, 100, 1),    # last chunk partially filled
+    (17, 96, 8, 8, 64, 1),      # one tile per frame, passes past the end
+    (2, 48, 3, 100, 20, 1),     # tiles spanning rows
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("density", [0.0, 0.01, 0.3])
+def test_px3_fp32_matches_dense(case, density):
+    N, C, H, W, Co, s = case
+    announce(f"px3 {case} p={density}")
+    x = spikes((N, C, H, W), density, seed=N * 11 + C + s)
+    w = _weights(Co, C, seed=C + Co)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(3)) * 0.1
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV), s)
+    assert "conv_px3" in kernels and "conv_gather" not in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, s, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    assert native_loaded()
+
+
+@pytest.mark.parametrize("stride", [1, 2])
+def test_px3_dense_input(stride):
+    x = spikes((2, 96, 12, 12), 0.9, seed=21)
+    w = _weights(64, 96, seed=22)
+    announce(f"px3 dense s{stride}")
+    y, kernels = _run(x.to(DEV), w.to(DEV), None, stride)
+    assert "conv_px3" in kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, stride, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_px3_all_ones_input():
+    x = torch.ones(2, 64, 6, 56)
+    w = _weights(64, 64, seed=9)
+    announce("px3 all-ones")
+    y, kernels = _run(x.to(DEV), w.to(DEV), None, 1)
+    assert "conv_px3" in kernels
+    ok, err, _ = close(y, oconv.conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("stride", [1, 2])
+def test_px3_value_path_only_where_flagged(stride):
+    g = torch.Generator().manual_seed(4)
+    x = spikes((3, 96, 32, 32), 0.05, seed=6)
+    x[1, :, 10:12] = x[1, :, 10:12] * torch.randn(96, 2, 32, generator=g)
+    x[2, 5, 31, 31] = -2.5
+    x[0, 0, 0, 0] = 3e-7       # below the activity threshold: dropped
+    w = _weights(64, 96, seed=10)
+    announce(f"px3 value path s{stride}")
+    y, kernels = _run(x.to(DEV), w.to(DEV), None, stride)
+    assert "conv_px3" in kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, stride, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_px3_half_activations(dtype):
+    x = spikes((4, 128, 13, 13), 0.05, seed=11)
+    x[0, :, 3] = x[0, :, 3] * 0.5   # a value-path chunk in reduced precision
+    w = _weights(128, 128, seed=12)
+    b = torch.linspace(-0.5, 0.5, 128)
+    announce(f"px3 {dtype}")
+    xr = x.to(dtype).float()
+    y, kernels = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), 1)
+    assert "conv_px3" in kernels and y.dtype == dtype
+    ok, err, _ = close(y, oconv.conv2d_ref(xr, w, b, 1, 1), atol=1e-2, rtol=1e-2)
+    assert ok, f"max abs err {err}"
+    y32, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), 1, output_dtype=torch.float32)
+    assert y32.dtype == torch.float32
+    ok, err, _ = close(y32, oconv.conv2d_ref(xr, w, b, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_px3_deterministic_bitwise():
+    x = spikes((16, 64, 56, 56), 0.02, seed=13).to(DEV)
+    w = _weights(64, 64, seed=14).to(DEV)
+    announce("px3 determinism")
+    y1, _ = _run(x, w, None, 1)
+    y2, _ = _run(x, w, None, 1)
+    assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("stride", [1, 2])
+def test_px3_and_gather_agree(stride):
+    # C_out = 6 is not a multiple of 4, so the same input goes through the
+    # gather kernel; its channels match the pixel kernel's first six.
+    x = spikes((4, 80, 12, 20), 0.03, seed=15)
+    w = _weights(8, 80, seed=16)
+    announce(f"px3 vs gather s{stride}")
+    y_px, k1 = _run(x.to(DEV), w.to(DEV), None, stride)
+    y_gather, k2 = _run(x.to(DEV), w[:6].contiguous().to(DEV), None, stride)
+    assert "conv_px3" in k1 and "conv_gather" in k2
+    assert torch.allclose(y_px[:, :6], y_gather, atol=1e-5, rtol=1e-5)

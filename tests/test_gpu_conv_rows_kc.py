@@ -45,7 +45,7 @@ CASES = [
     (4, 256, 14, 14, 256),  # ResNet50 layer3 conv2 shape (8 chunks)
     (3, 64, 28, 28, 64),    # two chunks: resident, no barriers
     (2, 1, 27, 28, 4),      # one channel, odd height (last tile one row)
-    (2, 64, 13, 14, 64),    # odd plane size (13*14 % 4 != 0): falls back to the gather kernel
+    (2, 64, 13, 14, 64),    # odd plane size (13*14 % 4 != 0): goes to the pixel-tile kernel
     (5, 96, 10, 14, 100),   # three chunks, last tile two rows, ragged group
     (2, 33, 2, 14, 64),     # two-row frames: one tile per frame
     (1, 300, 14, 14, 64),   # last chunk partially filled
@@ -62,7 +62,7 @@ def test_rows_kc_fp32_matches_dense(case, density):
     w = _weights(Co, C, seed=C + Co)
     b = torch.randn(Co, generator=torch.Generator().manual_seed(3)) * 0.1
     y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV))
-    expect = "conv_gather" if (H * W) % 4 else "conv_rows_kc"
+    expect = "conv_px3" if (H * W) % 4 else "conv_rows_kc"
     assert expect in kernels and len(kernels) == 2, kernels  # prescan_pack + one conv kernel
     ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
     assert ok, f"max abs err {err}"
