@@ -230,6 +230,21 @@ def cpu_baseline(name, target_seconds=12.0):
     }
 
 
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch (fetched + written) of `kernel` on `workload` as
+    measured by the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes, or
+    None when no profile of that kernel is committed."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(workload, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+    if not rec:
+        return None
+    return int(rec["fetch_bytes"]) + int(rec["write_bytes"])
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,7 +315,7 @@ def main():
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": measured_traffic(args.workload, dom),
         "avg_launch_us": round(kus[dom], 2),
         "alg_bytes_per_launch": dom_bytes,
     }
