@@ -170,7 +170,7 @@ int sf_conv_lif_forward(const sf_conv_desc* desc, int32_t T, const void* x,
  * hipEvent pair on its stream.  sf_timing_collect synchronises those events
  * and accumulates per-kernel totals; sf_timing_query reads them by name
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
- * "conv_rows_kc", "conv_flat", "conv_px3").
+ * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

@@ -265,7 +265,7 @@ def conv_lif_forward(desc: ConvDesc, T: int, x: torch.Tensor, wt: torch.Tensor, 
 # Per-kernel timing (bench instrumentation)
 # ---------------------------------------------------------------------------
 
-KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3")
+KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3")
 
 
 def timing_enable(on: bool) -> None:

@@ -193,7 +193,7 @@ std::vector<TimingRec> g_pending;
 double g_total_ms[sf::K_COUNT] = {};
 int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
-                                     "conv_rows_kc", "conv_flat", "conv_px3"};
+                                     "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3"};
 
 }  // namespace
 
@@ -416,6 +416,11 @@ int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const f
   a.v_reset = lif->v_reset;
   a.hard_reset = lif->hard_reset != 0;
   a.decay_input = lif->decay_input != 0;
+  if (sf::px3_applicable(a)) {
+    rc = sf::launch_conv_lif_px3(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
+    if (rc != hipSuccess) return hip_fail(rc, "conv_lif_px3 launch");
+    return SF_OK;
+  }
   rc = sf::launch_conv_lif(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "conv_lif launch");
   return SF_OK;

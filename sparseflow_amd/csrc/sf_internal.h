@@ -102,6 +102,9 @@ int launch_conv_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t
 // Pixel-tile Stage 2 for 3x3 convolutions (stride 1 or 2, C_out % 4 == 0).
 bool px3_applicable(const ConvArgs& a);
 int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+// Fused conv + multi-step LIF on the pixel-tile formulation (3x3 s1; same
+// applicability as px3_applicable with stride 1).
+int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
@@ -109,7 +112,7 @@ void conv_geometry(ConvArgs& a, bool lif);
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_COUNT = 8 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_COUNT = 9 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

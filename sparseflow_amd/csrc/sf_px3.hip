@@ -30,45 +30,64 @@ namespace sf {
 
 namespace {
 
-constexpr int kPx3Ch = 32;                              // input channels per chunk (one bitmap word)
-constexpr int kPx3Rows = kPx3Ch * 9;                    // weight rows per chunk
-constexpr int kPx3Pieces = 17;                          // 16-byte pieces per padded row (16 + pad)
-constexpr int kPx3Units = (kPx3Rows * kPx3Pieces + 63) / 64;  // 1 KB load units per chunk (77)
-constexpr int kPx3ChunkBytes = kPx3Units * 1024;        // 77 KB
+constexpr int kPx3Ch = 32;               // input channels per chunk (one bitmap word)
+constexpr int kPx3Rows = kPx3Ch * 9;     // weight rows per chunk
 
-// Direct-to-LDS loads of weight chunk c.  The chunk is an array of 16-byte
-// pieces, row r piece s at position 17 r + s (position 17 r + 16 is padding).
-// Unit u fills positions 64 u .. 64 u + 63, lane l position 64 u + l.  Pads,
-// rows past C_in and channels past C_out read a valid but unrelated address
-// whose values are never used.
+// LDS layout of a chunk for a workgroup slice of CO output channels.
+//  CO = 64: rows of 16 pieces (16 bytes = 4 channels) padded to 17 pieces
+//           (272 bytes), read at immediate offsets.
+//  CO = 32: rows of 8 pieces (128 bytes), piece s of row r stored at
+//           position s ^ ((r >> 1) & 7) so that lanes reading different rows
+//           spread over the banks without padding (the whole 128-channel
+//           config-4 layer stays resident).
+template <int CO>
+struct Px3Layout {
+  static constexpr int pieces = CO / 4;                         // logical pieces per row
+  static constexpr int stride = CO == 64 ? 17 : pieces;         // pieces per row in LDS
+  static constexpr int units = (kPx3Rows * stride + 63) / 64;   // 1 KB load units per chunk
+  static constexpr int chunk_bytes = units * 1024;
+  static constexpr int resident_chunks = kMaxLdsBytes / chunk_bytes;  // chunks that fit at once
+};
+
+// Direct-to-LDS loads of weight chunk c (output channels co0 .. co0+CO-1).
+// The chunk is an array of 16-byte positions; unit u fills positions
+// 64 u .. 64 u + 63, lane l position 64 u + l.  Pads, rows past C_in and
+// channels past C_out read a valid but unrelated address whose values are
+// never used.
+template <int CO>
 __device__ __forceinline__ void load_chunk_px3(char* buf, const float* __restrict__ wt, int c, int krows,
                                                int c_out, int co0, int wave, int lane) {
+  typedef Px3Layout<CO> L;
 #pragma unroll
-  for (int j = 0; j < (kPx3Units + kRowsWaves - 1) / kRowsWaves; ++j) {
+  for (int j = 0; j < (L::units + kRowsWaves - 1) / kRowsWaves; ++j) {
     const int u = wave + kRowsWaves * j;
-    if (u < kPx3Units) {
+    if (u < L::units) {
       const int pos = u * 64 + lane;
-      const int r = pos / kPx3Pieces;
-      const int s = pos - r * kPx3Pieces;
+      const int r = pos / L::stride;
+      const int q = pos - r * L::stride;
+      const int s = CO == 64 ? q : (q ^ ((r >> 1) & 7));  // logical piece stored at position q
       const int row = c * kPx3Rows + r;
       const int col = co0 + 4 * s;
       const float* src =
-          (s < 16 && r < kPx3Rows && row < krows && col < c_out) ? wt + (int64_t)row * c_out + col : wt;
+          (q < L::pieces && r < kPx3Rows && row < krows && col < c_out) ? wt + (int64_t)row * c_out + col : wt;
       __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
     }
   }
 }
 
-// Add padded weight row r of the chunk, times xv, to the 64 accumulators.
-__device__ __forceinline__ void px3_add_row(float (&acc)[64], const char* chunk, int r, float xv) {
-  static_assert(kPx3Pieces * 16 == 272, "row stride is 256 + 16 bytes");
-  const float4* rp = reinterpret_cast<const float4*>(chunk + (r << 8) + (r << 4));
+// Add weight row r of the chunk, times xv, to the CO accumulators.
+template <int CO>
+__device__ __forceinline__ void px3_add_row(float (&acc)[CO], const char* chunk, int r, float xv) {
+  typedef Px3Layout<CO> L;
+  const char* rowp = chunk + (r * L::stride) * 16;
+  const int key = CO == 64 ? 0 : ((r >> 1) & 7) << 4;
 #pragma unroll
-  for (int s = 0; s < 16; ++s) {
+  for (int s = 0; s < L::pieces; ++s) {
     // Groups of four pieces: the scheduler may not hoist more than 16
-    // loaded registers ahead of their use (the accumulators take 64).
+    // loaded registers ahead of their use (the accumulators take CO).
     if (s % 4 == 0) __builtin_amdgcn_sched_barrier(0);
-    const float4 v = rp[s];
+    const float4 v = CO == 64 ? reinterpret_cast<const float4*>(rowp)[s]
+                              : *reinterpret_cast<const float4*>(rowp + ((s << 4) ^ key));
     acc[4 * s] = fmaf(xv, v.x, acc[4 * s]);
     acc[4 * s + 1] = fmaf(xv, v.y, acc[4 * s + 1]);
     acc[4 * s + 2] = fmaf(xv, v.z, acc[4 * s + 2]);
@@ -110,19 +129,60 @@ __device__ __forceinline__ void px3_load_words(uint32_t (&w)[9], const uint32_t*
   }
 }
 
-template <typename TOut>
-__device__ __forceinline__ void px3_store(const float (&acc)[64], TOut* __restrict__ yp, int hw, int nco) {
-  if (nco >= 64) {
+template <int CO, typename TOut>
+__device__ __forceinline__ void px3_store(const float (&acc)[CO], TOut* __restrict__ yp, int hw, int nco) {
+  if (nco >= CO) {
 #pragma unroll
-    for (int co = 0; co < 64; ++co) yp[(int64_t)co * hw] = from_f32<TOut>(acc[co]);
+    for (int co = 0; co < CO; ++co) yp[(int64_t)co * hw] = from_f32<TOut>(acc[co]);
   } else {
 #pragma unroll
-    for (int co = 0; co < 64; ++co)
+    for (int co = 0; co < CO; ++co)
       if (co < nco) yp[(int64_t)co * hw] = from_f32<TOut>(acc[co]);
   }
 }
 
-template <typename TIn>
+// Multi-step LIF on the accumulators.  The membrane lives in the accumulator
+// registers between steps, stored in the form that the next step's taps are
+// added to:
+//   decay_input:  acc = (tau - 1) V + V_r + b + sum  ->  H = acc / tau
+//   otherwise:    acc = (1 - 1/tau) V + V_r / tau + b + sum  ->  H = acc
+// (the same H as V + (I - (V - V_r)) / tau, resp. V - (V - V_r) / tau + I,
+// with I = b + sum, up to rounding).
+struct LifCoef {
+  float a, vr_term, inv_tau, v_th, v_reset;
+  bool hard, decay_input;
+};
+
+template <int CO>
+__device__ __forceinline__ void lif_seed(float (&acc)[CO], const LifCoef& L, const float* __restrict__ bias, int co0,
+                                         int c_out) {
+  if (bias != nullptr) {
+    // Channels past C_out read the last bias (never stored).
+#pragma unroll
+    for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], L.vr_term + bias[min(co0 + co, c_out - 1)]);
+  } else {
+#pragma unroll
+    for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], L.vr_term);
+  }
+}
+
+// H, spike and reset of one step: the spike of channel co goes straight to
+// sp[co * hw] (when the lane's pixel exists), the new membrane stays in acc.
+template <int CO, typename TOut>
+__device__ __forceinline__ void lif_step(float (&acc)[CO], const LifCoef& L, TOut* __restrict__ sp, int hw, int nco,
+                                         bool mine) {
+#pragma unroll
+  for (int co = 0; co < CO; ++co) {
+    const float h = L.decay_input ? acc[co] * L.inv_tau : acc[co];
+    const bool fire = h >= L.v_th;
+    if (mine && co < nco) sp[(int64_t)co * hw] = from_f32<TOut>(fire ? 1.f : 0.f);
+    acc[co] = L.hard ? (fire ? L.v_reset : h) : h - (fire ? L.v_th : 0.f);
+  }
+}
+
+// TOut is the spike type of the fused LIF kernel; the plain conv kernel
+// takes its output type at run time (out_dtype) and ignores TOut.
+template <typename TIn, typename TOut, int CO, bool LIF>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const uint32_t* __restrict__ bits,
                                                               const uint32_t* __restrict__ flags,
                                                               const TIn* __restrict__ x,
@@ -130,26 +190,39 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
                                                               const float* __restrict__ bias_p,
                                                               void* __restrict__ y, int groups, int nchunks,
                                                               int out_dtype) {
+  typedef Px3Layout<CO> LY;
   extern __shared__ __align__(16) char smem[];
   const int lane0 = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = blockIdx.x % groups;
-  const int co0 = grp * 64;
+  const int co0 = grp * CO;
   const int krows = a.c_in * 9;
   const int hwo = a.hw_out;
   const int tpf = (hwo + 63) / 64;
-  const int total = (int)a.n * tpf;
+  const int total = (int)a.n * tpf;   // LIF: a.n = samples, the T steps run inside a tile
   const int nblk = (int)(gridDim.x / groups);
-  const bool resident = nchunks <= 2;
+  const bool resident = nchunks <= LY::resident_chunks;
+  const int steps = LIF ? a.T : 1;
+  LifCoef L;
+  L.inv_tau = 1.f / a.tau;
+  L.decay_input = a.decay_input != 0;
+  L.hard = a.hard_reset != 0;
+  L.v_th = a.v_th;
+  L.v_reset = a.v_reset;
+  {
+    const float vr = L.hard ? a.v_reset : 0.f;
+    L.a = L.decay_input ? a.tau - 1.f : 1.f - L.inv_tau;
+    L.vr_term = L.decay_input ? vr : vr * L.inv_tau;
+  }
 
   if (resident) {
     for (int c = 0; c < nchunks; ++c)
-      load_chunk_px3(smem + c * kPx3ChunkBytes, wt, c, krows, a.c_out, co0, wave, lane0);
+      load_chunk_px3<CO>(smem + c * LY::chunk_bytes, wt, c, krows, a.c_out, co0, wave, lane0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  // Passes of kRowsWaves tiles.  With more than two chunks every wavefront
-  // takes part in every barrier, including those of a pass past the end.
+  // Passes of kRowsWaves tiles.  With streamed chunks every wavefront takes
+  // part in every barrier, including those of a pass past the end.
   for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
     // Lane-dependent addresses are recomputed in every pass rather than kept
     // live across the loop (the accumulators need the registers).
@@ -157,8 +230,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
     asm volatile("" : "+v"(lane));
     const int t = pass * kRowsWaves + wave;
     const bool valid = t < total;
-    const int frame = valid ? t / tpf : 0;
-    const int p0 = valid ? (t - frame * tpf) * 64 : 0;
+    const int sample = valid ? t / tpf : 0;
+    const int p0 = valid ? (t - sample * tpf) * 64 : 0;
     const int npx = min(64, hwo - p0);
     const bool mine = valid && lane < npx;
     // This lane's output pixel and the top-left corner of its input window.
@@ -170,90 +243,120 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
     const float* __restrict__ bias_t = bias_p;
     int hwo_t = hwo, c_out_t = a.c_out;
     asm volatile("" : "+s"(bias_t), "+s"(hwo_t), "+s"(c_out_t));
-    float acc[64];
+    const int nco = min(CO, c_out_t - co0);
+    float acc[CO];
+    if constexpr (LIF) {
+      // Membrane before step 0: v_init or 0.
+      const float* vi = a.v_init;
 #pragma unroll
-    for (int co = 0; co < 64; ++co) acc[co] = (bias_t != nullptr && co0 + co < c_out_t) ? bias_t[co0 + co] : 0.f;
-    bool value = false;
-    if (valid) {
-      const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
-      value = rows_value_path(a, flags, frame, oh_a * a.s - 1, oh_b * a.s + 1);
-    }
-    const uint32_t* __restrict__ bf = bits + (int64_t)frame * a.hw_in * a.cwp;
-    const TIn* __restrict__ xf = x + (int64_t)frame * a.c_in * a.hw_in;
-    uint32_t wn[9];
-    if (mine) px3_load_words(wn, bf, a, ih0, iw0, 0);
-    if (!resident) {
-      __syncthreads();  // the previous pass is done with both buffers
-      load_chunk_px3(smem, wt, 0, krows, a.c_out, co0, wave, lane);
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-    }
-    for (int c = 0; c < nchunks; ++c) {
-      // Stream chunk c+1 into the other buffer; it was last read during
-      // chunk c-1, which every wavefront finished before the last barrier.
-      if (!resident && c + 1 < nchunks)
-        load_chunk_px3(smem + ((c + 1) & 1) * kPx3ChunkBytes, wt, c + 1, krows, a.c_out, co0, wave, lane);
-      if (mine) {
-        // This chunk's words were loaded during the previous chunk's walk;
-        // start the next chunk's loads now.
-        uint32_t w[9];
+      for (int co = 0; co < CO; ++co) acc[co] = 0.f;
+      if (vi != nullptr && mine) {
+        const float* vp = vi + ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
 #pragma unroll
-        for (int tp = 0; tp < 9; ++tp) w[tp] = wn[tp];
-        // Opaque to the optimiser: a select between two array elements would
-        // otherwise be folded into an indexed load, which keeps the array in
-        // scratch memory.
-        asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]),
-                     "+v"(w[7]), "+v"(w[8]));
-        if (c + 1 < nchunks) px3_load_words(wn, bf, a, ih0, iw0, c + 1);
-        uint32_t nz = 0u;
-#pragma unroll
-        for (int tp = 0; tp < 9; ++tp) nz |= (w[tp] != 0u ? 1u : 0u) << tp;
-        const char* chunk = smem + (c & 1) * kPx3ChunkBytes;
-        uint32_t m = 0u;
-        int tap = 0;
-        // Per-lane cursor over (tap, ci): the wavefront loops while any lane
-        // has spikes left.
-        while ((m | nz) != 0u) {
-          if (m == 0u) {
-            tap = __builtin_ctz(nz);
-            nz &= nz - 1u;
-            m = px3_select(w, tap);
-          }
-          const int bit = __builtin_ctz(m);
-          m &= m - 1u;
-          float xv = 1.f;
-          if (value) {
-            const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
-            xv = to_f32<TIn>(xf[(int64_t)(c * kPx3Ch + bit) * a.hw_in + ih * a.w_in + iw]);
-          }
-          px3_add_row(acc, chunk, bit * 9 + tap, xv);
-        }
+        for (int co = 0; co < CO; ++co)
+          if (co < nco) acc[co] = vp[(int64_t)co * hwo_t];
       }
+    } else {
+#pragma unroll
+      for (int co = 0; co < CO; ++co) acc[co] = (bias_t != nullptr && co0 + co < c_out_t) ? bias_t[co0 + co] : 0.f;
+    }
+    for (int st = 0; st < steps; ++st) {
+      const int64_t frame = LIF ? (int64_t)st * a.n + sample : sample;
+      if constexpr (LIF) lif_seed<CO>(acc, L, bias_t, co0, c_out_t);
+      bool value = false;
+      if (valid) {
+        const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
+        value = rows_value_path(a, flags, frame, oh_a * a.s - 1, oh_b * a.s + 1);
+      }
+      const uint32_t* __restrict__ bf = bits + frame * a.hw_in * a.cwp;
+      const TIn* __restrict__ xf = x + frame * a.c_in * a.hw_in;
+      uint32_t wn[9];
+      if (mine) px3_load_words(wn, bf, a, ih0, iw0, 0);
       if (!resident) {
+        __syncthreads();  // the previous step/pass is done with both buffers
+        load_chunk_px3<CO>(smem, wt, 0, krows, a.c_out, co0, wave, lane);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
       }
+      for (int c = 0; c < nchunks; ++c) {
+        // Stream chunk c+1 into the other buffer; it was last read during
+        // chunk c-1, which every wavefront finished before the last barrier.
+        if (!resident && c + 1 < nchunks)
+          load_chunk_px3<CO>(smem + ((c + 1) & 1) * LY::chunk_bytes, wt, c + 1, krows, a.c_out, co0, wave, lane);
+        if (mine) {
+          // This chunk's words were loaded during the previous chunk's walk;
+          // start the next chunk's loads now.
+          uint32_t w[9];
+#pragma unroll
+          for (int tp = 0; tp < 9; ++tp) w[tp] = wn[tp];
+          // Opaque to the optimiser: a select between two array elements
+          // would otherwise be folded into an indexed load, which keeps the
+          // array in scratch memory.
+          asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]),
+                       "+v"(w[7]), "+v"(w[8]));
+          if (c + 1 < nchunks) px3_load_words(wn, bf, a, ih0, iw0, c + 1);
+          uint32_t nz = 0u;
+#pragma unroll
+          for (int tp = 0; tp < 9; ++tp) nz |= (w[tp] != 0u ? 1u : 0u) << tp;
+          const char* chunk = smem + (resident ? c : (c & 1)) * LY::chunk_bytes;
+          uint32_t m = 0u;
+          int tap = 0;
+          // Per-lane cursor over (tap, ci): the wavefront loops while any
+          // lane has spikes left.
+          while ((m | nz) != 0u) {
+            if (m == 0u) {
+              tap = __builtin_ctz(nz);
+              nz &= nz - 1u;
+              m = px3_select(w, tap);
+            }
+            const int bit = __builtin_ctz(m);
+            m &= m - 1u;
+            float xv = 1.f;
+            if (value) {
+              const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+              xv = to_f32<TIn>(xf[(int64_t)(c * kPx3Ch + bit) * a.hw_in + ih * a.w_in + iw]);
+            }
+            px3_add_row<CO>(acc, chunk, bit * 9 + tap, xv);
+          }
+        }
+        if (!resident) {
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+        }
+      }
+      if constexpr (LIF) {
+        // H, spike and the reset; the spikes of this step are stored now and
+        // the membrane stays in acc.
+        const int64_t sb = (frame * c_out_t + co0) * hwo_t + p0 + lane;
+        lif_step<CO>(acc, L, static_cast<TOut*>(y) + sb, hwo_t, nco, mine);
+      }
     }
     if (mine) {
-      const int64_t yb = ((int64_t)frame * c_out_t + co0) * hwo_t + p0 + lane;
-      const int nco = min(64, c_out_t - co0);
-      if (out_dtype == SF_F16) px3_store(acc, static_cast<__half*>(y) + yb, hwo_t, nco);
-      else if (out_dtype == SF_BF16) px3_store(acc, static_cast<__hip_bfloat16*>(y) + yb, hwo_t, nco);
-      else px3_store(acc, static_cast<float*>(y) + yb, hwo_t, nco);
+      if constexpr (LIF) {
+        const int64_t vb = ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
+        px3_store<CO>(acc, a.v_out + vb, hwo_t, nco);
+      } else {
+        const int64_t yb = ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
+        if (out_dtype == SF_F16) px3_store<CO>(acc, static_cast<__half*>(y) + yb, hwo_t, nco);
+        else if (out_dtype == SF_BF16) px3_store<CO>(acc, static_cast<__hip_bfloat16*>(y) + yb, hwo_t, nco);
+        else px3_store<CO>(acc, static_cast<float*>(y) + yb, hwo_t, nco);
+      }
     }
   }
 }
 
-template <typename TIn>
+template <typename TIn, typename TOut, int CO, bool LIF>
 int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
-  const int groups = (a.c_out + 63) / 64;
+  typedef Px3Layout<CO> LY;
+  const int groups = (a.c_out + CO - 1) / CO;
   const int nchunks = (a.c_in + kPx3Ch - 1) / kPx3Ch;
-  const size_t lds = (size_t)(nchunks < 2 ? nchunks : 2) * kPx3ChunkBytes;
+  const int held = nchunks <= LY::resident_chunks ? nchunks : 2;
+  const size_t lds = (size_t)held * LY::chunk_bytes;
   const int64_t tiles = a.n * (int64_t)((a.hw_out + 63) / 64);
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_px3<TIn>;
+  auto kern = k_conv_px3<TIn, TOut, CO, LIF>;
   static bool attr_done = false;
   if (!attr_done) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -265,6 +368,31 @@ int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
+int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  if (in_dtype == SF_F16) return launch_px3_t<__half, float, 64, false>(a, out_dtype, stream);
+  if (in_dtype == SF_BF16) return launch_px3_t<__hip_bfloat16, float, 64, false>(a, out_dtype, stream);
+  return launch_px3_t<float, float, 64, false>(a, out_dtype, stream);
+}
+
+// Fused LIF: 32 output channels per workgroup.  The membrane shares the
+// accumulator registers, and with 32 channels the weights of up to 128 input
+// channels stay resident (config 4) and a sample's tiles spread over twice
+// as many workgroups.
+template <typename TIn, typename TOut>
+int launch_px3_lif_t(const ConvArgs& a, hipStream_t stream) {
+  return launch_px3_t<TIn, TOut, 32, true>(a, 0, stream);
+}
+
+int launch_px3_lif(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  // Spike dtype: the input's, or f32 (the combinations sf_conv_lif_forward accepts).
+  if (in_dtype == SF_F16)
+    return out_dtype == SF_F32 ? launch_px3_lif_t<__half, float>(a, stream) : launch_px3_lif_t<__half, __half>(a, stream);
+  if (in_dtype == SF_BF16)
+    return out_dtype == SF_F32 ? launch_px3_lif_t<__hip_bfloat16, float>(a, stream)
+                               : launch_px3_lif_t<__hip_bfloat16, __hip_bfloat16>(a, stream);
+  return launch_px3_lif_t<float, float>(a, stream);
+}
+
 }  // namespace
 
 bool px3_applicable(const ConvArgs& a) {
@@ -274,10 +402,15 @@ bool px3_applicable(const ConvArgs& a) {
 
 int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
   timing_begin(K_PX3, stream);
-  const int rc = in_dtype == SF_F16    ? launch_px3_t<__half>(a, out_dtype, stream)
-                 : in_dtype == SF_BF16 ? launch_px3_t<__hip_bfloat16>(a, out_dtype, stream)
-                                       : launch_px3_t<float>(a, out_dtype, stream);
+  const int rc = launch_px3_conv(a, in_dtype, out_dtype, stream);
   timing_end(K_PX3, stream);
+  return rc;
+}
+
+int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  timing_begin(K_LIF_PX3, stream);
+  const int rc = launch_px3_lif(a, in_dtype, out_dtype, stream);
+  timing_end(K_LIF_PX3, stream);
   return rc;
 }
 

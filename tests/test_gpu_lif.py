@@ -149,3 +149,55 @@ def test_config4_full_size_sampled():
         assert bad == 0
         if comparable[-1, 0]:
             assert abs(v_c[n, co, oh, ow] - v_ref[0]) <= 1e-4 + 1e-4 * abs(v_ref[0])
+
+
+def _lif_kernels(fn):
+    from sparseflow_amd import _lib
+
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        out = fn()
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return out, {k: c for k, (c, _) in stats.items() if c > 0}
+
+
+PX_LIF_CASES = [
+    # (T, N, C, H, W, Co, density, v_reset, decay_input, gain): 3x3 with C_out % 4 == 0 runs the pixel-tile kernel
+    (4, 2, 64, 16, 16, 64, 0.05, 0.0, True, 1.0),     # two chunks
+    (3, 3, 128, 14, 14, 128, 0.03, 0.0, True, 3.0),   # config-4 channel counts: four chunks resident
+    (3, 2, 160, 9, 9, 64, 0.1, 0.0, False, 1.0),      # five chunks: streamed through two LDS buffers
+    (5, 2, 33, 7, 11, 36, 0.1, None, True, 2.0),      # soft reset, ragged channel group, odd plane
+    (2, 1, 1, 5, 5, 4, 0.5, -0.3, True, 6.0),         # one input channel
+]
+
+
+@pytest.mark.parametrize("case", PX_LIF_CASES)
+def test_fused_lif_pixel_kernel(case):
+    T, N, C, H, W, Co, dens, v_reset, decay_input, gain = case
+    announce(f"lif px3 {case}")
+    x = spikes((T, N, C, H, W), dens, seed=T * 10 + C)
+    g = torch.Generator().manual_seed(C + Co)
+    w = torch.randn(Co, C, 3, 3, generator=g) * (4.0 / (C * 9)) ** 0.5 * gain
+    b = torch.randn(Co, generator=g) * 0.2
+    (spk, v, _), kernels = _lif_kernels(lambda: sparse_fused_conv_lif_multistep(
+        x.to(DEV), w.to(DEV), b.to(DEV), tau=2.0, v_threshold=1.0, v_reset=v_reset, decay_input=decay_input))
+    assert "conv_lif_px3" in kernels and "conv_lif" not in kernels, kernels
+    assert spk.float().mean() > 0.0
+    _check(spk, v, x, w, b, 3, 2.0, 1.0, v_reset, decay_input)
+
+
+def test_fused_lif_pixel_kernel_value_path():
+    # Non-binary inputs in one sample's step: that tile multiplies by x.
+    T, N, C, H, W, Co = 3, 2, 64, 10, 10, 64
+    x = spikes((T, N, C, H, W), 0.1, seed=17)
+    x[1, 0, :, 2:4] = x[1, 0, :, 2:4] * torch.rand(C, 2, W, generator=torch.Generator().manual_seed(18)) * 2
+    w = torch.randn(Co, C, 3, 3, generator=torch.Generator().manual_seed(19)) * 0.3
+    announce("lif px3 value path")
+    (spk, v, _), kernels = _lif_kernels(lambda: sparse_fused_conv_lif_multistep(x.to(DEV), w.to(DEV), None))
+    assert "conv_lif_px3" in kernels
+    _check(spk, v, x, w, None, 3, 2.0, 1.0, 0.0, True)
