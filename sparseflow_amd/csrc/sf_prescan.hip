@@ -57,24 +57,36 @@ __device__ __forceinline__ void load_vec(const T* p, float (&v)[VEC]) {
 }
 
 // One wavefront packs one chunk of 64*VEC consecutive pixels of one frame
-// over a contiguous range of bitmap words (all words when csplit == 1).  The
-// four wavefronts of a block cover 4/csplit chunks.
+// over a contiguous range of bitmap words (all words when csplit == 1).  A
+// block has max(4, csplit) wavefronts and covers max(4, csplit)/csplit
+// chunks.
+// Bitmap words of a block's chunks staged in LDS when they fit, so that each
+// chunk's words leave as one contiguous run of 128-bit stores instead of
+// per-pixel scattered words.
+constexpr int kPackStageWords = 4 * 256 * 2;  // 4 chunks x 256 pixels x 2 words (or fewer chunks x more words)
+
 template <typename T, int VEC, bool ALIGNED>
-__global__ __launch_bounds__(256) void k_pack(PackArgs a) {
-  __shared__ uint32_t s_nb[4];
+__global__ __launch_bounds__(512) void k_pack(PackArgs a) {
+  __shared__ uint32_t s_nb[8];
+  __shared__ __align__(16) uint32_t s_words[kPackStageWords];
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
   const int csplit = a.csplit;
+  const int cpb = (int)(blockDim.x >> 6) / csplit;  // chunks per block
   const int lc = wave / csplit;
   const int sp = wave - lc * csplit;
-  const int64_t gchunk = (int64_t)blockIdx.x * (4 / csplit) + lc;
+  const int64_t gchunk = (int64_t)blockIdx.x * cpb + lc;
   const bool chunk_ok = gchunk < a.total_chunks;
   const float cut = a.cutoff;
   uint32_t nb = 0;
 
+  // Staging: chunk lc of the block owns s_words[lc * chunk * cwp ...].
+  const bool stage = cpb * 64 * VEC * a.cwp <= kPackStageWords;
+  uint32_t* sw = s_words + lc * (64 * VEC) * a.cwp;
+  int64_t frame = 0, chk = 0;
   if (chunk_ok) {
-    const int64_t frame = gchunk / a.chunks_per_frame;
-    const int64_t chk = gchunk - frame * a.chunks_per_frame;
+    frame = gchunk / a.chunks_per_frame;
+    chk = gchunk - frame * a.chunks_per_frame;
     const int p0 = (int)(chk * (64 * VEC)) + lane * VEC;
     if (p0 < a.hw) {
       const int wps = a.cwp / csplit;
@@ -111,7 +123,10 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
             }
           }
         }
-        if (a.cwp == 1) {
+        if (stage) {
+#pragma unroll
+          for (int i = 0; i < VEC; ++i) sw[(lane * VEC + i) * a.cwp + cw] = word[i];
+        } else if (a.cwp == 1) {
           if constexpr (VEC == 4) {
             *reinterpret_cast<uint4*>(bf) = make_uint4(word[0], word[1], word[2], word[3]);
           } else if constexpr (VEC == 2) {
@@ -130,6 +145,20 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
   const uint64_t bal = __ballot(nb != 0u);
   if (lane == 0) s_nb[wave] = bal != 0ull ? 1u : 0u;
   __syncthreads();
+  if (stage && chunk_ok) {
+    // The chunk's pixels p0 .. p0+npx-1 take npx * cwp consecutive words of
+    // the bitmap; its csplit wavefronts copy them out, 4 words per lane.
+    const int p0 = (int)(chk * (64 * VEC));
+    const int nwords = min(64 * VEC, a.hw - p0) * a.cwp;
+    uint32_t* dst = a.bits + (frame * a.hw + p0) * (int64_t)a.cwp;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(dst) | (uintptr_t)nwords * 4) & 15) == 0;
+    if (vec_ok) {
+      for (int i = (sp * 64 + lane) * 4; i < nwords; i += csplit * 64 * 4)
+        *reinterpret_cast<uint4*>(dst + i) = *reinterpret_cast<const uint4*>(sw + i);
+    } else {
+      for (int i = sp * 64 + lane; i < nwords; i += csplit * 64) dst[i] = sw[i];
+    }
+  }
   if (chunk_ok && sp == 0 && lane == 0) {
     uint32_t f = 0u;
     for (int q = 0; q < csplit; ++q) f |= s_nb[lc * csplit + q];
@@ -223,15 +252,16 @@ __global__ __launch_bounds__(256) void k_tiles(TilesArgs a) {
 
 template <typename T, int VEC>
 int launch_pack_t(const PackArgs& a, hipStream_t stream) {
-  const int cpb = 4 / a.csplit;
+  const int wpb = a.csplit > 4 ? a.csplit : 4;
+  const int cpb = wpb / a.csplit;
   const int64_t blocks = (a.total_chunks + cpb - 1) / cpb;
   if (blocks == 0) return (int)hipSuccess;
   const uintptr_t align = (uintptr_t)a.x;
   const bool aligned = (align % (sizeof(T) * VEC)) == 0;
   if (aligned) {
-    hipLaunchKernelGGL((k_pack<T, VEC, true>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((k_pack<T, VEC, true>), dim3((unsigned)blocks), dim3(64 * wpb), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((k_pack<T, VEC, false>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((k_pack<T, VEC, false>), dim3((unsigned)blocks), dim3(64 * wpb), 0, stream, a);
   }
   return (int)hipGetLastError();
 }
@@ -269,7 +299,7 @@ PackPlan make_pack_plan(int64_t n, int c, int h, int w) {
     return n * cpf * cs;
   };
   int csplit = 1;
-  while (csplit < 4 && csplit < pl.cwp && (pl.cwp / csplit > 2 || waves_for(vec, csplit) < want_waves)) csplit <<= 1;
+  while (csplit < 8 && csplit < pl.cwp && (pl.cwp / csplit > 1 || waves_for(vec, csplit) < want_waves)) csplit <<= 1;
   while (vec > 1 && waves_for(vec, csplit) < want_waves / 4) vec >>= 1;
   pl.vec = vec;
   pl.chunk = 64 * vec;
