@@ -120,6 +120,7 @@ def bench_conv(name, steps, warmup, dev, with_miopen=True):
         kt = kernel_times(step, max(5, min(steps, 20)))
         miopen_ms = None
         if with_miopen:
+            log(f"[bench] {name}: sparse path timed; MIOpen baseline next")
             torch.backends.cudnn.benchmark = True
             wd = conv.weight.float()
             dense = lambda: torch.nn.functional.conv2d(x, wd, None, s, (k - 1) // 2)  # noqa: E731
@@ -162,6 +163,7 @@ def bench_lif(steps, warmup, dev, with_miopen=True):
         kt = kernel_times(step, max(5, min(steps, 20)))
         miopen_ms = None
         if with_miopen:
+            log(f"[bench] {name}: sparse path timed; MIOpen baseline next")
             torch.backends.cudnn.benchmark = True
             xf = x.reshape(T * N, C, H, W)
 
@@ -230,6 +232,67 @@ def cpu_baseline(name, target_seconds=12.0):
     }
 
 
+E2E_WORKLOAD = "resnet50_e2e"  # T=16, batch 32, 3x224x224, images/s
+
+
+def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
+    """Spiking-ResNet50 forward (random init, BN folded, multi-step LIF
+    tau=2 v_th=1 hard reset) through optimize(): images/s = batch / t."""
+    import copy
+
+    import sparseflow_amd as sf
+    from sparseflow_amd.Models import fold_bn_, spiking_resnet50
+    from sparseflow_amd.neuron import LIFNode, reset_net
+
+    t0 = time.time()
+    # The dense convs (stem, stride-2 downsamples, layer4) and the baseline
+    # use MIOpen's default algorithm choice; an exhaustive search over every
+    # layer shape at 512 frames takes minutes.
+    torch.backends.cudnn.benchmark = False
+    torch.manual_seed(0)
+    model = fold_bn_(spiking_resnet50(T=T)).to(dev)
+    dense = copy.deepcopy(model) if with_dense else None
+    g = torch.Generator(device=dev).manual_seed(0)
+    img = torch.randn(batch, 3, 224, 224, generator=g, device=dev)
+    sf.optimize(model, sample_input=img, verbose=False)
+    n_sparse = sum(type(m).__name__ == "SparseConv2d" for m in model.modules())
+    torch.cuda.synchronize()
+    log(f"[bench] e2e: model built and optimized ({n_sparse} sparse convs) in {time.time() - t0:.1f} s")
+
+    def run(m):
+        reset_net(m)
+        return m(img)
+
+    densities = {}
+    hooks = [mod.register_forward_hook(lambda _m, _i, o, n=name: densities.__setitem__(n, float(o.float().mean())))
+             for name, mod in model.named_modules() if isinstance(mod, LIFNode)]
+    with torch.no_grad():
+        out = run(model)
+    for h in hooks:
+        h.remove()
+    torch.cuda.synchronize()
+    log(f"[bench] e2e: first forward done at {time.time() - t0:.1f} s")
+    with torch.no_grad():
+        ms = time_gpu(lambda: run(model), steps, warmup)
+        log(f"[bench] e2e: {ms:.2f} ms per forward ({time.time() - t0:.1f} s)")
+        res = {
+            "workload": E2E_WORKLOAD, "T": T, "batch": batch, "ms_per_forward": ms,
+            "images_per_s": batch / (ms * 1e-3), "sparse_convs": n_sparse,
+            "mean_spike_density": sum(densities.values()) / max(1, len(densities)),
+            "spike_density_by_layer": {k: round(v, 5) for k, v in densities.items()},
+        }
+        if dense is not None:
+            ref = run(dense)
+            torch.cuda.synchronize()
+            log(f"[bench] e2e: dense first forward done at {time.time() - t0:.1f} s")
+            dms = time_gpu(lambda: run(dense), max(2, steps // 2), 1)
+            res["dense_ms_per_forward"] = dms
+            res["dense_images_per_s"] = batch / (dms * 1e-3)
+            res["speedup_vs_dense"] = dms / ms
+            res["max_abs_logit_diff_vs_dense"] = float((out - ref).abs().max())
+    return res
+
+
 def measured_traffic(workload, kernel):
     """HBM bytes per launch (fetched + written) of `kernel` on `workload` as
     measured by the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes, or
@@ -252,7 +315,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="resnet50_layer1_conv3x3", choices=sorted(WORKLOADS))
     ap.add_argument("--extra", default="all", help="'all', 'none' or comma-separated workload names (+ "
-                                                   f"{LIF_WORKLOAD})")
+                                                   f"{LIF_WORKLOAD}, {E2E_WORKLOAD})")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-miopen", action="store_true", help="skip the MIOpen baselines")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -289,7 +352,7 @@ def main():
     extra = {}
     names = []
     if args.extra == "all":
-        names = [n for n in WORKLOADS if n != args.workload] + [LIF_WORKLOAD]
+        names = [n for n in WORKLOADS if n != args.workload] + [LIF_WORKLOAD, E2E_WORKLOAD]
     elif args.extra != "none":
         names = [n.strip() for n in args.extra.split(",") if n.strip()]
     for name in names:
@@ -297,6 +360,8 @@ def main():
         steps = max(5, args.steps // 2)
         if name == LIF_WORKLOAD:
             r = bench_lif(steps, 3, dev, with_miopen=not args.no_miopen)
+        elif name == E2E_WORKLOAD:
+            r = bench_e2e(max(3, steps // 5), 2, dev, with_dense=not args.no_miopen)
         else:
             r = bench_conv(name, steps, 3, dev, with_miopen=not args.no_miopen)
         extra[name] = r

@@ -164,13 +164,27 @@ int sf_conv_lif_forward(const sf_conv_desc* desc, int32_t T, const void* x,
                         const float* v_init, void* spikes, float* v_out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- spiking neuron -------------------------------------------------------- */
+
+/* Multi-step LIF over T steps of m neurons: x [T, m] input currents (in_dtype),
+ * spikes [T, m] in out_dtype (in_dtype or f32), v_out [m] f32 = membrane after
+ * step T.  v_init [m] f32 may be NULL for V_0 = v_reset (hard reset) or 0
+ * (soft reset).  Same update as sf_conv_lif_forward, computed operation by
+ * operation without fused multiply-adds.  Replaces spikingjelly's multi-step
+ * LIFNode used between the convolutions of the reference's spiking models
+ * (Benchmark/bench_4test.py:166-197; update rule as restated in
+ * Ops/sparse_fused_conv_lif.py:283-292). */
+int sf_lif_multistep(const void* x, int32_t in_dtype, int32_t T, int64_t m,
+                     const sf_lif_params* lif, const float* v_init, void* spikes,
+                     int32_t out_dtype, float* v_out, void* stream);
+
 /* ---- per-kernel timing (bench instrumentation) --------------------------- */
 
 /* When enabled, every kernel launched by the library is bracketed by a
  * hipEvent pair on its stream.  sf_timing_collect synchronises those events
  * and accumulates per-kernel totals; sf_timing_query reads them by name
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
- * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3").
+ * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

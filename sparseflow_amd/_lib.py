@@ -50,6 +50,7 @@ EXPORTS = {
     "sf_conv2d_sparse": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_conv2d_forward": (c_int, [_P, _P, _P, _P, c_float, _P, c_size_t, _P, _P]),
     "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
+    "sf_lif_multistep": (c_int, [_P, c_int32, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P]),
     "sf_timing_enable": (c_int, [c_int32]),
     "sf_timing_collect": (c_int, []),
     "sf_timing_query": (c_int64, [ctypes.c_char_p, ctypes.POINTER(c_double)]),
@@ -261,11 +262,37 @@ def conv_lif_forward(desc: ConvDesc, T: int, x: torch.Tensor, wt: torch.Tensor, 
     _check(rc, "sf_conv_lif_forward")
 
 
+def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torch.Tensor] = None,
+                  spikes: Optional[torch.Tensor] = None, v_out: Optional[torch.Tensor] = None,
+                  out_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x [T, ...] currents -> (spikes [T, ...] in out_dtype (default x's), v [...] f32)."""
+    _require_device(x, "x")
+    x = x.contiguous()
+    if x.shape[0] != T:
+        raise ValueError(f"x has {x.shape[0]} steps, expected T={T}")
+    m = x.numel() // T
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    if spikes is None:
+        spikes = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    if v_out is None:
+        v_out = torch.empty(x.shape[1:], dtype=torch.float32, device=x.device)
+    if v_init is not None:
+        _require_device(v_init, "v_init")
+        if v_init.dtype != torch.float32 or v_init.numel() != m:
+            raise ValueError("v_init must be float32 with one value per neuron")
+        v_init = v_init.contiguous()
+    rc = lib().sf_lif_multistep(_ptr(x), dtype_code(x.dtype), int(T), int(m), ctypes.byref(lif), _ptr(v_init),
+                                _ptr(spikes), dtype_code(out_dtype), _ptr(v_out), _stream(x.device))
+    _check(rc, "sf_lif_multistep")
+    return spikes, v_out
+
+
 # ---------------------------------------------------------------------------
 # Per-kernel timing (bench instrumentation)
 # ---------------------------------------------------------------------------
 
-KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3")
+KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
+                "lif_multistep")
 
 
 def timing_enable(on: bool) -> None:

@@ -193,7 +193,8 @@ std::vector<TimingRec> g_pending;
 double g_total_ms[sf::K_COUNT] = {};
 int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
-                                     "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3"};
+                                     "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
+                                     "lif_multistep"};
 
 }  // namespace
 
@@ -423,6 +424,23 @@ int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const f
   }
   rc = sf::launch_conv_lif(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "conv_lif launch");
+  return SF_OK;
+}
+
+int sf_lif_multistep(const void* x, int32_t in_dtype, int32_t T, int64_t m, const sf_lif_params* lif,
+                     const float* v_init, void* spikes, int32_t out_dtype, float* v_out, void* stream) {
+  if (lif == nullptr) return fail(SF_ERR_INVALID, "lif params NULL");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  if (T < 1 || m < 0) return fail(SF_ERR_INVALID, "T < 1 or m < 0");
+  if (!(lif->tau != 0.f)) return fail(SF_ERR_INVALID, "tau must be non-zero");
+  if (m == 0) return SF_OK;
+  if (x == nullptr || spikes == nullptr || v_out == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  const int rc = sf::launch_lif_multistep(x, in_dtype, T, m, lif->tau, lif->v_threshold, lif->v_reset,
+                                          lif->hard_reset, lif->decay_input, v_init, spikes, out_dtype, v_out,
+                                          static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "lif_multistep launch");
   return SF_OK;
 }
 

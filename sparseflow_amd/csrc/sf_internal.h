@@ -106,13 +106,18 @@ int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
 // applicability as px3_applicable with stride 1).
 int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Standalone multi-step LIF over T steps of m neurons.
+int launch_lif_multistep(const void* x, int in_dtype, int T, int64_t m, float tau, float v_th, float v_reset,
+                         int hard_reset, int decay_input, const float* v_init, void* spikes, int out_dtype,
+                         float* v_out, hipStream_t stream);
+
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
 
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_COUNT = 9 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_COUNT = 10 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

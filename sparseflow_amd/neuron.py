@@ -9,6 +9,11 @@ sources by Core.registry.SpikeOpRegistry.default().
 
 Multi-step mode takes [T, B, ...] input and loops over T; single-step mode
 takes one step and keeps the membrane in `self.v` until `reset()`.
+
+On ROCm tensors `LIFNode` runs the library's multi-step LIF kernel
+(`sf_lif_multistep`: one pass over the T steps with the membrane in
+registers, the same arithmetic as the torch path below, bit for bit); the
+torch path is the CPU implementation and the checker.
 """
 
 from __future__ import annotations
@@ -80,6 +85,26 @@ class LIFNode(BaseNode):
         if self.decay_input:
             return v + (x - (v - vr)) / self.tau
         return v - (v - vr) / self.tau + x
+
+    def _hip_steps(self, x_seq: torch.Tensor) -> torch.Tensor:
+        from . import _lib
+
+        lif = _lib.LifParams(self.tau, self.v_threshold, 0.0 if self.v_reset is None else self.v_reset,
+                             0 if self.v_reset is None else 1, 1 if self.decay_input else 0)
+        v0 = self.v if (self.v is not None and self.v.shape == x_seq.shape[1:] and self.v.device == x_seq.device
+                        and self.v.dtype == torch.float32) else None
+        spikes, self.v = _lib.lif_multistep(x_seq, int(x_seq.shape[0]), lif, v_init=v0)
+        return spikes
+
+    def single_step_forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.is_cuda:
+            return self._hip_steps(x.unsqueeze(0))[0]
+        return super().single_step_forward(x)
+
+    def multi_step_forward(self, x_seq: torch.Tensor) -> torch.Tensor:
+        if x_seq.is_cuda:
+            return self._hip_steps(x_seq)
+        return super().multi_step_forward(x_seq)
 
     def extra_repr(self):
         return f"tau={self.tau}, decay_input={self.decay_input}, " + super().extra_repr()
