@@ -166,17 +166,25 @@ int sf_conv_lif_forward(const sf_conv_desc* desc, int32_t T, const void* x,
 
 /* ---- spiking neuron -------------------------------------------------------- */
 
-/* Multi-step LIF over T steps of m neurons: x [T, m] input currents (in_dtype),
- * spikes [T, m] in out_dtype (in_dtype or f32), v_out [m] f32 = membrane after
- * step T.  v_init [m] f32 may be NULL for V_0 = v_reset (hard reset) or 0
- * (soft reset).  Same update as sf_conv_lif_forward, computed operation by
- * operation without fused multiply-adds.  Replaces spikingjelly's multi-step
- * LIFNode used between the convolutions of the reference's spiking models
- * (Benchmark/bench_4test.py:166-197; update rule as restated in
- * Ops/sparse_fused_conv_lif.py:283-292). */
-int sf_lif_multistep(const void* x, int32_t in_dtype, int32_t T, int64_t m,
-                     const sf_lif_params* lif, const float* v_init, void* spikes,
-                     int32_t out_dtype, float* v_out, void* stream);
+/* Multi-step LIF over T steps of n x c x hw neurons: x [T, n, c, hw] input
+ * currents (in_dtype), plus x2 (same layout and dtype, may be NULL) summed
+ * into the current and rounded once -- a residual add fused into the neuron
+ * layer; spikes [T, n, c, hw] in out_dtype (in_dtype or f32); v_out [n, c, hw]
+ * f32 = membrane after step T.  v_init (f32, same layout as v_out) may be
+ * NULL for V_0 = v_reset (hard reset) or 0 (soft reset).  Same update as
+ * sf_conv_lif_forward, computed operation by operation without fused
+ * multiply-adds.  When bits and flags are given the spike map of the T*n
+ * output frames is written in the layout sf_prescan_pack produces for them
+ * (sf_prescan_bitmap_bytes / sf_prescan_flags_bytes(T*n, c, 1, hw) bytes;
+ * flags all zero), so sf_conv2d_sparse can consume the spikes without a
+ * prescan.  Replaces spikingjelly's multi-step LIFNode used between the
+ * convolutions of the reference's spiking models (Benchmark/bench_4test.py:
+ * 166-197; update rule as restated in Ops/sparse_fused_conv_lif.py:283-292);
+ * the spike map output has no counterpart in the reference. */
+int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T,
+                     int64_t n, int32_t c, int64_t hw, const sf_lif_params* lif,
+                     const float* v_init, void* spikes, int32_t out_dtype,
+                     float* v_out, uint32_t* bits, uint32_t* flags, void* stream);
 
 /* ---- per-kernel timing (bench instrumentation) --------------------------- */
 

@@ -24,6 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _lib
+from . import spike_map
 from ..Utils.config import PRESCAN_ACTIVITY_EPS, SPARSE_DENSE_RATIO_THRESHOLD
 from ..Utils.sparse_helpers import (
     TILE_DENSEISH,
@@ -241,7 +242,12 @@ def sparse_conv2d_forward(
     stats = None
     ms = 0.0
 
-    if not (need_meta or return_ms):
+    handed = None if (need_meta or return_ms) else spike_map.lookup(x, threshold)
+    if handed is not None:
+        # The neuron layer that produced x already wrote its spike map.
+        meta["reason"] = "bitmap_gather_handed_spike_map"
+        _lib.conv2d_sparse(desc, handed[0], handed[1], x, wt, b, y)
+    elif not (need_meta or return_ms):
         _lib.conv2d_forward(desc, x, wt, b, threshold, workspace, y)
     else:
         off = (int(_lib.lib().sf_prescan_bitmap_bytes(N, C_IN, H_IN, W_IN)) + 255) // 256 * 256

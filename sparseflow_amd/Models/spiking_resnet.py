@@ -63,7 +63,7 @@ class SpikingBottleneck(nn.Module):
         out = self.sn2(_seq(self.conv2, self.bn2, out))
         out = _seq(self.conv3, self.bn3, out)
         identity = x if self.downsample is None else _seq(self.downsample[0], self.downsample[1], x)
-        return self.sn3(out + identity)
+        return self.sn3(out, identity)  # LIF(out + identity), the add fused into the neuron pass
 
 
 class SpikingResNet(nn.Module):

@@ -50,7 +50,8 @@ EXPORTS = {
     "sf_conv2d_sparse": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_conv2d_forward": (c_int, [_P, _P, _P, _P, c_float, _P, c_size_t, _P, _P]),
     "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
-    "sf_lif_multistep": (c_int, [_P, c_int32, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P]),
+    "sf_lif_multistep": (c_int, [_P, _P, c_int32, c_int32, c_int64, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P, _P,
+                                 _P]),
     "sf_timing_enable": (c_int, [c_int32]),
     "sf_timing_collect": (c_int, []),
     "sf_timing_query": (c_int64, [ctypes.c_char_p, ctypes.POINTER(c_double)]),
@@ -264,13 +265,26 @@ def conv_lif_forward(desc: ConvDesc, T: int, x: torch.Tensor, wt: torch.Tensor, 
 
 def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torch.Tensor] = None,
                   spikes: Optional[torch.Tensor] = None, v_out: Optional[torch.Tensor] = None,
-                  out_dtype: Optional[torch.dtype] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """x [T, ...] currents -> (spikes [T, ...] in out_dtype (default x's), v [...] f32)."""
+                  out_dtype: Optional[torch.dtype] = None, x2: Optional[torch.Tensor] = None,
+                  spike_map: bool = False):
+    """x [T, ...] currents (+ x2, same shape) -> (spikes [T, ...] in out_dtype
+    (default x's), v [...] f32, map) where map is None or, with spike_map=True
+    on a [T, N, C, H, W] input, (bits, flags) of the T*N output frames in the
+    prescan's layout."""
     _require_device(x, "x")
     x = x.contiguous()
     if x.shape[0] != T:
         raise ValueError(f"x has {x.shape[0]} steps, expected T={T}")
-    m = x.numel() // T
+    if x2 is not None:
+        if x2.shape != x.shape or x2.dtype != x.dtype:
+            raise ValueError("x2 must match x in shape and dtype")
+        _require_device(x2, "x2")
+        x2 = x2.contiguous()
+    if x.dim() == 5:
+        n, c, hw = int(x.shape[1]), int(x.shape[2]), int(x.shape[3]) * int(x.shape[4])
+    else:
+        n, c, hw = 1, 1, x.numel() // T
+        spike_map = False
     out_dtype = x.dtype if out_dtype is None else out_dtype
     if spikes is None:
         spikes = torch.empty(x.shape, dtype=out_dtype, device=x.device)
@@ -278,13 +292,22 @@ def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torc
         v_out = torch.empty(x.shape[1:], dtype=torch.float32, device=x.device)
     if v_init is not None:
         _require_device(v_init, "v_init")
-        if v_init.dtype != torch.float32 or v_init.numel() != m:
+        if v_init.dtype != torch.float32 or v_init.numel() != n * c * hw:
             raise ValueError("v_init must be float32 with one value per neuron")
         v_init = v_init.contiguous()
-    rc = lib().sf_lif_multistep(_ptr(x), dtype_code(x.dtype), int(T), int(m), ctypes.byref(lif), _ptr(v_init),
-                                _ptr(spikes), dtype_code(out_dtype), _ptr(v_out), _stream(x.device))
+    bits = flags = None
+    if spike_map:
+        L = lib()
+        frames = T * n
+        bits = torch.empty(max(int(L.sf_prescan_bitmap_bytes(frames, c, 1, hw)) // 4, 1), dtype=torch.int32,
+                           device=x.device)
+        flags = torch.empty(max(int(L.sf_prescan_flags_bytes(frames, c, 1, hw)) // 4, 1), dtype=torch.int32,
+                            device=x.device)
+    rc = lib().sf_lif_multistep(_ptr(x), _ptr(x2), dtype_code(x.dtype), int(T), n, c, hw, ctypes.byref(lif),
+                                _ptr(v_init), _ptr(spikes), dtype_code(out_dtype), _ptr(v_out), _ptr(bits),
+                                _ptr(flags), _stream(x.device))
     _check(rc, "sf_lif_multistep")
-    return spikes, v_out
+    return spikes, v_out, (None if bits is None else (bits, flags))
 
 
 # ---------------------------------------------------------------------------

@@ -427,19 +427,32 @@ int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const f
   return SF_OK;
 }
 
-int sf_lif_multistep(const void* x, int32_t in_dtype, int32_t T, int64_t m, const sf_lif_params* lif,
-                     const float* v_init, void* spikes, int32_t out_dtype, float* v_out, void* stream) {
+int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T, int64_t n, int32_t c, int64_t hw,
+                     const sf_lif_params* lif, const float* v_init, void* spikes, int32_t out_dtype, float* v_out,
+                     uint32_t* bits, uint32_t* flags, void* stream) {
   if (lif == nullptr) return fail(SF_ERR_INVALID, "lif params NULL");
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
   if (out_dtype != in_dtype && out_dtype != SF_F32)
     return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
-  if (T < 1 || m < 0) return fail(SF_ERR_INVALID, "T < 1 or m < 0");
+  if (T < 1 || n < 0 || c < 0 || hw < 0) return fail(SF_ERR_INVALID, "T < 1 or negative size");
   if (!(lif->tau != 0.f)) return fail(SF_ERR_INVALID, "tau must be non-zero");
-  if (m == 0) return SF_OK;
+  if ((bits == nullptr) != (flags == nullptr)) return fail(SF_ERR_INVALID, "bits and flags go together");
+  if (bits != nullptr && (hw > INT32_MAX || c > 4096)) return fail(SF_ERR_UNSUPPORTED, "spike map: c <= 4096, hw < 2^31");
+  if (n == 0 || c == 0 || hw == 0) return SF_OK;
   if (x == nullptr || spikes == nullptr || v_out == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
-  const int rc = sf::launch_lif_multistep(x, in_dtype, T, m, lif->tau, lif->v_threshold, lif->v_reset,
-                                          lif->hard_reset, lif->decay_input, v_init, spikes, out_dtype, v_out,
-                                          static_cast<hipStream_t>(stream));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int cwp = 0;
+  int64_t nflags = 0;
+  if (bits != nullptr) {
+    // The spike map of T*n frames of c x hw, exactly as sf_prescan_pack lays
+    // it out; every chunk is binary, so the flags are all zero.
+    const sf::PackPlan pl = sf::make_pack_plan((int64_t)T * n, c, 1, (int)hw);
+    cwp = pl.cwp;
+    nflags = pl.total_chunks;
+  }
+  const int rc = sf::launch_lif_multistep(x, x2, in_dtype, T, n, c, hw, lif->tau, lif->v_threshold, lif->v_reset,
+                                          lif->hard_reset, lif->decay_input, v_init, spikes, out_dtype, v_out, bits, cwp,
+                                          flags, nflags, s);
   if (rc != hipSuccess) return hip_fail(rc, "lif_multistep launch");
   return SF_OK;
 }

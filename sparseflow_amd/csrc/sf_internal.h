@@ -106,10 +106,14 @@ int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
 // applicability as px3_applicable with stride 1).
 int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
-// Standalone multi-step LIF over T steps of m neurons.
-int launch_lif_multistep(const void* x, int in_dtype, int T, int64_t m, float tau, float v_th, float v_reset,
-                         int hard_reset, int decay_input, const float* v_init, void* spikes, int out_dtype,
-                         float* v_out, hipStream_t stream);
+// Standalone multi-step LIF over T steps of n x c x hw neurons (x2: optional
+// second input summed into the current; bits: optional spike map output in
+// the prescan layout with cwp words per pixel, with its nflags chunk flags
+// cleared).
+int launch_lif_multistep(const void* x, const void* x2, int in_dtype, int T, int64_t n, int c, int64_t hw, float tau,
+                         float v_th, float v_reset, int hard_reset, int decay_input, const float* v_init, void* spikes,
+                         int out_dtype, float* v_out, uint32_t* bits, int cwp, uint32_t* flags, int64_t nflags,
+                         hipStream_t stream);
 
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);

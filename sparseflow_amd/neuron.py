@@ -79,6 +79,7 @@ class LIFNode(BaseNode):
         super().__init__(v_threshold, v_reset, detach_reset, step_mode, backend)
         self.tau = float(tau)
         self.decay_input = bool(decay_input)
+        self.emit_spike_map = True
 
     def neuronal_charge(self, x, v):
         vr = 0.0 if self.v_reset is None else self.v_reset
@@ -86,14 +87,22 @@ class LIFNode(BaseNode):
             return v + (x - (v - vr)) / self.tau
         return v - (v - vr) / self.tau + x
 
-    def _hip_steps(self, x_seq: torch.Tensor) -> torch.Tensor:
+    def _hip_steps(self, x_seq: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         from . import _lib
+        from .Kernels import spike_map
 
         lif = _lib.LifParams(self.tau, self.v_threshold, 0.0 if self.v_reset is None else self.v_reset,
                              0 if self.v_reset is None else 1, 1 if self.decay_input else 0)
         v0 = self.v if (self.v is not None and self.v.shape == x_seq.shape[1:] and self.v.device == x_seq.device
                         and self.v.dtype == torch.float32) else None
-        spikes, self.v = _lib.lif_multistep(x_seq, int(x_seq.shape[0]), lif, v_init=v0)
+        # [T, N, C, H, W] spikes also leave as a spike map for the next
+        # sparse convolution (skips its prescan).
+        want_map = self.emit_spike_map and x_seq.dim() == 5
+        spikes, self.v, smap = _lib.lif_multistep(x_seq, int(x_seq.shape[0]), lif, v_init=v0, x2=residual,
+                                                  spike_map=want_map)
+        if smap is not None:
+            T, N, C, H, W = (int(v) for v in x_seq.shape)
+            spike_map.attach(spikes, T * N, C, H, W, smap[0], smap[1])
         return spikes
 
     def single_step_forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -105,6 +114,17 @@ class LIFNode(BaseNode):
         if x_seq.is_cuda:
             return self._hip_steps(x_seq)
         return super().multi_step_forward(x_seq)
+
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """LIF(x), or LIF(x + residual): the sum feeds the neuron directly (on
+        the GPU in the same pass; bit-identical to adding first)."""
+        if residual is not None:
+            if x.is_cuda:
+                if self.step_mode == "m":
+                    return self._hip_steps(x, residual)
+                return self._hip_steps(x.unsqueeze(0), residual.unsqueeze(0))[0]
+            x = x + residual
+        return super().forward(x)
 
     def extra_repr(self):
         return f"tau={self.tau}, decay_input={self.decay_input}, " + super().extra_repr()

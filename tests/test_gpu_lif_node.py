@@ -80,3 +80,58 @@ def test_lif_multistep_rejects_bad_arguments():
         _lib.lif_multistep(x, 3, lif)
     with pytest.raises(_lib.SparseFlowLibError):
         _lib.lif_multistep(x, 2, _lib.LifParams(0.0, 1.0, 0.0, 1, 1))
+
+
+def test_lif_residual_fused_equals_add_first():
+    g = torch.Generator().manual_seed(7)
+    a = (torch.randn(4, 2, 24, 9, 9, generator=g) * 1.5).to(DEV)
+    b = (torch.rand(4, 2, 24, 9, 9, generator=g) < 0.3).float().to(DEV)
+    announce("lif residual")
+    n1, n2 = LIFNode(step_mode="m"), LIFNode(step_mode="m")
+    s_fused = n1(a, b)
+    s_ref = n2(a + b)
+    assert torch.equal(s_fused, s_ref)
+    assert torch.equal(n1.v, n2.v)
+
+
+@pytest.mark.parametrize("shape", [(4, 2, 64, 14, 14), (3, 2, 256, 7, 9), (2, 3, 40, 5, 5), (2, 1, 3, 6, 6)])
+def test_lif_spike_map_equals_prescan(shape):
+    from sparseflow_amd.Kernels import spike_map
+
+    g = torch.Generator().manual_seed(sum(shape))
+    x = (torch.randn(shape, generator=g) * 2).to(DEV)
+    announce(f"lif spike map {shape}")
+    node = LIFNode(step_mode="m")
+    s = node(x)
+    T, N, C, H, W = shape
+    got = spike_map.lookup(s.flatten(0, 1), 1e-6)
+    assert got is not None
+    bits_ref, flags_ref = _lib.prescan_pack(s.flatten(0, 1), 1e-6)
+    nb = bits_ref.numel()
+    assert torch.equal(got[0][:nb], bits_ref)
+    assert torch.equal(got[1][:flags_ref.numel()], flags_ref)
+    # An in-place change invalidates the map.
+    s.mul_(1.0)
+    assert spike_map.lookup(s.flatten(0, 1), 1e-6) is None
+
+
+def test_conv_consumes_handed_spike_map():
+    from sparseflow_amd.Kernels.conv2d import sparse_conv2d_forward
+
+    g = torch.Generator().manual_seed(9)
+    x = (torch.randn(4, 2, 64, 16, 16, generator=g) * 2).to(DEV)
+    w = (torch.randn(64, 64, 3, 3, generator=g) * 0.05).to(DEV)
+    announce("handed spike map conv")
+    s = LIFNode(step_mode="m")(x)
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        y_handed, _, meta = sparse_conv2d_forward(s.flatten(0, 1), w, None, 3, 1, 1, return_backend_meta=True)
+        y_own = sparse_conv2d_forward(s.flatten(0, 1).clone(), w, None, 3, 1, 1)[0]
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    assert meta["reason"] == "bitmap_gather_handed_spike_map"
+    assert stats["prescan_pack"][0] == 1  # only the clone was packed
+    assert torch.equal(y_handed, y_own)
