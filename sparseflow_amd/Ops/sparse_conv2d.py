@@ -125,6 +125,9 @@ class SparseConv2d(nn.Module):
         self.diag_source = "measured"
         self.support_status = "supported"
         self.score_family = "conv"
+        # "sparse" (library kernels) or "dense" (F.conv2d), set per layer by
+        # Utils.dispatch from measurements.
+        self.backend_mode = "sparse"
 
     # ---- runtime switches (Ops/sparse_conv2d.py:234-250) --------------------
     def set_launch_all_tiles(self, enabled: bool):
@@ -236,7 +239,7 @@ class SparseConv2d(nn.Module):
             raise ValueError(f"Expected 4D or 5D input, got {x.dim()}D")
         self._forward_count += 1
 
-        if x4d.is_cuda and self._supports_sparse():
+        if x4d.is_cuda and self._supports_sparse() and self.backend_mode != "dense":
             y4d, backend = self._hip_forward(x4d)
             path = {"dense_fallback": "dense(fallback)", "zero_tiles_only": "zero(tile_compaction)"}.get(
                 backend, "sparse")
@@ -250,7 +253,7 @@ class SparseConv2d(nn.Module):
         else:
             y4d = self._fallback_forward(x4d)
             path = "dense"
-            self.fallback_reason = "module_dense_path"
+            self.fallback_reason = "dispatch_dense" if self.backend_mode == "dense" else "module_dense_path"
             if self.profile_runtime:
                 self._profile.dense_path_hits += 1
 
