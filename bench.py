@@ -163,7 +163,7 @@ def bench_lif(steps, warmup, dev, with_miopen=True):
         kt = kernel_times(step, max(5, min(steps, 20)))
         miopen_ms = None
         if with_miopen:
-            log(f"[bench] {name}: sparse path timed; MIOpen baseline next")
+            log(f"[bench] {LIF_WORKLOAD}: sparse path timed; MIOpen baseline next")
             torch.backends.cudnn.benchmark = True
             xf = x.reshape(T * N, C, H, W)
 
@@ -233,6 +233,7 @@ def cpu_baseline(name, target_seconds=12.0):
 
 
 E2E_WORKLOAD = "resnet50_e2e"  # T=16, batch 32, 3x224x224, images/s
+ATTN_WORKLOAD = "config5_spikformer_block"  # T=4, N=64, 196 tokens, dim 384, 12 heads, Bernoulli(0.1)
 
 
 def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
@@ -293,6 +294,79 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
     return res
 
 
+def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=384, heads=12, p=0.1):
+    """Spikformer-style block at BASELINE config 5: binary Q/K/V Bernoulli(p)
+    [T*N, heads, tokens, dim/heads]; the q/k/v/proj projections as sparse
+    Linear on spike tokens [T*N*tokens, dim]; Q @ K^T and attn @ V as sparse
+    batched matmuls; the patch-embed stem conv3x3 3 -> dim on N(0,1) 32x32
+    frames.  Each op is timed sparse and dense (hipBLASLt / rocBLAS / MIOpen
+    through torch) on the same tensors."""
+    from sparseflow_amd import _lib
+    from sparseflow_amd.Kernels.attention import sparse_attn_v_forward, sparse_qk_forward
+    from sparseflow_amd.Kernels.linear import sparse_linear_forward, tap_weight
+    from sparseflow_amd.Ops.sparse_conv2d import SparseConv2d
+
+    hd = dim // heads
+    bt = T * N
+    g = torch.Generator(device=dev).manual_seed(5)
+    qkv = [(torch.rand(bt, heads, tokens, hd, generator=g, device=dev) < p).float() for _ in range(3)]
+    x_tok = (torch.rand(bt * tokens, dim, generator=g, device=dev) < p).float()
+    lin = torch.nn.Linear(dim, dim).to(dev)
+    wt = tap_weight(lin.weight)
+    ws = torch.empty(_lib.linear_workspace_size(bt * tokens, dim), dtype=torch.uint8, device=dev)
+    scale = hd ** -0.5
+    ops = {}
+    with torch.no_grad():
+        attn = sparse_qk_forward(qkv[0], qkv[1], scale)[0]
+        cases = {
+            "linear_384x384": (
+                lambda: sparse_linear_forward(x_tok, lin.weight, lin.bias, w_t=wt, workspace=ws),
+                lambda: torch.nn.functional.linear(x_tok, lin.weight, lin.bias),
+                x_tok.numel() * 4 + dim * dim * 4 + bt * tokens * dim * 4),
+            "qk": (
+                lambda: sparse_qk_forward(qkv[0], qkv[1], scale),
+                lambda: torch.matmul(qkv[0], qkv[1].transpose(-2, -1)) * scale,
+                2 * qkv[0].numel() * 4 + bt * heads * tokens * tokens * 4),
+            "av": (
+                lambda: sparse_attn_v_forward(attn, qkv[2]),
+                lambda: torch.matmul(attn, qkv[2]),
+                attn.numel() * 4 + 2 * qkv[2].numel() * 4),
+        }
+        for name, (sp_fn, dn_fn, alg) in cases.items():
+            ms = time_gpu(sp_fn, steps, warmup)
+            kt = kernel_times(sp_fn, max(5, min(steps, 20)))
+            dms = time_gpu(dn_fn, max(5, steps // 2), 3) if with_dense else None
+            ops[name] = {"us": ms * 1e3, "dense_us": None if dms is None else dms * 1e3,
+                         "speedup_vs_dense": None if dms is None else dms / ms,
+                         "hbm_gbs": alg / (ms * 1e-3) / 1e9, "alg_bytes": alg,
+                         "kernels_us": {k: v[1] * 1e3 for k, v in kt.items()}}
+            log(f"[bench] attn {name}: {ms * 1e3:.1f} us (dense {'-' if dms is None else f'{dms * 1e3:.1f}'} us)")
+        del attn
+        torch.cuda.empty_cache()
+        # Patch-embed stem: conv3x3 3 -> dim on dense N(0,1) frames.
+        img = torch.randn(bt, 3, 32, 32, generator=g, device=dev)
+        conv = make_conv(3, dim, 3, 1, dev)
+        sp = SparseConv2d.from_dense(conv).to(dev)
+        sp.set_inference_mode(True)
+        ms = time_gpu(lambda: sp(img), steps, warmup)
+        torch.backends.cudnn.benchmark = True
+        wd = conv.weight.float()
+        dms = time_gpu(lambda: torch.nn.functional.conv2d(img, wd, None, 1, 1), max(5, steps // 2), 3) \
+            if with_dense else None
+        torch.backends.cudnn.benchmark = False
+        ops["stem_conv3x3_3to384"] = {"us": ms * 1e3, "dense_us": None if dms is None else dms * 1e3,
+                                      "speedup_vs_dense": None if dms is None else dms / ms}
+    # One SSA block: q, k, v, proj projections + qk + av.
+    blk = 4 * ops["linear_384x384"]["us"] + ops["qk"]["us"] + ops["av"]["us"]
+    res = {"workload": ATTN_WORKLOAD, "T": T, "N": N, "tokens": tokens, "dim": dim, "heads": heads,
+           "spike_p": p, "ops": ops, "ssa_block_us": blk}
+    if with_dense:
+        dblk = 4 * ops["linear_384x384"]["dense_us"] + ops["qk"]["dense_us"] + ops["av"]["dense_us"]
+        res["ssa_block_dense_us"] = dblk
+        res["ssa_block_speedup_vs_dense"] = dblk / blk
+    return res
+
+
 def measured_traffic(workload, kernel):
     """HBM bytes per launch (fetched + written) of `kernel` on `workload` as
     measured by the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes, or
@@ -315,7 +389,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="resnet50_layer1_conv3x3", choices=sorted(WORKLOADS))
     ap.add_argument("--extra", default="all", help="'all', 'none' or comma-separated workload names (+ "
-                                                   f"{LIF_WORKLOAD}, {E2E_WORKLOAD})")
+                                                   f"{LIF_WORKLOAD}, {ATTN_WORKLOAD}, {E2E_WORKLOAD})")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-miopen", action="store_true", help="skip the MIOpen baselines")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -352,7 +426,7 @@ def main():
     extra = {}
     names = []
     if args.extra == "all":
-        names = [n for n in WORKLOADS if n != args.workload] + [LIF_WORKLOAD, E2E_WORKLOAD]
+        names = [n for n in WORKLOADS if n != args.workload] + [LIF_WORKLOAD, ATTN_WORKLOAD, E2E_WORKLOAD]
     elif args.extra != "none":
         names = [n.strip() for n in args.extra.split(",") if n.strip()]
     for name in names:
@@ -360,6 +434,8 @@ def main():
         steps = max(5, args.steps // 2)
         if name == LIF_WORKLOAD:
             r = bench_lif(steps, 3, dev, with_miopen=not args.no_miopen)
+        elif name == ATTN_WORKLOAD:
+            r = bench_attn(steps, 3, dev, with_dense=not args.no_miopen)
         elif name == E2E_WORKLOAD:
             r = bench_e2e(max(3, steps // 5), 2, dev, with_dense=not args.no_miopen)
         else:

@@ -186,13 +186,63 @@ int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T,
                      const float* v_init, void* spikes, int32_t out_dtype,
                      float* v_out, uint32_t* bits, uint32_t* flags, void* stream);
 
+/* ---- sparse linear ------------------------------------------------------------ */
+
+/* y[m, c_out] = x[m, k] @ wt[k, c_out] + bias for a spike-sparse row-major x
+ * (any leading shape flattened to m rows; wt = weight transposed, f32).
+ * Replaces the reference's sparse_linear_forward (Kernels/linear.py:460-778:
+ * grouped prescan + tile classification + sparse_linear_grouped_kernel) for
+ * the Linear layers of its spiking transformers (Ops/sparse_linear.py:68-890).
+ *
+ * Stage 1 (sf_linear_prescan): one bit per element, bit j of word w of row r
+ * = f16(|x[r, 32w + j]|) > f16(threshold) (the test sf_prescan_pack applies),
+ * sf_linear_bitmap_bytes(m, k) bytes; one non-binary flag word per 16 rows
+ * (sf_linear_flags_bytes(m)), non-zero when a row of the chunk holds a value
+ * other than 0 and 1.  Stage 2 (sf_linear_sparse): each output row sums the
+ * weight rows of its active elements (times the element where the chunk is
+ * flagged) in increasing k; deterministic.  c_out must be a multiple of 4;
+ * out_dtype = in_dtype or f32; m < 2^30.  sf_linear_forward runs both with
+ * the bitmap in `workspace` (sf_linear_workspace_size(m, k) bytes). */
+size_t sf_linear_bitmap_bytes(int64_t m, int32_t k);
+size_t sf_linear_flags_bytes(int64_t m);
+size_t sf_linear_workspace_size(int64_t m, int32_t k);
+int sf_linear_prescan(const void* x, int32_t dtype, int64_t m, int32_t k,
+                      float threshold, uint32_t* bits, uint32_t* flags,
+                      void* stream);
+int sf_linear_sparse(const uint32_t* bits, const uint32_t* flags, const void* x,
+                     int32_t in_dtype, int64_t m, int32_t k, const float* wt,
+                     const float* bias, int32_t c_out, void* y,
+                     int32_t out_dtype, void* stream);
+int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k,
+                      const float* wt, const float* bias, int32_t c_out,
+                      float threshold, void* workspace, size_t workspace_bytes,
+                      void* y, int32_t out_dtype, void* stream);
+
+/* ---- sparse batched matmul -------------------------------------------------- */
+
+/* c[b] = a[b] @ B[b] for b < batches: a [batches, m, k] contiguous and
+ * spike-sparse, B read at B[b*b_stride_batch + kk*b_stride_k + j*b_stride_n]
+ * (elements; a transposed view such as K^T needs no copy), c [batches, m, n]
+ * contiguous in out_dtype (in_dtype or f32).  a and B share in_dtype.
+ * Elements of a with f16(|a|) <= f16(threshold) are skipped; the rest are
+ * summed in f32 in increasing k (deterministic).  Supported while
+ * sf_bmm_supported(k, n) (k <= 252).  Replaces the reference's
+ * sparse_bmm_forward (Kernels/bmm.py:195-361) used by its sparse attention
+ * (Kernels/attention.py:27-121, Ops/sparse_bmm.py:22-131). */
+int sf_bmm_supported(int32_t k, int32_t n);
+int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batches,
+                  int32_t m, int32_t k, int32_t n, int64_t b_stride_batch,
+                  int64_t b_stride_k, int64_t b_stride_n, float threshold,
+                  void* c, int32_t out_dtype, void* stream);
+
 /* ---- per-kernel timing (bench instrumentation) --------------------------- */
 
 /* When enabled, every kernel launched by the library is bracketed by a
  * hipEvent pair on its stream.  sf_timing_collect synchronises those events
  * and accumulates per-kernel totals; sf_timing_query reads them by name
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
- * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep").
+ * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep",
+ * "prescan_rows", "linear_flat", "bmm_sparse").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

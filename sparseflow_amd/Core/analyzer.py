@@ -12,10 +12,13 @@ discovery modes tried in order (Core/analyzer.py:233-280):
   3. Module order: a window of 15 modules after each spike source, skipping
      transparent layers (Core/analyzer.py:506-549).
 
-Eligibility (Core/analyzer.py:575-636): groups == 1 and one of 3x3/s1/p1,
-3x3/s2/p1, 1x1/s1/p0.  Feature maps the block rule rejects (input H < 8,
-Utils/block_selector.py) are skipped; the chosen block size is recorded on
-the target.  Only Conv2d targets are produced by this build.
+Targets (Core/analyzer.py:575-700): Conv2d with groups == 1 and one of
+3x3/s1/p1, 3x3/s2/p1, 1x1/s1/p0 (feature maps the block rule rejects,
+input H < 8, Utils/block_selector.py, are skipped; the chosen block size is
+recorded on the target); nn.Linear (op "linear"); and attention blocks --
+modules carrying Linear q/k/v/proj and an attn_lif, traced as leaves --
+with the variant inferred as the reference does (Core/analyzer.py:121-147).
+Conv1d/Conv3d consumers end a search branch but are not targets here.
 """
 
 from __future__ import annotations
@@ -89,13 +92,37 @@ def display_block_info(target: ReplacementTarget) -> str:
     return ""
 
 
+def is_attention_like_module(module: nn.Module) -> bool:
+    """An attention block carries Linear q/k/v/proj and an attn_lif
+    (Core/analyzer.py:121-131)."""
+    if module is None:
+        return False
+    for attr in ("q", "k", "v", "proj"):
+        if not isinstance(getattr(module, attr, None), nn.Linear):
+            return False
+    return hasattr(module, "attn_lif")
+
+
+def infer_attention_variant(module: nn.Module) -> str:
+    """Core/analyzer.py:139-145: class name with "qkmix" -> qkmix; a `scale`
+    attribute -> q @ k^T @ v; else the linear-attention form."""
+    if "qkmix" in module.__class__.__name__.lower():
+        return "attention_qkmix"
+    if hasattr(module, "scale"):
+        return "attention_qkav"
+    return "attention_linear"
+
+
+ATTENTION_OP_TYPES = ("attention_qkav", "attention_linear", "attention_qkmix")
+
+
 class _SpikeLeafTracer(torch.fx.Tracer):
     def __init__(self, registry: SpikeOpRegistry):
         super().__init__()
         self._registry = registry
 
     def is_leaf_module(self, m: nn.Module, qualname: str) -> bool:
-        if self._registry.is_spike_op(m):
+        if self._registry.is_spike_op(m) or is_attention_like_module(m):
             return True
         return super().is_leaf_module(m, qualname)
 
@@ -150,7 +177,7 @@ class NetworkAnalyzer:
             if node.op != "call_module" or not self.registry.is_spike_op(modules.get(node.target)):
                 continue
             for name in self._bfs_find_targets(node, modules, visited):
-                t = self._make_conv2d_target(name, modules[name], node.target, input_shapes)
+                t = self._make_target(name, modules[name], node.target, input_shapes)
                 if t is not None:
                     targets.append(t)
                     visited.add(name)
@@ -167,8 +194,8 @@ class NetworkAnalyzer:
             seen.add(id(node))
             mod = modules.get(node.target) if node.op == "call_module" else None
             if mod is not None:
-                if isinstance(mod, (nn.Conv1d, nn.Conv2d, nn.Conv3d, nn.Linear)):
-                    if isinstance(mod, nn.Conv2d) and node.target not in visited:
+                if isinstance(mod, (nn.Conv1d, nn.Conv2d, nn.Conv3d, nn.Linear)) or is_attention_like_module(mod):
+                    if not isinstance(mod, (nn.Conv1d, nn.Conv3d)) and node.target not in visited:
                         found.append(node.target)
                     continue  # a consumer ends this branch
                 if self.registry.is_spike_op(mod):
@@ -184,7 +211,7 @@ class NetworkAnalyzer:
         for name, m in model.named_modules():
             if self.registry.is_spike_op(m):
                 hooks.append(m.register_forward_hook(lambda _m, _i, _o, n=name: events.append(("spike", n))))
-            elif isinstance(m, (nn.Conv1d, nn.Conv2d, nn.Conv3d, nn.Linear)):
+            elif isinstance(m, (nn.Conv2d, nn.Linear)) or is_attention_like_module(m):
                 hooks.append(m.register_forward_hook(lambda _m, _i, _o, n=name: events.append(("target", n))))
         try:
             _reset_states(model)
@@ -194,6 +221,7 @@ class NetworkAnalyzer:
             for h in hooks:
                 h.remove()
             _reset_states(model)
+        attn_names = [n for n, m in modules.items() if n and is_attention_like_module(m)]
         targets, visited, last_spike = [], set(), None
         for kind, name in events:
             if kind == "spike":
@@ -201,7 +229,9 @@ class NetworkAnalyzer:
                 continue
             if name in visited or last_spike is None:
                 continue
-            t = self._make_conv2d_target(name, modules[name], last_spike, input_shapes)
+            if any(name.startswith(a + ".") for a in attn_names):
+                continue  # inside an attention block: the block is the target
+            t = self._make_target(name, modules[name], last_spike, input_shapes)
             if t is not None:
                 targets.append(t)
                 visited.add(name)
@@ -210,6 +240,7 @@ class NetworkAnalyzer:
     # ---- mode 3: module order ---------------------------------------------
     def _analyze_fallback(self, model: nn.Module, input_shapes: dict) -> List[ReplacementTarget]:
         mods = list(model.named_modules())
+        attn_names = [n for n, m in mods if n and is_attention_like_module(m)]
         targets, visited = [], set()
         for i, (name, m) in enumerate(mods):
             if not self.registry.is_spike_op(m):
@@ -220,15 +251,31 @@ class NetworkAnalyzer:
                     continue
                 if self.registry.is_spike_op(nxt):
                     break
-                if isinstance(nxt, _TRANSPARENT_MODULES) or not isinstance(nxt, nn.Conv2d):
+                if isinstance(nxt, _TRANSPARENT_MODULES) or not isinstance(nxt, (nn.Conv2d, nn.Linear)):
                     continue
-                t = self._make_conv2d_target(nxt_name, nxt, name, input_shapes)
+                if any(nxt_name.startswith(a + ".") for a in attn_names):
+                    continue
+                t = self._make_target(nxt_name, nxt, name, input_shapes)
                 if t is not None:
                     targets.append(t)
                     visited.add(nxt_name)
         return targets
 
     # ---- target construction ----------------------------------------------
+    def _make_target(self, name, module, spike_name, input_shapes) -> Optional[ReplacementTarget]:
+        if isinstance(module, nn.Conv2d):
+            return self._make_conv2d_target(name, module, spike_name, input_shapes)
+        if isinstance(module, nn.Linear):
+            return ReplacementTarget(conv_name=name, conv_module=module, spike_name=str(spike_name),
+                                     op_type="linear", block_size=None)
+        if is_attention_like_module(module):
+            shp = input_shapes.get(name)
+            n, c = (int(shp[-2]), int(shp[-1])) if shp is not None and len(shp) >= 2 else (0, 0)
+            return ReplacementTarget(conv_name=name, conv_module=module, spike_name=str(spike_name),
+                                     op_type=infer_attention_variant(module), block_size=None,
+                                     input_h=n, input_w=c)
+        return None
+
     def _make_conv2d_target(self, conv_name, conv_module, spike_name, input_shapes) -> Optional[ReplacementTarget]:
         op_type = conv2d_op_type(conv_module)
         if op_type is None:

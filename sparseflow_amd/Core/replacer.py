@@ -1,9 +1,11 @@
 """Module replacement pass (drop-in for Core/replacer.py).
 
 Swaps each ReplacementTarget in place by its dotted name: conv2d targets
-become SparseConv2d.from_dense (or StaticZeroConv2d for layers listed as
-exact-zero), with the reference's `sf_*` observability attributes and its
-4-tuple return (Core/replacer.py:83-292).
+become SparseConv2d.from_dense, linear targets SparseLinear.from_dense,
+attention blocks SparseAttentionBlock.from_dense (StaticZeroConv2d /
+StaticZeroLinear for layers listed as exact-zero), with the reference's
+`sf_*` observability attributes and its 4-tuple return
+(Core/replacer.py:83-292,320-370).
 """
 
 from __future__ import annotations
@@ -12,11 +14,14 @@ from typing import Any, Dict, List, Optional, Set, Tuple
 
 import torch.nn as nn
 
+from ..Ops.sparse_attention_block import SparseAttentionBlock
 from ..Ops.sparse_conv2d import SparseConv2d
+from ..Ops.sparse_linear import SparseLinear
 from ..Ops.static_zero_conv2d import StaticZeroConv2d
-from .analyzer import CONV2D_OP_TYPES, ReplacementTarget, display_block_info
+from ..Ops.static_zero_linear import StaticZeroLinear
+from .analyzer import ATTENTION_OP_TYPES, CONV2D_OP_TYPES, ReplacementTarget, display_block_info
 
-_STATIC_ZERO_OP_TYPES = CONV2D_OP_TYPES
+_STATIC_ZERO_OP_TYPES = CONV2D_OP_TYPES + ("linear",)
 
 
 def _set_module_by_name(model: nn.Module, name: str, new_module: nn.Module) -> None:
@@ -37,6 +42,10 @@ class ModuleReplacer:
             return "conv"
         if op_type == "linear":
             return "linear"
+        if op_type == "attention_linear":
+            return "attn_linear"
+        if op_type in ("attention_qkav", "attention_qkmix"):
+            return "attn_matmul"
         return "unknown"
 
     def _attach_observability(self, module: nn.Module, target: ReplacementTarget, backend_mode: str,
@@ -84,13 +93,16 @@ class ModuleReplacer:
             if block_sizes and name in block_sizes:
                 block = block_sizes[name]
             if name in static_zero_layers and op in _STATIC_ZERO_OP_TYPES:
-                new = StaticZeroConv2d.from_conv(target.conv_module)
+                if op == "linear":
+                    new, kind = StaticZeroLinear.from_linear(target.conv_module), "StaticZeroLinear"
+                else:
+                    new, kind = StaticZeroConv2d.from_conv(target.conv_module), "StaticZeroConv2d"
                 self._attach_observability(new, target, "staticzero", "exact_zero")
                 _set_module_by_name(model, name, new)
                 replaced += 1
                 static_zero_count += 1
                 if self.verbose:
-                    print(f"  [STATIC ] {name} ({op}) -> StaticZeroConv2d")
+                    print(f"  [STATIC ] {name} ({op}) -> {kind}")
                 continue
             if only_static_zero:
                 dense_keep += 1
@@ -114,6 +126,19 @@ class ModuleReplacer:
     def _create_sparse_module(self, target: ReplacementTarget, block: Optional[int],
                               sparse_kwargs: Optional[Dict[str, Any]] = None) -> Optional[nn.Module]:
         sparse_kwargs = sparse_kwargs or {}
+        thr = float(sparse_kwargs.get("threshold", 1e-6))
+        rms = bool(sparse_kwargs.get("return_ms", False))
+        if target.op_type == "linear" and isinstance(target.conv_module, nn.Linear):
+            lin = SparseLinear.from_dense(target.conv_module, threshold=thr, return_ms=rms)
+            lin.collect_diag = bool(sparse_kwargs.get("collect_diag", False))
+            lin.profile_runtime = bool(sparse_kwargs.get("profile_runtime", False))
+            return lin.to(target.conv_module.weight.device)
+        if target.op_type in ATTENTION_OP_TYPES:
+            blk = SparseAttentionBlock.from_dense(target.conv_module, variant=target.op_type, threshold=thr,
+                                                  return_ms=rms,
+                                                  profile_runtime=bool(sparse_kwargs.get("profile_runtime", False)))
+            blk.collect_diag = bool(sparse_kwargs.get("collect_diag", False))
+            return blk
         if target.op_type not in CONV2D_OP_TYPES or not isinstance(target.conv_module, nn.Conv2d):
             return None
         mod = target.conv_module

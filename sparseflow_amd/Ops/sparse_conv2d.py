@@ -26,6 +26,7 @@ import torch.nn.functional as F
 
 from .. import _lib
 from ..Kernels.conv2d import BACKEND_NAME, _select_tile_sizes, choose_group_size, sparse_conv2d_forward
+from ..Utils import config as _config
 from ..Utils.block_selector import select_block_size
 from .static_zero_conv2d import ZERO_BACKEND_FAMILY, make_zero_conv_output  # noqa: F401
 
@@ -113,6 +114,17 @@ class SparseConv2d(nn.Module):
         self._zero_streak_needed = int(max(1, zero_streak_needed))
         self._forward_count = 0
         self._inference_mode = False
+        # Runtime fallback policy (Ops/sparse_conv2d.py:449-496): an EMA of
+        # the active-group ratio forces dense above dense_threshold, a streak
+        # of all-zero inputs forces the zero output.  Off unless enabled in
+        # Utils.config or per module via `runtime_policy`, as in the reference.
+        self.runtime_policy = bool(_config.ENABLE_RUNTIME_FALLBACK_POLICY)
+        self._ema_active_ratio = None
+        self._zero_streak = 0
+        self._force_dense = False
+        self._force_zero = False
+        self._runtime_dispatch_seen = 0
+        self._runtime_dispatch_mismatch = 0
 
         self.collect_diag = False
         self._last_diag = {}
@@ -224,12 +236,63 @@ class SparseConv2d(nn.Module):
                 sparse.bias.copy_(conv.bias)
         return sparse
 
+    # ---- runtime policy (Ops/sparse_conv2d.py:323-334,449-496) ---------------------
+    def _should_collect_ratio(self) -> bool:
+        if not self.runtime_policy or self._inference_mode:
+            return False
+        if self._warmup_left > 0:
+            return True
+        return (self._forward_count % self._calib_every) == 0
+
+    def _update_policy(self, avg_active_ratio):
+        if avg_active_ratio is None:
+            return
+        self._last_avg_active_ratio = float(avg_active_ratio)
+        if not self.runtime_policy:
+            return
+        if self._warmup_left > 0:
+            self._warmup_left -= 1
+            self._ema_active_ratio = avg_active_ratio
+            return
+        if self._ema_active_ratio is None:
+            self._ema_active_ratio = avg_active_ratio
+        else:
+            self._ema_active_ratio = self._ema_decay * self._ema_active_ratio + (1 - self._ema_decay) * avg_active_ratio
+        self._zero_streak = self._zero_streak + 1 if avg_active_ratio == 0.0 else 0
+        if self._zero_streak >= self._zero_streak_needed:
+            self._force_zero = True
+        self._force_dense = self._ema_active_ratio > self._dense_threshold
+
+    def _record_runtime_dispatch(self, runtime_backend: str):
+        """Count forwards whose path differs from the dispatch decision
+        stamped on the module (sf_dispatch_decision / sf_backend_mode)."""
+        expected = str(getattr(self, "sf_dispatch_decision", getattr(self, "sf_backend_mode", ""))).strip().lower()
+        if not expected:
+            return
+        self._runtime_dispatch_seen += 1
+        if expected != runtime_backend:
+            self._runtime_dispatch_mismatch += 1
+
     # ---- forward ----------------------------------------------------------------
     def forward(self, x: torch.Tensor):
         self.fallback_reason = ""
         if self.profile_runtime:
             self._profile.calls += 1
             t_total = self._stamp()
+        if x.dim() not in (4, 5):
+            raise ValueError(f"Expected 4D or 5D input, got {x.dim()}D")
+        if self.runtime_policy and self._force_zero:
+            y = self._zero_output_5d(x) if x.dim() == 5 else self._zero_output_4d(x)
+            self._last_sparse_ms = 0.0
+            self.fallback_reason = "force_zero"
+            self._record_runtime_dispatch("staticzero")
+            if self.profile_runtime:
+                self._profile.zero_path_hits += 1
+                self._profile.last_path = "zero(force)"
+                ms = self._elapsed_ms(t_total)
+                self._profile.total_ms += ms
+                self._profile.last_total_ms = ms
+            return y
         if x.dim() == 5:
             T, B = int(x.shape[0]), int(x.shape[1])
             x4d = x.reshape(T * B, *x.shape[2:])
@@ -237,12 +300,18 @@ class SparseConv2d(nn.Module):
             x4d = x
         else:
             raise ValueError(f"Expected 4D or 5D input, got {x.dim()}D")
+
+        forced_dense = self.runtime_policy and self._force_dense
+        need_ratio = x4d.is_cuda and not forced_dense and self._should_collect_ratio()
         self._forward_count += 1
 
-        if x4d.is_cuda and self._supports_sparse() and self.backend_mode != "dense":
-            y4d, backend = self._hip_forward(x4d)
+        ratio = None
+        if x4d.is_cuda and self._supports_sparse() and self.backend_mode != "dense" and not forced_dense:
+            y4d, backend, ratio = self._hip_forward(x4d, need_ratio)
             path = {"dense_fallback": "dense(fallback)", "zero_tiles_only": "zero(tile_compaction)"}.get(
                 backend, "sparse")
+            self._record_runtime_dispatch({"dense_fallback": "dense", "zero_tiles_only": "staticzero"}.get(
+                backend, "sparse"))
             if self.profile_runtime:
                 if path == "sparse":
                     self._profile.sparse_path_hits += 1
@@ -253,9 +322,17 @@ class SparseConv2d(nn.Module):
         else:
             y4d = self._fallback_forward(x4d)
             path = "dense"
-            self.fallback_reason = "dispatch_dense" if self.backend_mode == "dense" else "module_dense_path"
+            self.fallback_reason = ("force_dense" if forced_dense else
+                                    "dispatch_dense" if self.backend_mode == "dense" else "module_dense_path")
+            self._record_runtime_dispatch("dense")
             if self.profile_runtime:
                 self._profile.dense_path_hits += 1
+
+        self._update_policy(ratio)
+        if self.runtime_policy and self._force_zero and ratio == 0.0:
+            y4d = self._zero_output_4d(x4d)
+            path = "zero(promoted)"
+            self.fallback_reason = "zero_promoted"
 
         y = y4d.reshape(T, B, *y4d.shape[1:]) if x.dim() == 5 else y4d
         if self.profile_runtime:
@@ -265,10 +342,12 @@ class SparseConv2d(nn.Module):
             self._profile.total_ms += ms
             self._profile.last_total_ms = ms
         if self.collect_diag:
+            self._last_diag["runtime_dispatch_seen"] = int(self._runtime_dispatch_seen)
+            self._last_diag["runtime_dispatch_mismatch"] = int(self._runtime_dispatch_mismatch)
             self._last_diag["fallback_reason"] = str(self.fallback_reason)
         return y
 
-    def _hip_forward(self, x4d):
+    def _hip_forward(self, x4d, need_ratio=False):
         want_diag = self.collect_diag and not self._inference_mode
         k = self.kernel_size[0]
         result = sparse_conv2d_forward(
@@ -277,7 +356,7 @@ class SparseConv2d(nn.Module):
             dilation=self.dilation[0], groups=self.groups, threshold=self.threshold,
             w_cl=self._get_w_tap(),
             return_ms=self.return_ms,
-            return_avg_active_ratio=want_diag,
+            return_avg_active_ratio=want_diag or need_ratio,
             return_tile_stats=want_diag,
             return_backend_meta=True,
             output_dtype=x4d.dtype,
@@ -289,6 +368,9 @@ class SparseConv2d(nn.Module):
         if want_diag:
             ratio, stats = result[2], result[3]
             idx = 4
+        elif need_ratio:
+            ratio = result[2]
+            idx = 3
         meta = result[idx]
         backend = meta.get("backend", BACKEND_NAME)
         if backend == "dense_fallback":
@@ -298,11 +380,9 @@ class SparseConv2d(nn.Module):
         if self.profile_runtime:
             self._profile.sparse_kernel_ms += self._last_sparse_ms
             self._profile.last_sparse_kernel_ms = self._last_sparse_ms
-        if ratio is not None:
-            self._last_avg_active_ratio = float(ratio)
         if want_diag:
             self._collect_diag(x4d, ms, ratio, stats, meta)
-        return y, backend
+        return y, backend, ratio
 
     def _collect_diag(self, x4d, ms, ratio, stats, meta):
         """Diagnostics with host syncs; never enabled on timed runs."""

@@ -52,6 +52,16 @@ EXPORTS = {
     "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
     "sf_lif_multistep": (c_int, [_P, _P, c_int32, c_int32, c_int64, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P, _P,
                                  _P]),
+    "sf_linear_bitmap_bytes": (c_size_t, [c_int64, c_int32]),
+    "sf_linear_flags_bytes": (c_size_t, [c_int64]),
+    "sf_linear_workspace_size": (c_size_t, [c_int64, c_int32]),
+    "sf_linear_prescan": (c_int, [_P, c_int32, c_int64, c_int32, c_float, _P, _P, _P]),
+    "sf_linear_sparse": (c_int, [_P, _P, _P, c_int32, c_int64, c_int32, _P, _P, c_int32, _P, c_int32, _P]),
+    "sf_linear_forward": (c_int, [_P, c_int32, c_int64, c_int32, _P, _P, c_int32, c_float, _P, c_size_t, _P, c_int32,
+                                  _P]),
+    "sf_bmm_supported": (c_int, [c_int32, c_int32]),
+    "sf_bmm_sparse": (c_int, [_P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_float,
+                              _P, c_int32, _P]),
     "sf_timing_enable": (c_int, [c_int32]),
     "sf_timing_collect": (c_int, []),
     "sf_timing_query": (c_int64, [ctypes.c_char_p, ctypes.POINTER(c_double)]),
@@ -311,11 +321,71 @@ def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torc
 
 
 # ---------------------------------------------------------------------------
+# Sparse linear / batched matmul
+# ---------------------------------------------------------------------------
+
+def linear_prescan(x2d: torch.Tensor, threshold: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """x [m, k] (contiguous) -> (bits int32 [m * words], flags int32) of the
+    row prescan (sf_linear_prescan)."""
+    _require_device(x2d, "x")
+    m, k = (int(v) for v in x2d.shape)
+    L = lib()
+    bits = torch.empty(max(int(L.sf_linear_bitmap_bytes(m, k)) // 4, 1), dtype=torch.int32, device=x2d.device)
+    flags = torch.empty(max(int(L.sf_linear_flags_bytes(m)) // 4, 1), dtype=torch.int32, device=x2d.device)
+    rc = L.sf_linear_prescan(_ptr(x2d), dtype_code(x2d.dtype), m, k, float(threshold), _ptr(bits), _ptr(flags),
+                             _stream(x2d.device))
+    _check(rc, "sf_linear_prescan")
+    return bits, flags
+
+
+def linear_workspace_size(m: int, k: int) -> int:
+    return int(lib().sf_linear_workspace_size(int(m), int(k)))
+
+
+def linear_forward(x2d: torch.Tensor, wt: torch.Tensor, bias: Optional[torch.Tensor], threshold: float,
+                   y: torch.Tensor, workspace: torch.Tensor) -> torch.Tensor:
+    """y [m, c_out] = x [m, k] @ wt [k, c_out] (f32) + bias (sf_linear_forward)."""
+    _require_device(x2d, "x")
+    m, k = (int(v) for v in x2d.shape)
+    rc = lib().sf_linear_forward(_ptr(x2d), dtype_code(x2d.dtype), m, k, _ptr(wt), _ptr(bias), int(wt.shape[1]),
+                                 float(threshold), _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                 _ptr(y), dtype_code(y.dtype), _stream(x2d.device))
+    _check(rc, "sf_linear_forward")
+    return y
+
+
+def linear_sparse(bits: torch.Tensor, flags: torch.Tensor, x2d: torch.Tensor, wt: torch.Tensor,
+                  bias: Optional[torch.Tensor], y: torch.Tensor) -> torch.Tensor:
+    m, k = (int(v) for v in x2d.shape)
+    rc = lib().sf_linear_sparse(_ptr(bits), _ptr(flags), _ptr(x2d), dtype_code(x2d.dtype), m, k, _ptr(wt),
+                                _ptr(bias), int(wt.shape[1]), _ptr(y), dtype_code(y.dtype), _stream(x2d.device))
+    _check(rc, "sf_linear_sparse")
+    return y
+
+
+def bmm_supported(k: int, n: int) -> bool:
+    return bool(lib().sf_bmm_supported(int(k), int(n)))
+
+
+def bmm_sparse(a: torch.Tensor, b: torch.Tensor, threshold: float, c: torch.Tensor) -> torch.Tensor:
+    """c [B, m, n] = a [B, m, k] (contiguous) @ b [B, k, n] (any strides,
+    same dtype as a) (sf_bmm_sparse)."""
+    _require_device(a, "a")
+    _require_device(b, "b")
+    bt, m, k = (int(v) for v in a.shape)
+    n = int(b.shape[2])
+    rc = lib().sf_bmm_sparse(_ptr(a), _ptr(b), dtype_code(a.dtype), bt, m, k, n, int(b.stride(0)), int(b.stride(1)),
+                             int(b.stride(2)), float(threshold), _ptr(c), dtype_code(c.dtype), _stream(a.device))
+    _check(rc, "sf_bmm_sparse")
+    return c
+
+
+# ---------------------------------------------------------------------------
 # Per-kernel timing (bench instrumentation)
 # ---------------------------------------------------------------------------
 
 KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
-                "lif_multistep")
+                "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse")
 
 
 def timing_enable(on: bool) -> None:

@@ -194,7 +194,7 @@ double g_total_ms[sf::K_COUNT] = {};
 int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
-                                     "lif_multistep"};
+                                     "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse"};
 
 }  // namespace
 
@@ -372,6 +372,133 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
   }
   rc = sf::launch_conv(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "conv_gather launch");
+  return SF_OK;
+}
+
+// ---- sparse linear ------------------------------------------------------------
+
+size_t sf_linear_bitmap_bytes(int64_t m, int32_t k) {
+  if (m <= 0 || k < 1) return 0;
+  return (size_t)m * (size_t)sf::linear_words_per_row(k) * 4u;
+}
+
+size_t sf_linear_flags_bytes(int64_t m) {
+  if (m <= 0) return 0;
+  return (size_t)((m + sf::kLinearRowChunk - 1) / sf::kLinearRowChunk) * 4u;
+}
+
+size_t sf_linear_workspace_size(int64_t m, int32_t k) {
+  if (m <= 0 || k < 1) return 0;
+  return align256(sf_linear_bitmap_bytes(m, k)) + align256(sf_linear_flags_bytes(m));
+}
+
+int sf_linear_prescan(const void* x, int32_t dtype, int64_t m, int32_t k, float threshold, uint32_t* bits,
+                      uint32_t* flags, void* stream) {
+  if (m < 0 || k < 1) return fail(SF_ERR_INVALID, "bad linear prescan shape");
+  if (!dtype_ok(dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (m >= (1ll << 30)) return fail(SF_ERR_UNSUPPORTED, "m >= 2^30 rows");
+  if (m == 0) return SF_OK;
+  if (x == nullptr || bits == nullptr || flags == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  sf::PackArgs a{};
+  a.x = x;
+  a.bits = bits;
+  a.flags = flags;
+  a.n = m;
+  a.c = k;
+  a.cwp = sf::linear_words_per_row(k);
+  a.total_chunks = (m + sf::kLinearRowChunk - 1) / sf::kLinearRowChunk;
+  a.cutoff = sf_activity_cutoff(threshold);
+  const int rc = sf::launch_pack_rows(a, dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "prescan_rows launch");
+  return SF_OK;
+}
+
+int sf_linear_sparse(const uint32_t* bits, const uint32_t* flags, const void* x, int32_t in_dtype, int64_t m,
+                     int32_t k, const float* wt, const float* bias, int32_t c_out, void* y, int32_t out_dtype,
+                     void* stream) {
+  if (m < 0 || k < 1 || c_out < 1) return fail(SF_ERR_INVALID, "bad linear shape");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  if (c_out % 4 != 0) return fail(SF_ERR_UNSUPPORTED, "c_out must be a multiple of 4");
+  if (m >= (1ll << 30)) return fail(SF_ERR_UNSUPPORTED, "m >= 2^30 rows");
+  if (m == 0) return SF_OK;
+  if (bits == nullptr || flags == nullptr || x == nullptr || wt == nullptr || y == nullptr)
+    return fail(SF_ERR_INVALID, "NULL pointer");
+  sf::ConvArgs a{};
+  a.bits = bits;
+  a.flags = flags;
+  a.x = x;
+  a.wt = wt;
+  a.bias = bias;
+  a.y = y;
+  a.n = 1;
+  a.c_in = k;
+  a.h_in = a.h_out = (int)m;
+  a.w_in = a.w_out = 1;
+  a.hw_in = a.hw_out = (int)m;
+  a.c_out = c_out;
+  a.k = 1;
+  a.s = 1;
+  a.cwp = sf::linear_words_per_row(k);
+  a.chunk = sf::kLinearRowChunk;
+  a.chunks_per_frame = (m + sf::kLinearRowChunk - 1) / sf::kLinearRowChunk;
+  a.T = 1;
+  const int rc = sf::launch_linear_flat(a, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "linear_flat launch");
+  return SF_OK;
+}
+
+int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k, const float* wt, const float* bias,
+                      int32_t c_out, float threshold, void* workspace, size_t workspace_bytes, void* y,
+                      int32_t out_dtype, void* stream) {
+  if (m < 0 || k < 1 || c_out < 1) return fail(SF_ERR_INVALID, "bad linear shape");
+  if (m == 0) return SF_OK;
+  if (workspace == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  if (workspace_bytes < sf_linear_workspace_size(m, k)) return fail(SF_ERR_WORKSPACE, "workspace too small");
+  uint32_t* bits = static_cast<uint32_t*>(workspace);
+  uint32_t* flags =
+      reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + align256(sf_linear_bitmap_bytes(m, k)));
+  // Validate the Stage-2 arguments before the prescan is queued.
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  if (c_out % 4 != 0) return fail(SF_ERR_UNSUPPORTED, "c_out must be a multiple of 4");
+  if (x == nullptr || wt == nullptr || y == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  int rc = sf_linear_prescan(x, in_dtype, m, k, threshold, bits, flags, stream);
+  if (rc != SF_OK) return rc;
+  return sf_linear_sparse(bits, flags, x, in_dtype, m, k, wt, bias, c_out, y, out_dtype, stream);
+}
+
+// ---- sparse batched matmul ------------------------------------------------------
+
+int sf_bmm_supported(int32_t k, int32_t n) { return k >= 1 && n >= 1 && sf::bmm_column_blocks(k, n) > 0; }
+
+int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batches, int32_t m, int32_t k, int32_t n,
+                  int64_t b_stride_batch, int64_t b_stride_k, int64_t b_stride_n, float threshold, void* c,
+                  int32_t out_dtype, void* stream) {
+  if (batches < 0 || m < 0 || k < 1 || n < 1) return fail(SF_ERR_INVALID, "bad bmm shape");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  if (sf::bmm_column_blocks(k, n) == 0) return fail(SF_ERR_UNSUPPORTED, "k > 252: a 64-column block of B exceeds the 64 KB LDS budget");
+  if (b_stride_k < 0 || b_stride_n < 0 || b_stride_batch < 0) return fail(SF_ERR_INVALID, "negative stride");
+  if (batches == 0 || m == 0) return SF_OK;
+  if (a == nullptr || b == nullptr || c == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  sf::BmmArgs args{};
+  args.a = a;
+  args.b = b;
+  args.c = c;
+  args.batches = batches;
+  args.m = m;
+  args.k = k;
+  args.n = n;
+  args.b_stride_batch = b_stride_batch;
+  args.b_stride_k = b_stride_k;
+  args.b_stride_n = b_stride_n;
+  args.cutoff = sf_activity_cutoff(threshold);
+  const int rc = sf::launch_bmm(args, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "bmm_sparse launch");
   return SF_OK;
 }
 

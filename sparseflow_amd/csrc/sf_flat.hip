@@ -18,6 +18,11 @@
 // the wavefronts never synchronise, beyond that chunk c+1 streams into the
 // second buffer (direct global->LDS loads) while chunk c is walked.
 //
+// The same kernel serves the sparse linear (ROWS = true): a "pixel" is a row
+// of x [m, k] (k contiguous, one frame), non-binary values are read along
+// the row and the lane's 64 outputs are one contiguous 256-byte run of the
+// row-major y [m, c_out], written as 16-byte pieces.
+//
 // Output element (co, p) = bias[co] + its spikes summed by one lane in
 // increasing ci: deterministic from run to run.
 // Replaces the reference's sparse_conv1x1_nhwc_kernel_8x8/8x16
@@ -104,7 +109,16 @@ __device__ __forceinline__ void px_store(const float (&acc)[64], TOut* __restric
   }
 }
 
-template <int CW, typename TIn>
+// Row-major store: the lane's outputs co0 .. co0+nco-1 are contiguous
+// (nco % 4 == 0).
+template <typename TOut>
+__device__ __forceinline__ void px_store_rows(const float (&acc)[64], TOut* __restrict__ yp, int nco) {
+#pragma unroll
+  for (int s = 0; s < 16; ++s)
+    if (nco >= 64 || 4 * s < nco) store4<TOut>(yp + 4 * s, acc[4 * s], acc[4 * s + 1], acc[4 * s + 2], acc[4 * s + 3]);
+}
+
+template <int CW, typename TIn, bool ROWS>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                const uint32_t* __restrict__ flags,
                                                                const TIn* __restrict__ x,
@@ -157,7 +171,9 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
       for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
       value = f != 0u;
     }
-    const TIn* xp = x + (int64_t)frame * a.c_in * hw + p0 + lane;  // this lane's pixel, channel 0
+    // This lane's pixel (row), channel 0, and the distance between channels.
+    const TIn* xp = ROWS ? x + (int64_t)(p0 + lane) * a.c_in : x + (int64_t)frame * a.c_in * hw + p0 + lane;
+    const int64_t xcs = ROWS ? 1 : hw;
     if (!resident) {
       __syncthreads();  // the previous pass is done with both buffers
       load_chunk_px(smem, wt, 0, a.c_in, a.c_out, co0, wave, lane);
@@ -186,7 +202,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
             const int r = j * BITS + px_first_bit(m);
             m &= m - 1;
             float xv = 1.f;
-            if (value) xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * hw]);
+            if (value) xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * xcs]);
             px_add_row(acc, chunk, r, xv);
           }
         }
@@ -196,7 +212,13 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
         __syncthreads();
       }
     }
-    if (mine) {
+    if (mine && ROWS) {
+      const int64_t yb = (int64_t)(p0 + lane) * c_out_t + co0;
+      const int nco = min(64, c_out_t - co0);
+      if (out_dtype == SF_F16) px_store_rows(acc, static_cast<__half*>(y) + yb, nco);
+      else if (out_dtype == SF_BF16) px_store_rows(acc, static_cast<__hip_bfloat16*>(y) + yb, nco);
+      else px_store_rows(acc, static_cast<float*>(y) + yb, nco);
+    } else if (mine) {
       const int64_t yb = ((int64_t)frame * c_out_t + co0) * hw_t + p0 + lane;
       const int nco = min(64, c_out_t - co0);
       if (out_dtype == SF_F16) px_store(acc, static_cast<__half*>(y) + yb, hw_t, nco);
@@ -206,7 +228,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
   }
 }
 
-template <int CW, typename TIn>
+template <int CW, typename TIn, bool ROWS>
 int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
   const int nchunks = CW < kPxChunkWords ? 1 : a.cwp / kPxChunkWords;
@@ -219,7 +241,7 @@ int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_flat<CW, TIn>;
+  auto kern = k_conv_flat<CW, TIn, ROWS>;
   static bool attr_done = false;
   if (!attr_done) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -231,12 +253,12 @@ int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
-template <typename TIn>
+template <typename TIn, bool ROWS>
 int launch_flat_d(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   switch (a.cwp) {
-    case 1: return launch_flat_t<1, TIn>(a, out_dtype, stream);
-    case 2: return launch_flat_t<2, TIn>(a, out_dtype, stream);
-    default: return launch_flat_t<4, TIn>(a, out_dtype, stream);
+    case 1: return launch_flat_t<1, TIn, ROWS>(a, out_dtype, stream);
+    case 2: return launch_flat_t<2, TIn, ROWS>(a, out_dtype, stream);
+    default: return launch_flat_t<4, TIn, ROWS>(a, out_dtype, stream);
   }
 }
 
@@ -249,10 +271,19 @@ bool flat_applicable(const ConvArgs& a) {
 
 int launch_conv_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
   timing_begin(K_FLAT, stream);
-  const int rc = in_dtype == SF_F16    ? launch_flat_d<__half>(a, out_dtype, stream)
-                 : in_dtype == SF_BF16 ? launch_flat_d<__hip_bfloat16>(a, out_dtype, stream)
-                                       : launch_flat_d<float>(a, out_dtype, stream);
+  const int rc = in_dtype == SF_F16    ? launch_flat_d<__half, false>(a, out_dtype, stream)
+                 : in_dtype == SF_BF16 ? launch_flat_d<__hip_bfloat16, false>(a, out_dtype, stream)
+                                       : launch_flat_d<float, false>(a, out_dtype, stream);
   timing_end(K_FLAT, stream);
+  return rc;
+}
+
+int launch_linear_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  timing_begin(K_LINEAR, stream);
+  const int rc = in_dtype == SF_F16    ? launch_flat_d<__half, true>(a, out_dtype, stream)
+                 : in_dtype == SF_BF16 ? launch_flat_d<__hip_bfloat16, true>(a, out_dtype, stream)
+                                       : launch_flat_d<float, true>(a, out_dtype, stream);
+  timing_end(K_LINEAR, stream);
   return rc;
 }
 

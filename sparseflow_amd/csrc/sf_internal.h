@@ -115,13 +115,41 @@ int launch_lif_multistep(const void* x, const void* x2, int in_dtype, int T, int
                          int out_dtype, float* v_out, uint32_t* bits, int cwp, uint32_t* flags, int64_t nflags,
                          hipStream_t stream);
 
+// Sparse linear (row-major x [m, k], weight wt [k, c_out]): row prescan and
+// the flat lane = row Stage 2.  Bitmap words per row: ceil(k/32), rounded up
+// to a multiple of 4 beyond two words; one flag word per kLinearRowChunk rows.
+constexpr int kLinearRowChunk = 16;
+int linear_words_per_row(int k);
+int launch_pack_rows(const PackArgs& a, int dtype, hipStream_t stream);
+// a: n = 1, hw_in = h_in = h_out = m, w = 1, c_in = k, cwp, chunk =
+// kLinearRowChunk, chunks_per_frame = row chunks; y is [m, c_out].
+int launch_linear_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
+// Sparse batched matmul C[b] = A[b] @ B[b] (A [batches, m, k] contiguous,
+// B through strides, C [batches, m, n] contiguous).
+struct BmmArgs {
+  const void* a;
+  const void* b;
+  void* c;
+  int64_t batches;
+  int m, k, n;
+  int64_t b_stride_batch, b_stride_k, b_stride_n;  // elements
+  int ncb;                                          // column blocks (set by the launcher)
+  float cutoff;
+};
+constexpr int kBmmLdsBytes = 64 * 1024;  // staged B block per workgroup
+// Columns per block / 64 (4, 2 or 1) for a k x n B, or 0 when even a
+// 64-column block of k rows exceeds the LDS budget.
+int bmm_column_blocks(int k, int n);
+int launch_bmm(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
 
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_COUNT = 10 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_COUNT = 13 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

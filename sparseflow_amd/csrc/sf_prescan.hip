@@ -166,6 +166,59 @@ __global__ __launch_bounds__(512) void k_pack(PackArgs a) {
   }
 }
 
+// Row-major prescan for the sparse linear: x [m, k] (k contiguous) -> bitmap
+// [m][cwp] (bit j of word w = |x[r, 32w + j]| >= cutoff; words past the
+// row's last element are zero) and one non-binary flag word per chunk of
+// kLinearRowChunk rows.  One wavefront per chunk: each load covers 64
+// consecutive elements of a row and one ballot turns them into two bitmap
+// words.  The (row, 64-element segment) items of the chunk are taken eight
+// at a time so that eight loads are in flight per lane.
+// (a.n = rows, a.c = k, a.total_chunks = row chunks.)
+template <typename T>
+__global__ __launch_bounds__(256) void k_pack_rows(PackArgs a) {
+  const int lane = lane_id();
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (chunk >= a.total_chunks) return;  // the kernel has no block-level barrier
+  const int64_t r0 = chunk * kLinearRowChunk;
+  const int rows = (int)min((int64_t)kLinearRowChunk, a.n - r0);
+  const int k = a.c, cwp = a.cwp;
+  const int nseg = (k + 63) / 64;
+  const int items = rows * nseg;
+  const T* __restrict__ x = static_cast<const T*>(a.x) + r0 * (int64_t)k;
+  uint32_t* __restrict__ bits = a.bits + r0 * (int64_t)cwp;
+  const float cut = a.cutoff;
+  uint32_t nb = 0u;
+  int r = 0, sg = 0;  // item i0 = r * nseg + sg
+  for (int i0 = 0; i0 < items; i0 += 8) {
+    float v[8];
+    int rr[8], ss[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      rr[u] = r;
+      ss[u] = sg;
+      const int kk = sg * 64 + lane;
+      v[u] = (i0 + u < items && kk < k) ? to_f32<T>(x[(int64_t)r * k + kk]) : 0.f;
+      if (++sg == nseg) { sg = 0; ++r; }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint64_t m = __ballot(fabsf(v[u]) >= cut);
+      nb |= (v[u] != 0.f && v[u] != 1.f) ? 1u : 0u;
+      const int w = 2 * ss[u] + lane;
+      if (i0 + u < items && lane < 2 && w < cwp)
+        bits[(int64_t)rr[u] * cwp + w] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
+    }
+  }
+  if (2 * nseg < cwp) {  // padding words of the chunk's rows
+    for (int i = lane; i < rows * (cwp - 2 * nseg); i += kWave) {
+      const int rw = i / (cwp - 2 * nseg);
+      bits[(int64_t)rw * cwp + 2 * nseg + (i - rw * (cwp - 2 * nseg))] = 0u;
+    }
+  }
+  const uint64_t bal = __ballot(nb != 0u);
+  if (lane == 0) a.flags[chunk] = bal != 0ull ? 1u : 0u;
+}
+
 // One wavefront per output tile.  Requires cwp <= 64 (a power of two), so
 // lane l always reads word (l % cwp) of the pixels it visits.
 __global__ __launch_bounds__(256) void k_tiles(TilesArgs a) {
@@ -330,6 +383,30 @@ int launch_tiles(const TilesArgs& a, hipStream_t stream) {
   const int rc = (int)hipGetLastError();
   timing_end(K_TILES, stream);
   return rc;
+}
+
+}  // namespace sf
+
+namespace sf {
+
+int linear_words_per_row(int k) {
+  const int w = (k + 31) / 32;
+  return w <= 2 ? w : (w + 3) / 4 * 4;
+}
+
+int launch_pack_rows(const PackArgs& a, int dtype, hipStream_t stream) {
+  const int64_t blocks = (a.total_chunks + 3) / 4;
+  if (blocks == 0) return (int)hipSuccess;
+  timing_begin(K_PACK_ROWS, stream);
+  switch (dtype) {
+    case SF_F16: hipLaunchKernelGGL(k_pack_rows<__half>, dim3((unsigned)blocks), dim3(256), 0, stream, a); break;
+    case SF_BF16:
+      hipLaunchKernelGGL(k_pack_rows<__hip_bfloat16>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+      break;
+    default: hipLaunchKernelGGL(k_pack_rows<float>, dim3((unsigned)blocks), dim3(256), 0, stream, a); break;
+  }
+  timing_end(K_PACK_ROWS, stream);
+  return (int)hipGetLastError();
 }
 
 }  // namespace sf

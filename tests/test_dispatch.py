@@ -105,3 +105,37 @@ def test_dispatch_all_layers_accepts_targets():
     dec = dp.dispatch_all_layers([t, {"name": "p", "op_type": "maxpool2d"}], {"l.conv": {"density": 0.01}})
     assert dec["l.conv"].backend == "sparse" and dec["p"].backend == "dense"
     assert dec["p"].reason_code == "pool_dense_keep"
+
+
+def test_runtime_policy_state_machine():
+    # Ops/sparse_conv2d.py:462-496: warmup seeds the EMA, a zero streak
+    # forces the zero path, an EMA above the dense threshold forces dense.
+    m = SparseConv2d(8, 8, 3, 1, 1, warmup_steps=2, zero_streak_needed=2, ema_decay=0.5, dense_threshold=0.85)
+    m.runtime_policy = True
+    assert m._should_collect_ratio()
+    m._update_policy(0.9)
+    m._update_policy(0.9)
+    assert m._warmup_left == 0 and not m._force_dense
+    m._update_policy(0.9)
+    assert m._force_dense and abs(m._ema_active_ratio - 0.9) < 1e-12
+    m._update_policy(0.0)            # EMA 0.45 -> not dense; streak 1
+    assert not m._force_dense and not m._force_zero
+    m._update_policy(0.0)
+    assert m._force_zero
+    m._forward_count = 31
+    assert not m._should_collect_ratio()
+    m._forward_count = 32
+    assert m._should_collect_ratio()
+    off = SparseConv2d(8, 8, 3, 1, 1)
+    assert not off.runtime_policy and not off._should_collect_ratio()
+    off._update_policy(0.0)
+    assert off._last_avg_active_ratio == 0.0 and not off._force_zero
+
+
+def test_runtime_policy_force_zero_output_on_cpu():
+    m = SparseConv2d(4, 6, 3, 1, 1, bias=True)
+    m.runtime_policy, m._force_zero = True, True
+    x = torch.randn(2, 3, 4, 5, 5)
+    y = m(x)
+    assert y.shape == (2, 3, 6, 5, 5) and m.fallback_reason == "force_zero"
+    assert torch.equal(y, m.bias.detach().view(1, 1, -1, 1, 1).expand_as(y))

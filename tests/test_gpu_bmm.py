@@ -1,0 +1,118 @@
+"""Sparse batched matmul and attention stages on the GPU (sf_bmm_sparse via
+Kernels.bmm / Kernels.attention / SparseAttention).
+
+Bar: fp32 within 1e-4 abs + 1e-4 rel of float64 torch.bmm on the activity-
+masked A; fp16/bf16 within 1e-2; K^T read through strides equals the
+contiguous copy bit for bit."""
+
+import pytest
+import torch
+
+from oracle import linear as olin
+from sparseflow_amd import _lib
+from sparseflow_amd.Kernels.attention import sparse_attn_v_forward, sparse_qk_forward
+from sparseflow_amd.Kernels.bmm import sparse_bmm_forward
+from sparseflow_amd.Ops import SparseAttention, SparseBMM, SparseMatmul
+from tests.gpu_helpers import DEV, announce, close, native_loaded, spikes
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = dict(atol=1e-4, rtol=1e-4)
+
+
+def _run(a, b, **kw):
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        c = sparse_bmm_forward(a, b, **kw)[0]
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return c, {k: n for k, (n, _) in stats.items() if n > 0}
+
+
+CASES = [  # (batches, m, k, n)
+    (1, 1, 1, 1), (3, 5, 7, 9), (48, 196, 32, 196), (48, 196, 196, 32), (4, 64, 252, 64), (2, 300, 64, 300),
+    (5, 17, 130, 70), (2, 8, 40, 513),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("density", [0.0, 0.1, 0.6])
+def test_bmm_fp32_matches_dense(case, density):
+    bt, m, k, n = case
+    announce(f"bmm {case} p={density}")
+    a = spikes((bt, m, k), density, seed=m + k)
+    b = torch.randn(bt, k, n, generator=torch.Generator().manual_seed(n))
+    c, kernels = _run(a.to(DEV), b.to(DEV))
+    assert "bmm_sparse" in kernels, kernels
+    ok, err, _ = close(c, olin.bmm_ref(a, b), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    assert native_loaded()
+
+
+def test_bmm_strided_b_equals_contiguous():
+    a = spikes((24, 196, 32), 0.1, seed=1).to(DEV)
+    k = spikes((24, 196, 32), 0.1, seed=2).to(DEV)
+    announce("bmm strided K^T")
+    c1, _ = _run(a, k.transpose(1, 2))
+    c2, _ = _run(a, k.transpose(1, 2).contiguous())
+    assert torch.equal(c1, c2)
+    ok, err, _ = close(c1, olin.bmm_ref(a.cpu(), k.cpu().transpose(1, 2)), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_bmm_value_a_and_half():
+    g = torch.Generator().manual_seed(3)
+    a = spikes((12, 196, 196), 0.3, seed=4) * torch.randint(1, 5, (12, 196, 196), generator=g).float() * 0.17
+    b = spikes((12, 196, 32), 0.1, seed=5)
+    announce("bmm attn @ v")
+    c, _ = _run(a.to(DEV), b.to(DEV))
+    ok, err, _ = close(c, olin.bmm_ref(a, b), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    for dt in (torch.float16, torch.bfloat16):
+        c, _ = _run(a.to(DEV, dt), b.to(DEV, dt))
+        assert c.dtype == dt
+        ok, err, _ = close(c, olin.bmm_ref(a.to(dt).float(), b.to(dt).float()), atol=1e-2, rtol=1e-2)
+        assert ok, f"{dt}: max abs err {err}"
+
+
+def test_bmm_large_k_falls_back():
+    a = spikes((2, 8, 300), 0.1, seed=6)
+    b = torch.randn(2, 300, 16, generator=torch.Generator().manual_seed(7))
+    c, kernels = _run(a.to(DEV), b.to(DEV), return_tile_stats=True)
+    assert "bmm_sparse" not in kernels
+    ok, err, _ = close(c, olin.bmm_ref(a, b), **FP32_TOL)
+    assert ok
+
+
+def test_attention_stages_and_modules():
+    T, N, H, S, D = 2, 3, 4, 50, 32
+    q = spikes((T * N, H, S, D), 0.1, seed=8)
+    k = spikes((T * N, H, S, D), 0.1, seed=9)
+    v = spikes((T * N, H, S, D), 0.1, seed=10)
+    announce("attention qk / av")
+    attn, _ = sparse_qk_forward(q.to(DEV), k.to(DEV))
+    ref_attn = torch.matmul(q.double(), k.double().transpose(-2, -1)) * D ** -0.5
+    ok, err, _ = close(attn, ref_attn, **FP32_TOL)
+    assert ok, f"qk err {err}"
+    out, _ = sparse_attn_v_forward(attn, v.to(DEV))
+    ok, err, _ = close(out, torch.matmul(ref_attn, v.double()), **FP32_TOL)
+    assert ok, f"av err {err}"
+    sa = SparseAttention(H, D)
+    ok, _, _ = close(sa.av(sa.qk(q.to(DEV), k.to(DEV)), v.to(DEV)), torch.matmul(ref_attn, v.double()), **FP32_TOL)
+    assert ok
+    bm = SparseBMM()
+    bm.collect_diag = True
+    c = bm(q.reshape(-1, S, D).to(DEV), v.reshape(-1, S, D).transpose(1, 2).contiguous().to(DEV))
+    assert c.shape == (T * N * H, S, S) and "total_tile_count" in bm._last_diag
+    mm = SparseMatmul()
+    a2 = spikes((70, 40), 0.2, seed=11)
+    b2 = torch.randn(40, 24, generator=torch.Generator().manual_seed(12))
+    ok, err, _ = close(mm(a2.to(DEV), b2.to(DEV)), olin.linear_ref(a2, b2.t(), None), **FP32_TOL)
+    assert ok, f"matmul err {err}"
+    b3 = torch.randn(40, 22, generator=torch.Generator().manual_seed(13))  # n % 4 != 0: batched path
+    ok, err, _ = close(mm(a2.to(DEV), b3.to(DEV)), olin.linear_ref(a2, b3.t(), None), **FP32_TOL)
+    assert ok, f"matmul (bmm path) err {err}"

@@ -83,3 +83,28 @@ def test_all_dense_dispatch_launches_no_conv_kernel():
         _lib.timing_enable(False)
     conv = {k: c for k, (c, _) in stats.items() if c > 0 and k.startswith("conv")}
     assert not conv, conv
+
+
+def test_runtime_policy_on_device():
+    announce("runtime policy")
+    conv = torch.nn.Conv2d(32, 16, 3, 1, 1).to(DEV)
+    z = SparseConv2d.from_dense(conv, warmup_steps=1, zero_streak_needed=2, calib_every=1)
+    z.runtime_policy = True
+    x0 = torch.zeros(4, 32, 16, 16, device=DEV)
+    for _ in range(3):
+        y = z(x0)
+    assert z._last_avg_active_ratio == 0.0 and z._force_zero
+    xs = (torch.rand(4, 32, 16, 16, generator=torch.Generator().manual_seed(5)) < 0.05).float().to(DEV)
+    y = z(xs)  # sticky, as the reference's policy
+    assert z.fallback_reason == "force_zero"
+    assert torch.equal(y, conv.bias.detach().view(1, -1, 1, 1).expand_as(y))
+
+    d = SparseConv2d.from_dense(conv, warmup_steps=1, calib_every=1)
+    d.runtime_policy = True
+    x1 = torch.ones(4, 32, 16, 16, device=DEV)
+    d(x1)
+    d(x1)
+    assert d._last_avg_active_ratio == 1.0 and d._force_dense
+    y = d(xs)
+    assert d.fallback_reason == "force_dense"
+    assert torch.allclose(y, conv(xs), atol=1e-4, rtol=1e-4)

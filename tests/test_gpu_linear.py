@@ -1,0 +1,138 @@
+"""Sparse Linear on the GPU (sf_linear_prescan / sf_linear_sparse through
+Kernels.linear.sparse_linear_forward and SparseLinear).
+
+Bar: row bitmap and chunk flags bit-exact against oracle/linear.py; fp32
+outputs within 1e-4 abs + 1e-4 rel of float64 F.linear on the activity-
+masked input; fp16/bf16 within 1e-2; bit-identical repeats."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import linear as olin
+from sparseflow_amd import _lib
+from sparseflow_amd.Kernels.linear import sparse_linear_forward
+from sparseflow_amd.Ops.sparse_linear import SparseLinear
+from tests.gpu_helpers import DEV, announce, close, native_loaded, spikes
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = dict(atol=1e-4, rtol=1e-4)
+
+
+def _w(c_out, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(c_out, k, generator=g) * (1.0 / k) ** 0.5
+
+
+def _run(x, w, b, **kw):
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        y = sparse_linear_forward(x, w, b, **kw)[0]
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return y, {k: c for k, (c, _) in stats.items() if c > 0}
+
+
+CASES = [
+    (1, 1, 4), (17, 33, 12), (64, 64, 64), (100, 100, 68), (130, 130, 8), (1000, 384, 384),
+    (4096, 1536, 384), (512, 2048, 1000), (3, 4100, 16),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("density", [0.0, 0.1, 0.5])
+def test_linear_fp32_matches_dense(case, density):
+    m, k, co = case
+    announce(f"linear {case} p={density}")
+    x = spikes((m, k), density, seed=m + k)
+    w = _w(co, k, seed=co)
+    b = torch.randn(co, generator=torch.Generator().manual_seed(5)) * 0.1
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert "linear_flat" in kernels and "prescan_rows" in kernels, kernels
+    ok, err, _ = close(y, olin.linear_ref(x, w, b), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    assert native_loaded()
+
+
+@pytest.mark.parametrize("m,k", [(5, 20), (40, 64), (33, 100), (300, 384), (17, 1536)])
+def test_row_bitmap_and_flags_bit_exact(m, k):
+    announce(f"linear bitmap {m}x{k}")
+    x = spikes((m, k), 0.2, seed=k)
+    x[m // 2, k // 3] = 2.5          # non-binary chunk
+    x[0, 0] = 4e-7                   # below the threshold
+    bits, flags = _lib.linear_prescan(x.to(DEV), 1e-6)
+    words = olin.linear_words_per_row(k)
+    got = bits[: m * words].cpu().numpy().view(np.uint32).reshape(m, words)
+    assert np.array_equal(got, olin.row_bitmap(x.numpy(), 1e-6))
+    nb = flags[: -(-m // 16)].cpu().numpy() != 0
+    assert np.array_equal(nb, olin.row_chunk_nonbinary(x.numpy()))
+
+
+def test_value_path_inputs():
+    g = torch.Generator().manual_seed(7)
+    x = spikes((256, 384), 0.1, seed=8)
+    x[:64] = x[:64] * 2.0                                   # sums of two spike maps
+    x[100:110] = x[100:110] * torch.randn(10, 384, generator=g)
+    w = _w(384, 384, seed=9)
+    announce("linear value path")
+    y, _ = _run(x.to(DEV), w.to(DEV), None)
+    ok, err, _ = close(y, olin.linear_ref(x, w, None), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_linear_half(dtype):
+    x = spikes((512, 384), 0.1, seed=10)
+    x[5] = x[5] * 0.5
+    w = _w(384, 384, seed=11)
+    b = torch.linspace(-0.5, 0.5, 384)
+    announce(f"linear {dtype}")
+    y, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV))
+    assert y.dtype == dtype
+    ok, err, _ = close(y, olin.linear_ref(x.to(dtype).float(), w, b), atol=1e-2, rtol=1e-2)
+    assert ok, f"max abs err {err}"
+    y32, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), output_dtype=torch.float32)
+    assert y32.dtype == torch.float32
+    ok, err, _ = close(y32, olin.linear_ref(x.to(dtype).float(), w, b), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_linear_deterministic_and_stats_path():
+    x = spikes((2048, 384), 0.05, seed=12).to(DEV)
+    w = _w(384, 384, seed=13).to(DEV)
+    announce("linear determinism + stats")
+    y1, _ = _run(x, w, None)
+    y2, _ = _run(x, w, None)
+    assert torch.equal(y1, y2)
+    res = sparse_linear_forward(x, w, None, return_ms=True, return_avg_active_ratio=True, return_tile_stats=True,
+                                return_backend_meta=True)
+    assert torch.equal(res[0], y1)
+    assert 0.0 < res[2] <= 1.0 and res[3]["total_tiles"] == 16 and res[4]["backend"] == "sparse_hip"
+
+
+def test_unsupported_c_out_falls_back_dense():
+    x = spikes((64, 32), 0.1, seed=14)
+    w = _w(6, 32, seed=15)
+    res = sparse_linear_forward(x.to(DEV), w.to(DEV), None, return_backend_meta=True)
+    assert res[2]["backend"] == "dense_fallback"
+    ok, err, _ = close(res[0], olin.linear_ref(x, w, None), **FP32_TOL)
+    assert ok
+
+
+def test_sparse_linear_module_shapes():
+    lin = torch.nn.Linear(384, 1536).to(DEV)
+    sl = SparseLinear.from_dense(lin)
+    x = spikes((4, 8, 49, 384), 0.1, seed=16).to(DEV)
+    announce("SparseLinear module")
+    y = sl(x)
+    assert y.shape == (4, 8, 49, 1536)
+    ok, err, _ = close(y, olin.linear_ref(x.cpu(), lin.weight, lin.bias), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    x5 = spikes((2, 3, 4, 4, 24), 0.2, seed=17).to(DEV)
+    sl5 = SparseLinear.from_dense(torch.nn.Linear(4 * 4 * 24, 8).to(DEV))
+    assert sl5(x5).shape == (2, 3, 8)
