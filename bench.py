@@ -302,7 +302,7 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
     frames.  Each op is timed sparse and dense (hipBLASLt / rocBLAS / MIOpen
     through torch) on the same tensors."""
     from sparseflow_amd import _lib
-    from sparseflow_amd.Kernels.attention import sparse_attn_v_forward, sparse_qk_forward
+    from sparseflow_amd.Kernels.attention import sparse_attn_v_forward, sparse_qk_forward, sparse_spike_attention_forward
     from sparseflow_amd.Kernels.linear import sparse_linear_forward, tap_weight
     from sparseflow_amd.Ops.sparse_conv2d import SparseConv2d
 
@@ -331,6 +331,11 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
                 lambda: sparse_attn_v_forward(attn, qkv[2]),
                 lambda: torch.matmul(attn, qkv[2]),
                 attn.numel() * 4 + 2 * qkv[2].numel() * 4),
+            # q, k, v read once, y written once: the fused form of qk + av.
+            "attention_fused": (
+                lambda: sparse_spike_attention_forward(qkv[0], qkv[1], qkv[2], scale),
+                lambda: torch.matmul(torch.matmul(qkv[0], qkv[1].transpose(-2, -1)) * scale, qkv[2]),
+                4 * qkv[0].numel() * 4),
         }
         for name, (sp_fn, dn_fn, alg) in cases.items():
             ms = time_gpu(sp_fn, steps, warmup)
@@ -356,8 +361,9 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
         torch.backends.cudnn.benchmark = False
         ops["stem_conv3x3_3to384"] = {"us": ms * 1e3, "dense_us": None if dms is None else dms * 1e3,
                                       "speedup_vs_dense": None if dms is None else dms / ms}
-    # One SSA block: q, k, v, proj projections + qk + av.
-    blk = 4 * ops["linear_384x384"]["us"] + ops["qk"]["us"] + ops["av"]["us"]
+    # One SSA block: q, k, v, proj projections + the attention core (fused;
+    # the dense reference runs qk then av).
+    blk = 4 * ops["linear_384x384"]["us"] + ops["attention_fused"]["us"]
     res = {"workload": ATTN_WORKLOAD, "T": T, "N": N, "tokens": tokens, "dim": dim, "heads": heads,
            "spike_p": p, "ops": ops, "ssa_block_us": blk}
     if with_dense:

@@ -220,7 +220,7 @@ int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k,
 
 /* ---- sparse batched matmul -------------------------------------------------- */
 
-/* c[b] = a[b] @ B[b] for b < batches: a [batches, m, k] contiguous and
+/* c[b] = alpha * (a[b] @ B[b]) for b < batches: a [batches, m, k] contiguous and
  * spike-sparse, B read at B[b*b_stride_batch + kk*b_stride_k + j*b_stride_n]
  * (elements; a transposed view such as K^T needs no copy), c [batches, m, n]
  * contiguous in out_dtype (in_dtype or f32).  a and B share in_dtype.
@@ -233,7 +233,26 @@ int sf_bmm_supported(int32_t k, int32_t n);
 int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batches,
                   int32_t m, int32_t k, int32_t n, int64_t b_stride_batch,
                   int64_t b_stride_k, int64_t b_stride_n, float threshold,
-                  void* c, int32_t out_dtype, void* stream);
+                  float alpha, void* c, int32_t out_dtype, void* stream);
+
+/* ---- fused spike attention ------------------------------------------------ */
+
+/* Softmax-free attention core of spiking transformers, per frame tb and head:
+ * y[tb, m, h, :] = scale * sum_d q[tb, m, h, d] * (k^T v)[tb, h, d, :], which
+ * equals (q @ k^T * scale) @ v of the reference's two attention stages
+ * (Kernels/attention.py:27-121; Models/spikformer_github.py:141-146) without
+ * materialising the s x s scores.  Element (tb, m, h, d) of q, k and v is at
+ * tb*qkv_strides[0] + m*qkv_strides[1] + h*qkv_strides[2] + d, of y at the
+ * same form with y_strides (elements; d contiguous).  q elements with
+ * f16(|q|) <= f16(threshold) count as zero.  head_dim d in {16, 32, 64};
+ * supported while sf_spike_attention_supported(s, d).  No counterpart entry
+ * point in the reference (it runs the two stages as separate bmm calls). */
+int sf_spike_attention_supported(int32_t s, int32_t d);
+int sf_spike_attention(const void* q, const void* k, const void* v,
+                       int32_t in_dtype, int64_t tb, int32_t s, int32_t h,
+                       int32_t d, const int64_t* qkv_strides, float scale,
+                       float threshold, void* y, const int64_t* y_strides,
+                       int32_t out_dtype, void* stream);
 
 /* ---- per-kernel timing (bench instrumentation) --------------------------- */
 
@@ -242,7 +261,7 @@ int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batche
  * and accumulates per-kernel totals; sf_timing_query reads them by name
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
  * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep",
- * "prescan_rows", "linear_flat", "bmm_sparse").
+ * "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

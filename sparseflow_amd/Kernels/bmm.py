@@ -38,8 +38,11 @@ def sparse_bmm_forward(
     return_tile_stats: bool = False,
     fallback_ratio: float = FALLBACK_RATIO,
     output_dtype=None,
+    alpha: float = 1.0,
 ):
-    """Sparse BMM: C[b] = A[b] @ B[b], where A is expected sparse."""
+    """Sparse BMM: C[b] = alpha * (A[b] @ B[b]), where A is expected sparse
+    (`alpha` folds a following scale, such as attention's, into the
+    kernel's store)."""
     if a.ndim != 3 or b.ndim != 3:
         raise ValueError(f"sparse_bmm_forward expects 3-D operands, got {tuple(a.shape)} and {tuple(b.shape)}")
     B_dim, M, K = (int(v) for v in a.shape)
@@ -59,6 +62,8 @@ def sparse_bmm_forward(
 
     def _dense(reason):
         c = torch.bmm(a.float(), b.float())
+        if alpha != 1.0:
+            c = c * alpha
         if c.dtype != out_dtype:
             c = c.to(out_dtype)
         stats = {"total_tiles": B_dim * -(-M // _bmm_block_m(M)), "fallback": True, "reason": reason} \
@@ -107,7 +112,7 @@ def sparse_bmm_forward(
     if return_ms:
         se, ee = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         se.record()
-    _lib.bmm_sparse(a, b, threshold, c)
+    _lib.bmm_sparse(a, b, threshold, c, alpha)
     if return_ms:
         ee.record()
         torch.cuda.synchronize(a.device)

@@ -11,7 +11,7 @@ from typing import Any, Dict
 import torch
 import torch.nn as nn
 
-from ..Kernels.attention import sparse_attn_v_forward, sparse_qk_forward
+from ..Kernels.attention import sparse_attn_v_forward, sparse_qk_forward, sparse_spike_attention_forward
 
 
 class SparseAttention(nn.Module):
@@ -70,6 +70,15 @@ class SparseAttention(nn.Module):
         if want and len(res) > 2:
             self._last_diag["av_stats"] = res[2]
         return res[0]
+
+    def qkv(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        """av(qk(q, k), v) in one fused pass where the kernel takes the shape
+        (no seq x seq scores); [B, heads, seq, head_dim] in and out."""
+        if q.is_cuda:
+            y = sparse_spike_attention_forward(q, k, v, self.scale, self.threshold)
+            if y is not None:
+                return y
+        return self.av(self.qk(q, k), v)
 
     def _dense_qk(self, q, k):
         return torch.matmul(q.float(), k.float().transpose(-2, -1)) * self.scale

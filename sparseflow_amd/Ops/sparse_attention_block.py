@@ -3,7 +3,12 @@ sparse attention matmuls (drop-in for Ops/sparse_attention_block.py:35-315).
 
 Takes the dense block's q/k/v/proj Linear layers, their BatchNorm1d and
 neuron layers, and runs one of the reference's variants on [T, B, N, C]:
-  attention_qkav   (q @ k^T) * scale @ v          (SparseAttention qk / av)
+  attention_qkav   (q @ k^T) * scale @ v          (on the GPU one fused pass per
+                                                  frame and head computing
+                                                  q @ (k^T v) * scale, the
+                                                  same product without the
+                                                  seq x seq scores; else
+                                                  SparseAttention qk / av)
   attention_linear q @ (k^T @ v / N)              (two SparseMatmul)
   attention_qkmix  q @ (k^T v / N) + v @ (q^T k / N)
 """
@@ -15,6 +20,7 @@ from typing import Any, Dict
 import torch
 import torch.nn as nn
 
+from ..Kernels.attention import sparse_spike_attention_forward
 from .sparse_attention import SparseAttention
 from .sparse_bmm import SparseMatmul
 from .sparse_linear import SparseLinear
@@ -104,6 +110,20 @@ class SparseAttentionBlock(nn.Module):
         q = self._linear_bn_lif(x, self.q, self.q_bn, self.q_lif)
         k = self._linear_bn_lif(x, self.k, self.k_bn, self.k_lif)
         v = self._linear_bn_lif(x, self.v, self.v_bn, self.v_lif)
+        y = None
+        if self.variant == "attention_qkav" and q.is_cuda:
+            # One pass per (frame, head) over the token-major projections:
+            # no head permutes, no seq x seq scores.
+            tok = (t * b, n, self.num_heads, self.head_dim)
+            y = sparse_spike_attention_forward(q.reshape(tok), k.reshape(tok), v.reshape(tok),
+                                               self._sparse_attn.scale, self.threshold, token_major=True)
+        if y is not None:
+            self._last_sparse_ms = 0.0
+            self.diag_source = "missing"
+            y = self.attn_lif(y.reshape(t, b, n, c))
+            y2 = self.proj(y.flatten(0, 1))
+            y2 = self.proj_bn(y2.transpose(-1, -2)).transpose(-1, -2).reshape(t, b, n, c).contiguous()
+            return self.proj_lif(y2)
         heads = lambda z: z.reshape(t, b, n, self.num_heads, self.head_dim).permute(0, 1, 3, 2, 4).contiguous()  # noqa: E731
         q, k, v = heads(q), heads(k), heads(v)
         if self.variant == "attention_qkav":

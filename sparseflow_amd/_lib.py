@@ -61,7 +61,10 @@ EXPORTS = {
                                   _P]),
     "sf_bmm_supported": (c_int, [c_int32, c_int32]),
     "sf_bmm_sparse": (c_int, [_P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_float,
-                              _P, c_int32, _P]),
+                              c_float, _P, c_int32, _P]),
+    "sf_spike_attention_supported": (c_int, [c_int32, c_int32]),
+    "sf_spike_attention": (c_int, [_P, _P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, _P, c_float, c_float, _P,
+                                   _P, c_int32, _P]),
     "sf_timing_enable": (c_int, [c_int32]),
     "sf_timing_collect": (c_int, []),
     "sf_timing_query": (c_int64, [ctypes.c_char_p, ctypes.POINTER(c_double)]),
@@ -367,17 +370,38 @@ def bmm_supported(k: int, n: int) -> bool:
     return bool(lib().sf_bmm_supported(int(k), int(n)))
 
 
-def bmm_sparse(a: torch.Tensor, b: torch.Tensor, threshold: float, c: torch.Tensor) -> torch.Tensor:
-    """c [B, m, n] = a [B, m, k] (contiguous) @ b [B, k, n] (any strides,
-    same dtype as a) (sf_bmm_sparse)."""
+def bmm_sparse(a: torch.Tensor, b: torch.Tensor, threshold: float, c: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+    """c [B, m, n] = alpha * (a [B, m, k] (contiguous) @ b [B, k, n] (any
+    strides, same dtype as a)) (sf_bmm_sparse)."""
     _require_device(a, "a")
     _require_device(b, "b")
     bt, m, k = (int(v) for v in a.shape)
     n = int(b.shape[2])
     rc = lib().sf_bmm_sparse(_ptr(a), _ptr(b), dtype_code(a.dtype), bt, m, k, n, int(b.stride(0)), int(b.stride(1)),
-                             int(b.stride(2)), float(threshold), _ptr(c), dtype_code(c.dtype), _stream(a.device))
+                             int(b.stride(2)), float(threshold), float(alpha), _ptr(c), dtype_code(c.dtype),
+                             _stream(a.device))
     _check(rc, "sf_bmm_sparse")
     return c
+
+
+def spike_attention_supported(s: int, d: int) -> bool:
+    return bool(lib().sf_spike_attention_supported(int(s), int(d)))
+
+
+def spike_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, threshold: float,
+                    y: torch.Tensor) -> torch.Tensor:
+    """q, k, v, y [TB, S, H, D] views (any strides, d contiguous, q/k/v with
+    the same strides): y = (q @ k^T * scale) @ v per (tb, h) (sf_spike_attention)."""
+    _require_device(q, "q")
+    tb, s, h, d = (int(t) for t in q.shape)
+    if k.stride() != q.stride() or v.stride() != q.stride() or q.stride(3) != 1 or y.stride(3) != 1:
+        raise ValueError("q, k, v must share strides and every operand must have a contiguous last dim")
+    qs = (ctypes.c_int64 * 3)(q.stride(0), q.stride(1), q.stride(2))
+    ys = (ctypes.c_int64 * 3)(y.stride(0), y.stride(1), y.stride(2))
+    rc = lib().sf_spike_attention(_ptr(q), _ptr(k), _ptr(v), dtype_code(q.dtype), tb, s, h, d, qs, float(scale),
+                                  float(threshold), _ptr(y), ys, dtype_code(y.dtype), _stream(q.device))
+    _check(rc, "sf_spike_attention")
+    return y
 
 
 # ---------------------------------------------------------------------------
@@ -385,7 +409,7 @@ def bmm_sparse(a: torch.Tensor, b: torch.Tensor, threshold: float, c: torch.Tens
 # ---------------------------------------------------------------------------
 
 KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
-                "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse")
+                "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention")
 
 
 def timing_enable(on: bool) -> None:

@@ -12,8 +12,8 @@
 // increasing k: the element is broadcast from the lane that loaded it
 // (readlane) and every lane adds it times B's row k at its columns.  Zero
 // elements cost nothing; an all-zero row is just its store.  The row's
-// outputs leave as coalesced runs of n.  Accumulation is f32 in increasing
-// k: deterministic.
+// outputs leave as coalesced runs of n, times alpha (the attention scale).
+// Accumulation is f32 in increasing k: deterministic.
 //
 // Replaces the reference's _prescan_bmm_kernel + sparse BMM kernels
 // (Kernels/bmm.py:66-184) behind sparse_bmm_forward (Kernels/bmm.py:195).
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(64 * kBmmWaves) void k_bmm(BmmArgs a) {
       TOut* __restrict__ cr = C + (bt * M + m) * (int64_t)N + n0;
 #pragma unroll
       for (int j = 0; j < NBJ; ++j)
-        if (64 * j + lane < nbw) cr[64 * j + lane] = from_f32<TOut>(acc[j]);
+        if (64 * j + lane < nbw) cr[64 * j + lane] = from_f32<TOut>(acc[j] * a.alpha);
     }
   }
 }

@@ -194,7 +194,8 @@ double g_total_ms[sf::K_COUNT] = {};
 int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
-                                     "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse"};
+                                     "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse",
+                                     "spike_attention"};
 
 }  // namespace
 
@@ -475,8 +476,8 @@ int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k, con
 int sf_bmm_supported(int32_t k, int32_t n) { return k >= 1 && n >= 1 && sf::bmm_column_blocks(k, n) > 0; }
 
 int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batches, int32_t m, int32_t k, int32_t n,
-                  int64_t b_stride_batch, int64_t b_stride_k, int64_t b_stride_n, float threshold, void* c,
-                  int32_t out_dtype, void* stream) {
+                  int64_t b_stride_batch, int64_t b_stride_k, int64_t b_stride_n, float threshold, float alpha,
+                  void* c, int32_t out_dtype, void* stream) {
   if (batches < 0 || m < 0 || k < 1 || n < 1) return fail(SF_ERR_INVALID, "bad bmm shape");
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
   if (out_dtype != in_dtype && out_dtype != SF_F32)
@@ -497,8 +498,49 @@ int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batche
   args.b_stride_k = b_stride_k;
   args.b_stride_n = b_stride_n;
   args.cutoff = sf_activity_cutoff(threshold);
+  args.alpha = alpha;
   const int rc = sf::launch_bmm(args, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "bmm_sparse launch");
+  return SF_OK;
+}
+
+// ---- fused spike attention ----------------------------------------------------
+
+int sf_spike_attention_supported(int32_t s, int32_t d) {
+  return s >= 1 && (d == 16 || d == 32 || d == 64) && sf::attn_lds_bytes(s, d) <= (size_t)sf::kMaxLdsBytes;
+}
+
+int sf_spike_attention(const void* q, const void* k, const void* v, int32_t in_dtype, int64_t tb, int32_t s,
+                       int32_t h, int32_t d, const int64_t* qkv_strides, float scale, float threshold, void* y,
+                       const int64_t* y_strides, int32_t out_dtype, void* stream) {
+  if (tb < 0 || s < 1 || h < 1 || d < 1) return fail(SF_ERR_INVALID, "bad attention shape");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  if (!sf_spike_attention_supported(s, d))
+    return fail(SF_ERR_UNSUPPORTED, "head_dim must be 16, 32 or 64 and 2*s*d + d*(d+1) floats fit 160 KB of LDS");
+  if (qkv_strides == nullptr || y_strides == nullptr) return fail(SF_ERR_INVALID, "NULL strides");
+  if (tb == 0) return SF_OK;
+  if (q == nullptr || k == nullptr || v == nullptr || y == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  sf::AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.y = y;
+  a.tb = tb;
+  a.s = s;
+  a.h = h;
+  a.d = d;
+  a.s_tb = qkv_strides[0];
+  a.s_m = qkv_strides[1];
+  a.s_h = qkv_strides[2];
+  a.y_tb = y_strides[0];
+  a.y_m = y_strides[1];
+  a.y_h = y_strides[2];
+  a.scale = scale;
+  a.cutoff = sf_activity_cutoff(threshold);
+  const int rc = sf::launch_spike_attn(a, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "spike_attention launch");
   return SF_OK;
 }
 

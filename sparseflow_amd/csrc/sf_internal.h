@@ -136,6 +136,7 @@ struct BmmArgs {
   int64_t b_stride_batch, b_stride_k, b_stride_n;  // elements
   int ncb;                                          // column blocks (set by the launcher)
   float cutoff;
+  float alpha;                                      // output scale
 };
 constexpr int kBmmLdsBytes = 64 * 1024;  // staged B block per workgroup
 // Columns per block / 64 (4, 2 or 1) for a k x n B, or 0 when even a
@@ -143,13 +144,29 @@ constexpr int kBmmLdsBytes = 64 * 1024;  // staged B block per workgroup
 int bmm_column_blocks(int k, int n);
 int launch_bmm(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Fused spike attention core y = (q @ k^T * scale) @ v = q @ (k^T v) * scale
+// per (frame, head); element (tb, m, h, d) at tb*s_tb + m*s_m + h*s_h + d.
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* y;
+  int64_t tb;
+  int s, h, d;
+  int64_t s_tb, s_m, s_h;  // q / k / v strides (elements)
+  int64_t y_tb, y_m, y_h;  // y strides
+  float scale, cutoff;
+};
+size_t attn_lds_bytes(int s, int d);
+int launch_spike_attn(const AttnArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
 
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_COUNT = 13 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_COUNT = 14 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

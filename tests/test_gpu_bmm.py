@@ -116,3 +116,39 @@ def test_attention_stages_and_modules():
     b3 = torch.randn(40, 22, generator=torch.Generator().manual_seed(13))  # n % 4 != 0: batched path
     ok, err, _ = close(mm(a2.to(DEV), b3.to(DEV)), olin.linear_ref(a2, b3.t(), None), **FP32_TOL)
     assert ok, f"matmul (bmm path) err {err}"
+
+
+@pytest.mark.parametrize("shape", [(8, 12, 196, 32), (4, 3, 64, 64), (6, 8, 50, 16), (2, 2, 300, 32)])
+@pytest.mark.parametrize("p", [0.0, 0.1, 0.5])
+def test_fused_spike_attention(shape, p):
+    from sparseflow_amd.Kernels.attention import sparse_spike_attention_forward
+
+    B, H, S, D = shape
+    q, k, v = (spikes(shape, p, seed=s) for s in (20, 21, 22))
+    q[0, 0, 0, :4] = torch.tensor([2.0, -0.5, 3e-7, 1.0])   # values and a sub-threshold element
+    announce(f"spike attention {shape} p={p}")
+    ref = torch.matmul(torch.matmul(olin.masked(q, 1e-6).double(), k.double().transpose(-2, -1)) * D ** -0.5,
+                       v.double())
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    y = sparse_spike_attention_forward(q.to(DEV), k.to(DEV), v.to(DEV))
+    torch.cuda.synchronize()
+    stats = _lib.timing_collect()
+    _lib.timing_enable(False)
+    assert stats["spike_attention"][0] == 1
+    ok, err, _ = close(y, ref, **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    # Token-major views give the same numbers.
+    qt, kt, vt = (t.transpose(1, 2).contiguous().to(DEV) for t in (q, k, v))
+    yt = sparse_spike_attention_forward(qt, kt, vt, token_major=True)
+    assert torch.equal(yt.transpose(1, 2).cpu(), y.cpu())
+
+
+def test_fused_spike_attention_unsupported_shapes():
+    from sparseflow_amd.Kernels.attention import sparse_spike_attention_forward
+
+    q = spikes((2, 2, 20, 48), 0.1, seed=23).to(DEV)
+    assert sparse_spike_attention_forward(q, q, q) is None          # head_dim 48
+    q = spikes((1, 1, 700, 64), 0.1, seed=24).to(DEV)
+    assert sparse_spike_attention_forward(q, q, q) is None          # k, v exceed LDS
+    assert not _lib.spike_attention_supported(700, 64) and _lib.spike_attention_supported(196, 32)

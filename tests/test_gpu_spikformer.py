@@ -1,6 +1,6 @@
 """Spikformer end to end on the GPU: the optimized model (SparseConv2d in the
 patch embedding, SparseAttentionBlock with SparseLinear projections and the
-sparse batched matmul, SparseLinear MLP and head) against the same model
+fused spike-attention kernel, SparseLinear MLP and head) against the same model
 with dense torch layers.  Every neuron layer's spikes agree except at
 threshold ties (fp32 rounding of different summation orders, which can
 cascade to a few downstream neurons), and the logits agree."""
@@ -66,7 +66,7 @@ def test_spikformer_optimized_matches_dense(builder, T, B):
         for h in hooks:
             h.remove()
     launched = {k for k, (c, _) in stats.items() if c > 0}
-    assert {"linear_flat", "bmm_sparse"} <= launched, launched
+    assert {"linear_flat", "spike_attention"} <= launched, launched
     rates = {n: s.float().mean().item() for n, s in rec.items()}
     assert min(rates.values()) > 0.01, rates
     for name, s_ref in rec_d.items():
