@@ -303,7 +303,7 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
     through torch) on the same tensors."""
     from sparseflow_amd import _lib
     from sparseflow_amd.Kernels.attention import sparse_attn_v_forward, sparse_qk_forward, sparse_spike_attention_forward
-    from sparseflow_amd.Kernels.linear import sparse_linear_forward, tap_weight
+    from sparseflow_amd.Kernels.linear import sparse_linear_forward, split_weight_bf16, tap_weight
     from sparseflow_amd.Ops.sparse_conv2d import SparseConv2d
 
     hd = dim // heads
@@ -311,18 +311,30 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
     g = torch.Generator(device=dev).manual_seed(5)
     qkv = [(torch.rand(bt, heads, tokens, hd, generator=g, device=dev) < p).float() for _ in range(3)]
     x_tok = (torch.rand(bt * tokens, dim, generator=g, device=dev) < p).float()
+    h_tok = (torch.rand(bt * tokens, 4 * dim, generator=g, device=dev) < p).float()
     lin = torch.nn.Linear(dim, dim).to(dev)
+    fc1 = torch.nn.Linear(dim, 4 * dim).to(dev)
+    fc2 = torch.nn.Linear(4 * dim, dim).to(dev)
     wt = tap_weight(lin.weight)
-    ws = torch.empty(_lib.linear_workspace_size(bt * tokens, dim), dtype=torch.uint8, device=dev)
+    splits = {id(m): split_weight_bf16(m.weight) for m in (lin, fc1, fc2)}
+    ws = torch.empty(_lib.linear_workspace_size(bt * tokens, 4 * dim), dtype=torch.uint8, device=dev)
+
+    def lin_case(m, x):
+        return (lambda: sparse_linear_forward(x, m.weight, m.bias, w_split=splits[id(m)], kernel="mfma"),
+                lambda: torch.nn.functional.linear(x, m.weight, m.bias),
+                x.numel() * 4 + m.weight.numel() * 4 + x.shape[0] * m.out_features * 4)
     scale = hd ** -0.5
     ops = {}
     with torch.no_grad():
         attn = sparse_qk_forward(qkv[0], qkv[1], scale)[0]
         cases = {
-            "linear_384x384": (
-                lambda: sparse_linear_forward(x_tok, lin.weight, lin.bias, w_t=wt, workspace=ws),
+            "linear_384x384": lin_case(lin, x_tok),
+            "linear_384x384_walk": (
+                lambda: sparse_linear_forward(x_tok, lin.weight, lin.bias, w_t=wt, workspace=ws, kernel="walk"),
                 lambda: torch.nn.functional.linear(x_tok, lin.weight, lin.bias),
                 x_tok.numel() * 4 + dim * dim * 4 + bt * tokens * dim * 4),
+            "mlp_fc1_384x1536": lin_case(fc1, x_tok),
+            "mlp_fc2_1536x384": lin_case(fc2, h_tok),
             "qk": (
                 lambda: sparse_qk_forward(qkv[0], qkv[1], scale),
                 lambda: torch.matmul(qkv[0], qkv[1].transpose(-2, -1)) * scale,
@@ -361,15 +373,17 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
         torch.backends.cudnn.benchmark = False
         ops["stem_conv3x3_3to384"] = {"us": ms * 1e3, "dense_us": None if dms is None else dms * 1e3,
                                       "speedup_vs_dense": None if dms is None else dms / ms}
-    # One SSA block: q, k, v, proj projections + the attention core (fused;
-    # the dense reference runs qk then av).
-    blk = 4 * ops["linear_384x384"]["us"] + ops["attention_fused"]["us"]
+    # One Spikformer block's matmul work: q, k, v, proj projections, the
+    # attention core (fused; the dense reference runs qk then av) and the MLP.
+    mlp = ops["mlp_fc1_384x1536"]["us"] + ops["mlp_fc2_1536x384"]["us"]
+    blk = 4 * ops["linear_384x384"]["us"] + ops["attention_fused"]["us"] + mlp
     res = {"workload": ATTN_WORKLOAD, "T": T, "N": N, "tokens": tokens, "dim": dim, "heads": heads,
-           "spike_p": p, "ops": ops, "ssa_block_us": blk}
+           "spike_p": p, "ops": ops, "block_matmul_us": blk}
     if with_dense:
-        dblk = 4 * ops["linear_384x384"]["dense_us"] + ops["qk"]["dense_us"] + ops["av"]["dense_us"]
-        res["ssa_block_dense_us"] = dblk
-        res["ssa_block_speedup_vs_dense"] = dblk / blk
+        dblk = (4 * ops["linear_384x384"]["dense_us"] + ops["qk"]["dense_us"] + ops["av"]["dense_us"]
+                + ops["mlp_fc1_384x1536"]["dense_us"] + ops["mlp_fc2_1536x384"]["dense_us"])
+        res["block_matmul_dense_us"] = dblk
+        res["block_matmul_speedup_vs_dense"] = dblk / blk
     return res
 
 

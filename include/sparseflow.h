@@ -218,6 +218,20 @@ int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k,
                       float threshold, void* workspace, size_t workspace_bytes,
                       void* y, int32_t out_dtype, void* stream);
 
+/* The same product on the matrix cores, for inputs whose every 32-wide K
+ * slice is live in some row of a 128-row tile (transformer densities): W
+ * given as bf16 hi and lo parts (w_hi = bf16(W), w_lo = bf16(W - w_hi)),
+ * [c_out][kp] with kp = k rounded up to a multiple of 32 (zero padded),
+ * 16-byte aligned; y = x @ (w_hi + w_lo)^T + bias, with x split the same way
+ * in the kernel (exact for spikes and small integers; ~16 bits otherwise);
+ * elements with f16(|x|) <= f16(threshold) count as zero.  Every product is
+ * computed (dense tiles, the reference's all-groups-active case).  No
+ * prescan, no workspace.  k <= 8192. */
+int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k,
+                   const uint16_t* w_hi, const uint16_t* w_lo, int32_t kp,
+                   const float* bias, int32_t c_out, float threshold, void* y,
+                   int32_t out_dtype, void* stream);
+
 /* ---- sparse batched matmul -------------------------------------------------- */
 
 /* c[b] = alpha * (a[b] @ B[b]) for b < batches: a [batches, m, k] contiguous and
@@ -261,7 +275,8 @@ int sf_spike_attention(const void* q, const void* k, const void* v,
  * and accumulates per-kernel totals; sf_timing_query reads them by name
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
  * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep",
- * "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention").
+ * "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
+ * "linear_mfma").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

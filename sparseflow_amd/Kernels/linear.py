@@ -4,9 +4,16 @@
 (Kernels/linear.py:460-778): (y, ms) + optional (ratio,), (tile_stats,),
 (backend_meta,).  Device tensors go through the C ABI:
 
-  Stage 1  sf_linear_prescan  x [m, k] -> row bitmap (+ non-binary flags)
-  Stage 2  sf_linear_sparse   bitmap -> y [m, c_out] (lane = row walk of
-                              the active elements, weight rows from LDS)
+  "walk"  sf_linear_prescan  x [m, k] -> row bitmap (+ non-binary flags)
+          sf_linear_sparse   bitmap -> y [m, c_out] (lane = row walk of the
+                             active elements, weight rows from LDS)
+  "mfma"  sf_linear_mfma     one pass on the matrix cores with W and x split
+                             into bf16 hi + lo parts (dense tiles)
+
+The walk does ~density x the MACs on the VALU; the MFMA tile path does them
+all on the matrix cores and wins once every 32-wide K slice of a 128-row tile
+is live (transformer densities, p ~ 0.1).  `kernel="auto"` takes the MFMA
+path for k >= 32 (the walk for narrower inputs).
 
 Weights stay fp32 and the sum is fp32 (the reference casts x and W to fp16
 for tl.dot, Kernels/linear.py:572,720).  Elements with f16(|x|) <=
@@ -76,6 +83,20 @@ def tap_weight(weight: torch.Tensor) -> torch.Tensor:
     return weight.detach().to(torch.float32).t().contiguous()
 
 
+def split_weight_bf16(weight: torch.Tensor):
+    """Linear weight [c_out, k] -> (hi, lo) bf16 [c_out, kp] with
+    hi = bf16(W), lo = bf16(W - hi), kp = k rounded up to 32 (zero padded):
+    hi + lo carries ~16 bits of each fp32 weight."""
+    w = weight.detach().to(torch.float32)
+    c_out, k = w.shape
+    kp = -(-k // 32) * 32
+    hi = torch.zeros(c_out, kp, dtype=torch.bfloat16, device=w.device)
+    lo = torch.zeros(c_out, kp, dtype=torch.bfloat16, device=w.device)
+    hi[:, :k] = w.to(torch.bfloat16)
+    lo[:, :k] = (w - hi[:, :k].float()).to(torch.bfloat16)
+    return hi, lo
+
+
 def sparse_linear_forward(
     x,
     weight,
@@ -93,8 +114,13 @@ def sparse_linear_forward(
     launch_all_tiles=False,
     output_dtype=None,
     workspace=None,
+    w_split=None,
+    kernel="auto",
 ):
     """Sparse linear y = x @ weight^T + bias for x [N, C_IN].
+
+    `kernel` picks "walk", "mfma" or "auto" (see the module docstring);
+    `w_split` may carry the cached (hi, lo) of split_weight_bf16.
 
     `w_t` may carry a cached weight^T [C_IN, C_OUT] (f32 is used as is,
     other dtypes are converted).  `active_tile_ids_buf` and
@@ -145,10 +171,13 @@ def sparse_linear_forward(
 
     x = x.contiguous()
     lib_out = out_dtype if out_dtype in (x.dtype, torch.float32) else torch.float32
-    if w_t is not None and tuple(w_t.shape) == (C_IN, C_OUT):
-        wt = w_t if (w_t.dtype == torch.float32 and w_t.is_contiguous()) else w_t.detach().float().contiguous()
-    else:
-        wt = tap_weight(weight)
+    use_mfma = kernel == "mfma" or (kernel == "auto" and C_IN >= 32)
+    wt = None
+    if not use_mfma:
+        if w_t is not None and tuple(w_t.shape) == (C_IN, C_OUT):
+            wt = w_t if (w_t.dtype == torch.float32 and w_t.is_contiguous()) else w_t.detach().float().contiguous()
+        else:
+            wt = tap_weight(weight)
     b = None if bias is None else bias.detach().to(torch.float32).contiguous()
     y = torch.empty((N, C_OUT), dtype=lib_out, device=x.device)
 
@@ -164,7 +193,21 @@ def sparse_linear_forward(
     }
     ratio = stats = None
     ms = 0.0
-    if not (need_stats or return_ms):
+    if use_mfma:
+        if w_split is None or tuple(w_split[0].shape) != (C_OUT, -(-C_IN // 32) * 32):
+            w_split = split_weight_bf16(weight)
+        meta["reason"] = "linear_mfma_bf16x2"
+        meta["launch_count"] = int(-(-N // 128) * -(-C_OUT // 128))
+    if use_mfma and not need_stats:
+        if return_ms:
+            se, ee = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            se.record()
+        _lib.linear_mfma(x, w_split[0], w_split[1], b, y, threshold)
+        if return_ms:
+            ee.record()
+            torch.cuda.synchronize(x.device)
+            ms = se.elapsed_time(ee)
+    elif not (need_stats or return_ms):
         ws_bytes = _lib.linear_workspace_size(N, C_IN)
         if workspace is None or workspace.numel() * workspace.element_size() < ws_bytes:
             workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
@@ -197,7 +240,10 @@ def sparse_linear_forward(
         if return_ms:
             se, ee = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             se.record()
-        _lib.linear_sparse(bits, flags, x, wt, b, y)
+        if use_mfma:
+            _lib.linear_mfma(x, w_split[0], w_split[1], b, y, threshold)
+        else:
+            _lib.linear_sparse(bits, flags, x, wt, b, y)
         if return_ms:
             ee.record()
             torch.cuda.synchronize(x.device)

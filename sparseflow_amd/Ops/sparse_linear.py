@@ -18,7 +18,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..Kernels.linear import BACKEND_NAME, sparse_linear_forward, tap_weight
+from ..Kernels.linear import BACKEND_NAME, sparse_linear_forward, split_weight_bf16, tap_weight
 from ..Utils import config as _config
 from ..Utils.config import PRESCAN_ACTIVITY_EPS, SPARSE_DENSE_RATIO_THRESHOLD
 from .sparse_conv2d import _ProfileStats
@@ -65,6 +65,11 @@ class SparseLinear(nn.Module):
         self._last_avg_active_ratio = -1.0
         self._w_t = None
         self._w_t_key = None
+        self._w_split = None
+        self._w_split_key = None
+        # Stage-2 kernel: "auto" (matrix cores for in_features >= 32), "mfma"
+        # or "walk" (the spike walk; fewer MACs at very low densities).
+        self.kernel = "auto"
         self._workspace = None
         self._warmup_left = int(max(0, warmup_steps))
         self._calib_every = int(max(1, calib_every))
@@ -149,6 +154,13 @@ class SparseLinear(nn.Module):
             self._w_t = tap_weight(self.weight)
             self._w_t_key = key
         return self._w_t
+
+    def _get_w_split(self):
+        key = (self.weight._version, self.weight.data_ptr(), self.weight.device)
+        if self._w_split is None or self._w_split_key != key:
+            self._w_split = split_weight_bf16(self.weight)
+            self._w_split_key = key
+        return self._w_split
 
     def _flatten_input(self, x: torch.Tensor) -> Tuple[torch.Tensor, Tuple]:
         if x.dim() < 2:
@@ -241,7 +253,10 @@ class SparseLinear(nn.Module):
         if x2d.is_cuda and self._supports_sparse() and self.backend_mode != "dense" and not forced_dense:
             want_diag = self.collect_diag and not self._inference_mode
             res = sparse_linear_forward(
-                x2d, self.weight, self.bias, threshold=self.threshold, w_t=self._get_w_t(),
+                x2d, self.weight, self.bias, threshold=self.threshold,
+                w_t=self._get_w_t() if self.kernel == "walk" or self.in_features < 32 else None,
+                w_split=None if self.kernel == "walk" or self.in_features < 32 else self._get_w_split(),
+                kernel=self.kernel,
                 return_ms=self.return_ms, return_avg_active_ratio=want_diag or need_ratio,
                 return_tile_stats=want_diag, return_backend_meta=True, output_dtype=x2d.dtype,
                 workspace=self._get_workspace(x2d))

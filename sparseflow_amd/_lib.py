@@ -59,6 +59,8 @@ EXPORTS = {
     "sf_linear_sparse": (c_int, [_P, _P, _P, c_int32, c_int64, c_int32, _P, _P, c_int32, _P, c_int32, _P]),
     "sf_linear_forward": (c_int, [_P, c_int32, c_int64, c_int32, _P, _P, c_int32, c_float, _P, c_size_t, _P, c_int32,
                                   _P]),
+    "sf_linear_mfma": (c_int, [_P, c_int32, c_int64, c_int32, _P, _P, c_int32, _P, c_int32, c_float, _P, c_int32,
+                               _P]),
     "sf_bmm_supported": (c_int, [c_int32, c_int32]),
     "sf_bmm_sparse": (c_int, [_P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_float,
                               c_float, _P, c_int32, _P]),
@@ -366,6 +368,19 @@ def linear_sparse(bits: torch.Tensor, flags: torch.Tensor, x2d: torch.Tensor, wt
     return y
 
 
+def linear_mfma(x2d: torch.Tensor, w_hi: torch.Tensor, w_lo: torch.Tensor, bias: Optional[torch.Tensor],
+                y: torch.Tensor, threshold: float = 1e-6) -> torch.Tensor:
+    """y [m, c_out] = x [m, k] @ (w_hi + w_lo)^T + bias on the matrix cores
+    (sf_linear_mfma); w_hi / w_lo bf16 [c_out, kp] (kp = k rounded up to 32)."""
+    _require_device(x2d, "x")
+    m, k = (int(v) for v in x2d.shape)
+    c_out, kp = (int(v) for v in w_hi.shape)
+    rc = lib().sf_linear_mfma(_ptr(x2d), dtype_code(x2d.dtype), m, k, _ptr(w_hi), _ptr(w_lo), kp, _ptr(bias), c_out,
+                              float(threshold), _ptr(y), dtype_code(y.dtype), _stream(x2d.device))
+    _check(rc, "sf_linear_mfma")
+    return y
+
+
 def bmm_supported(k: int, n: int) -> bool:
     return bool(lib().sf_bmm_supported(int(k), int(n)))
 
@@ -409,7 +424,8 @@ def spike_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 # ---------------------------------------------------------------------------
 
 KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
-                "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention")
+                "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
+                "linear_mfma")
 
 
 def timing_enable(on: bool) -> None:

@@ -195,7 +195,7 @@ int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                                      "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse",
-                                     "spike_attention"};
+                                     "spike_attention", "linear_mfma"};
 
 }  // namespace
 
@@ -447,6 +447,36 @@ int sf_linear_sparse(const uint32_t* bits, const uint32_t* flags, const void* x,
   a.T = 1;
   const int rc = sf::launch_linear_flat(a, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "linear_flat launch");
+  return SF_OK;
+}
+
+int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k, const uint16_t* w_hi, const uint16_t* w_lo,
+                   int32_t kp, const float* bias, int32_t c_out, float threshold, void* y, int32_t out_dtype,
+                   void* stream) {
+  if (m < 0 || k < 1 || c_out < 1) return fail(SF_ERR_INVALID, "bad linear shape");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  if (kp % 32 != 0 || kp < k || kp - k >= 32) return fail(SF_ERR_INVALID, "kp must be k rounded up to a multiple of 32");
+  if (kp > sf::linear_mfma_max_kp()) return fail(SF_ERR_UNSUPPORTED, "k > 8192");
+  if (m >= (1ll << 30)) return fail(SF_ERR_UNSUPPORTED, "m >= 2^30 rows");
+  if (m == 0) return SF_OK;
+  if (x == nullptr || w_hi == nullptr || w_lo == nullptr || y == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(w_hi) | reinterpret_cast<uintptr_t>(w_lo)) & 15)
+    return fail(SF_ERR_INVALID, "w_hi / w_lo must be 16-byte aligned");
+  sf::LinMfmaArgs a{};
+  a.x = x;
+  a.wh = w_hi;
+  a.wl = w_lo;
+  a.bias = bias;
+  a.y = y;
+  a.m = m;
+  a.k = k;
+  a.kp = kp;
+  a.c_out = c_out;
+  a.cutoff = sf_activity_cutoff(threshold);
+  const int rc = sf::launch_linear_mfma(a, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "linear_mfma launch");
   return SF_OK;
 }
 

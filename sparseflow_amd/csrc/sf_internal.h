@@ -144,6 +144,21 @@ constexpr int kBmmLdsBytes = 64 * 1024;  // staged B block per workgroup
 int bmm_column_blocks(int k, int n);
 int launch_bmm(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Sparse Linear on MFMA: x [m, k] row-major, W split into bf16 hi / lo
+// [c_out][kp] (k contiguous, kp = k rounded up to 32, zero padded).
+struct LinMfmaArgs {
+  const void* x;
+  const uint16_t* wh;  // bf16 bit patterns
+  const uint16_t* wl;
+  const float* bias;
+  void* y;
+  int64_t m;
+  int k, kp, c_out;
+  float cutoff;  // elements with |x| < cutoff count as zero
+};
+int linear_mfma_max_kp();
+int launch_linear_mfma(const LinMfmaArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
 // Fused spike attention core y = (q @ k^T * scale) @ v = q @ (k^T v) * scale
 // per (frame, head); element (tb, m, h, d) at tb*s_tb + m*s_m + h*s_h + d.
 struct AttnArgs {
@@ -166,7 +181,7 @@ void conv_geometry(ConvArgs& a, bool lif);
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_COUNT = 14 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_COUNT = 15 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

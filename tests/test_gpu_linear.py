@@ -46,14 +46,18 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("density", [0.0, 0.1, 0.5])
-def test_linear_fp32_matches_dense(case, density):
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_linear_fp32_matches_dense(case, density, kernel):
     m, k, co = case
-    announce(f"linear {case} p={density}")
+    announce(f"linear {kernel} {case} p={density}")
     x = spikes((m, k), density, seed=m + k)
     w = _w(co, k, seed=co)
     b = torch.randn(co, generator=torch.Generator().manual_seed(5)) * 0.1
-    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV))
-    assert "linear_flat" in kernels and "prescan_rows" in kernels, kernels
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV), kernel=kernel)
+    if kernel == "walk":
+        assert "linear_flat" in kernels and "prescan_rows" in kernels, kernels
+    else:
+        assert set(kernels) == {"linear_mfma"}, kernels
     ok, err, _ = close(y, olin.linear_ref(x, w, b), **FP32_TOL)
     assert ok, f"max abs err {err}"
     assert native_loaded()
@@ -73,44 +77,62 @@ def test_row_bitmap_and_flags_bit_exact(m, k):
     assert np.array_equal(nb, olin.row_chunk_nonbinary(x.numpy()))
 
 
-def test_value_path_inputs():
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_value_path_inputs(kernel):
     g = torch.Generator().manual_seed(7)
     x = spikes((256, 384), 0.1, seed=8)
     x[:64] = x[:64] * 2.0                                   # sums of two spike maps
     x[100:110] = x[100:110] * torch.randn(10, 384, generator=g)
+    x[200, 5] = 3e-7                                        # below the activity threshold
     w = _w(384, 384, seed=9)
-    announce("linear value path")
-    y, _ = _run(x.to(DEV), w.to(DEV), None)
+    announce(f"linear value path {kernel}")
+    y, _ = _run(x.to(DEV), w.to(DEV), None, kernel=kernel)
     ok, err, _ = close(y, olin.linear_ref(x, w, None), **FP32_TOL)
     assert ok, f"max abs err {err}"
 
 
+def test_mfma_bf16_split_keeps_fp32_accuracy():
+    # Weights with full fp32 mantissas and large K: the hi + lo split keeps
+    # the error far inside 1e-4 (one bf16 alone would not).
+    g = torch.Generator().manual_seed(30)
+    x = spikes((1024, 1536), 0.3, seed=31)
+    w = torch.randn(384, 1536, generator=g) * 0.05
+    announce("linear mfma accuracy")
+    y, _ = _run(x.to(DEV), w.to(DEV), None, kernel="mfma")
+    ref = olin.linear_ref(x, w, None)
+    ok, err, _ = close(y, ref, **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    assert err < 2e-5
+
+
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_linear_half(dtype):
+def test_linear_half(dtype, kernel):
     x = spikes((512, 384), 0.1, seed=10)
     x[5] = x[5] * 0.5
     w = _w(384, 384, seed=11)
     b = torch.linspace(-0.5, 0.5, 384)
     announce(f"linear {dtype}")
-    y, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV))
+    y, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), kernel=kernel)
     assert y.dtype == dtype
     ok, err, _ = close(y, olin.linear_ref(x.to(dtype).float(), w, b), atol=1e-2, rtol=1e-2)
     assert ok, f"max abs err {err}"
-    y32, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), output_dtype=torch.float32)
+    y32, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), output_dtype=torch.float32, kernel=kernel)
     assert y32.dtype == torch.float32
     ok, err, _ = close(y32, olin.linear_ref(x.to(dtype).float(), w, b), **FP32_TOL)
     assert ok, f"max abs err {err}"
 
 
-def test_linear_deterministic_and_stats_path():
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_linear_deterministic_and_stats_path(kernel):
     x = spikes((2048, 384), 0.05, seed=12).to(DEV)
     w = _w(384, 384, seed=13).to(DEV)
-    announce("linear determinism + stats")
-    y1, _ = _run(x, w, None)
-    y2, _ = _run(x, w, None)
+    announce(f"linear determinism + stats {kernel}")
+    y1, _ = _run(x, w, None, kernel=kernel)
+    y2, _ = _run(x, w, None, kernel=kernel)
     assert torch.equal(y1, y2)
     res = sparse_linear_forward(x, w, None, return_ms=True, return_avg_active_ratio=True, return_tile_stats=True,
-                                return_backend_meta=True)
+                                return_backend_meta=True, kernel=kernel)
     assert torch.equal(res[0], y1)
     assert 0.0 < res[2] <= 1.0 and res[3]["total_tiles"] == 16 and res[4]["backend"] == "sparse_hip"
 
