@@ -120,3 +120,36 @@ def test_zero_frames_is_a_noop():
     empty = _lib.conv_desc(0, 8, 8, 8, 8, 8, 8, 3, 1, 1, 0, 0)
     assert _status(L.sf_conv2d_sparse, ctypes.byref(empty), None, None, None, None, None, None, None) == _lib.SF_OK
     assert _status(L.sf_prescan_pack, None, 0, 0, 8, 8, 8, 1e-6, None, None, None) == _lib.SF_OK
+
+
+def test_linear_bmm_attention_sizes_and_validation():
+    L = _lib.lib()
+    # Row bitmap: ceil(k/32) words, rounded up to a multiple of 4 beyond two.
+    assert L.sf_linear_bitmap_bytes(10, 20) == 10 * 1 * 4
+    assert L.sf_linear_bitmap_bytes(10, 64) == 10 * 2 * 4
+    assert L.sf_linear_bitmap_bytes(10, 65) == 10 * 4 * 4
+    assert L.sf_linear_bitmap_bytes(10, 384) == 10 * 12 * 4
+    assert L.sf_linear_flags_bytes(33) == 3 * 4
+    assert L.sf_linear_workspace_size(0, 10) == 0
+    assert L.sf_linear_workspace_size(10, 384) == 512 + 256
+    p = ctypes.c_void_p(1)  # never dereferenced: every call below fails validation or has no work
+    # c_out not a multiple of 4 -> unsupported; m = 0 -> nothing to do.
+    assert L.sf_linear_sparse(p, p, p, 0, 8, 32, p, None, 6, p, 0, None) == _lib.SF_ERR_UNSUPPORTED
+    assert L.sf_linear_sparse(p, p, p, 0, 0, 32, p, None, 8, p, 0, None) == _lib.SF_OK
+    assert L.sf_linear_forward(p, 0, 8, 32, p, None, 8, 1e-6, p, 1, p, 0, None) == _lib.SF_ERR_WORKSPACE
+    # MFMA linear: kp must be k rounded up to 32; k <= 8192.
+    assert L.sf_linear_mfma(p, 0, 8, 40, p, p, 40, None, 8, 1e-6, p, 0, None) == _lib.SF_ERR_INVALID
+    assert L.sf_linear_mfma(p, 0, 8, 9000, p, p, 9024, None, 8, 1e-6, p, 0, None) == _lib.SF_ERR_UNSUPPORTED
+    assert L.sf_linear_mfma(p, 0, 0, 40, p, p, 64, None, 8, 1e-6, p, 0, None) == _lib.SF_OK
+    # Batched matmul: B's 64-column block of k rows must fit 64 KB of LDS.
+    assert L.sf_bmm_supported(252, 10) and not L.sf_bmm_supported(253, 10)
+    assert L.sf_bmm_sparse(p, p, 0, 2, 4, 300, 8, 0, 1, 300, 1e-6, 1.0, p, 0, None) == _lib.SF_ERR_UNSUPPORTED
+    assert L.sf_bmm_sparse(p, p, 0, 0, 4, 30, 8, 0, 8, 1, 1e-6, 1.0, p, 0, None) == _lib.SF_OK
+    assert L.sf_bmm_sparse(p, p, 0, 2, 4, 30, 8, 0, -1, 1, 1e-6, 1.0, p, 0, None) == _lib.SF_ERR_INVALID
+    # Fused attention: head_dim 16/32/64 and k, v within LDS.
+    assert L.sf_spike_attention_supported(196, 32) and not L.sf_spike_attention_supported(196, 48)
+    assert not L.sf_spike_attention_supported(700, 64)
+    st = (ctypes.c_int64 * 3)(0, 0, 0)
+    assert L.sf_spike_attention(p, p, p, 0, 2, 196, 12, 48, st, 0.2, 1e-6, p, st, 0, None) == _lib.SF_ERR_UNSUPPORTED
+    assert L.sf_spike_attention(p, p, p, 0, 0, 196, 12, 32, st, 0.2, 1e-6, p, st, 0, None) == _lib.SF_OK
+    assert L.sf_spike_attention(p, p, p, 0, 2, 196, 12, 32, None, 0.2, 1e-6, p, st, 0, None) == _lib.SF_ERR_INVALID
