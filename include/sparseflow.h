@@ -244,6 +244,17 @@ int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k,
  * sparse_bmm_forward (Kernels/bmm.py:195-361) used by its sparse attention
  * (Kernels/attention.py:27-121, Ops/sparse_bmm.py:22-131). */
 int sf_bmm_supported(int32_t k, int32_t n);
+/* The same product on the matrix cores, for the attention shapes (rows of a
+ * dense enough that every 32-wide K slice of a 16-row tile is live): B and
+ * each 16-row tile of a split into bf16 hi + lo parts (~16 bits of both
+ * operands), all products computed.  Same arguments and bar as
+ * sf_bmm_sparse; supported while sf_bmm_mfma_supported(k, n) (k <= 256 and
+ * roundup(n, 16) * roundup(k, 32) <= 16384). */
+int sf_bmm_mfma_supported(int32_t k, int32_t n);
+int sf_bmm_mfma(const void* a, const void* b, int32_t in_dtype, int64_t batches,
+                int32_t m, int32_t k, int32_t n, int64_t b_stride_batch,
+                int64_t b_stride_k, int64_t b_stride_n, float threshold,
+                float alpha, void* c, int32_t out_dtype, void* stream);
 int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batches,
                   int32_t m, int32_t k, int32_t n, int64_t b_stride_batch,
                   int64_t b_stride_k, int64_t b_stride_n, float threshold,
@@ -276,7 +287,7 @@ int sf_spike_attention(const void* q, const void* k, const void* v,
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
  * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep",
  * "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
- * "linear_mfma").
+ * "linear_mfma", "bmm_mfma").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

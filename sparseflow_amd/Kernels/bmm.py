@@ -2,12 +2,16 @@
 
 `sparse_bmm_forward(a, b, ...)` keeps the reference's signature and return
 tuple (Kernels/bmm.py:195-361): C[b] = A[b] @ B[b] with A [B, M, K]
-spike-sparse.  Device tensors run sf_bmm_sparse: B (any strides, so K^T
-views need no copy) is staged in LDS per batch and each wavefront walks the
-active elements of A's rows; f32 accumulation (the reference casts both
-operands to fp16 for tl.dot, Kernels/bmm.py:162-172,305-306).  Shapes the
-kernel does not take (K > 252) run torch.bmm, as the reference's own
-fallbacks do (Kernels/bmm.py:221-270).
+spike-sparse.  Device tensors run one of two kernels, B read through
+strides (K^T views need no copy) and staged in LDS per batch:
+  sf_bmm_mfma    16-row tiles of A on the matrix cores, both operands split
+                 into bf16 hi + lo parts (attention densities: q at p ~ 0.1,
+                 the seq x seq scores), chosen when it takes the shape;
+  sf_bmm_sparse  each wavefront walks the active elements of A's rows in
+                 f32 (very sparse A, or K up to 252).
+(The reference casts both operands to fp16 for tl.dot, Kernels/bmm.py:
+162-172,305-306.)  Shapes neither kernel takes run torch.bmm, as the
+reference's own fallbacks do (Kernels/bmm.py:221-270).
 """
 
 from __future__ import annotations
@@ -39,10 +43,13 @@ def sparse_bmm_forward(
     fallback_ratio: float = FALLBACK_RATIO,
     output_dtype=None,
     alpha: float = 1.0,
+    kernel: str = "auto",
 ):
     """Sparse BMM: C[b] = alpha * (A[b] @ B[b]), where A is expected sparse
     (`alpha` folds a following scale, such as attention's, into the
-    kernel's store)."""
+    kernel's store).  `kernel`: "walk" (spike walk over A's active
+    elements), "mfma" (matrix-core tiles, for attention densities) or
+    "auto" (mfma where it takes the shape, else walk)."""
     if a.ndim != 3 or b.ndim != 3:
         raise ValueError(f"sparse_bmm_forward expects 3-D operands, got {tuple(a.shape)} and {tuple(b.shape)}")
     B_dim, M, K = (int(v) for v in a.shape)
@@ -76,7 +83,10 @@ def sparse_bmm_forward(
         return _dense("unsupported_dtype")
     if B_dim == 0 or M == 0 or N == 0 or K == 0:
         return _dense("empty_shape")
-    if not _lib.bmm_supported(K, N):
+    use_mfma = kernel == "mfma" or (kernel == "auto" and _lib.bmm_mfma_supported(K, N))
+    if use_mfma and not _lib.bmm_mfma_supported(K, N):
+        use_mfma = False
+    if not use_mfma and not _lib.bmm_supported(K, N):
         return _dense(f"k_too_large_for_lds(k={K})")
 
     a = a.contiguous()
@@ -112,7 +122,7 @@ def sparse_bmm_forward(
     if return_ms:
         se, ee = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         se.record()
-    _lib.bmm_sparse(a, b, threshold, c, alpha)
+    _lib.bmm_sparse(a, b, threshold, c, alpha, mfma=use_mfma)
     if return_ms:
         ee.record()
         torch.cuda.synchronize(a.device)

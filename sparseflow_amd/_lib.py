@@ -64,6 +64,9 @@ EXPORTS = {
     "sf_bmm_supported": (c_int, [c_int32, c_int32]),
     "sf_bmm_sparse": (c_int, [_P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_float,
                               c_float, _P, c_int32, _P]),
+    "sf_bmm_mfma_supported": (c_int, [c_int32, c_int32]),
+    "sf_bmm_mfma": (c_int, [_P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_float,
+                            c_float, _P, c_int32, _P]),
     "sf_spike_attention_supported": (c_int, [c_int32, c_int32]),
     "sf_spike_attention": (c_int, [_P, _P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, _P, c_float, c_float, _P,
                                    _P, c_int32, _P]),
@@ -385,17 +388,23 @@ def bmm_supported(k: int, n: int) -> bool:
     return bool(lib().sf_bmm_supported(int(k), int(n)))
 
 
-def bmm_sparse(a: torch.Tensor, b: torch.Tensor, threshold: float, c: torch.Tensor, alpha: float = 1.0) -> torch.Tensor:
+def bmm_mfma_supported(k: int, n: int) -> bool:
+    return bool(lib().sf_bmm_mfma_supported(int(k), int(n)))
+
+
+def bmm_sparse(a: torch.Tensor, b: torch.Tensor, threshold: float, c: torch.Tensor, alpha: float = 1.0,
+               mfma: bool = False) -> torch.Tensor:
     """c [B, m, n] = alpha * (a [B, m, k] (contiguous) @ b [B, k, n] (any
-    strides, same dtype as a)) (sf_bmm_sparse)."""
+    strides, same dtype as a)) (sf_bmm_sparse, or sf_bmm_mfma)."""
     _require_device(a, "a")
     _require_device(b, "b")
     bt, m, k = (int(v) for v in a.shape)
     n = int(b.shape[2])
-    rc = lib().sf_bmm_sparse(_ptr(a), _ptr(b), dtype_code(a.dtype), bt, m, k, n, int(b.stride(0)), int(b.stride(1)),
+    fn = lib().sf_bmm_mfma if mfma else lib().sf_bmm_sparse
+    rc = fn(_ptr(a), _ptr(b), dtype_code(a.dtype), bt, m, k, n, int(b.stride(0)), int(b.stride(1)),
                              int(b.stride(2)), float(threshold), float(alpha), _ptr(c), dtype_code(c.dtype),
                              _stream(a.device))
-    _check(rc, "sf_bmm_sparse")
+    _check(rc, "sf_bmm_mfma" if mfma else "sf_bmm_sparse")
     return c
 
 
@@ -425,7 +434,7 @@ def spike_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 
 KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                 "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
-                "linear_mfma")
+                "linear_mfma", "bmm_mfma")
 
 
 def timing_enable(on: bool) -> None:

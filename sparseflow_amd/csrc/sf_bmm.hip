@@ -139,3 +139,180 @@ int launch_bmm(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream
 }
 
 }  // namespace sf
+
+// ---------------------------------------------------------------------------
+// Batched matmul on the matrix cores, for the attention shapes (A's rows
+// dense enough that every 32-wide K slice of a 16-row tile is live: q at
+// p ~ 0.1 with head_dim 32, the seq x seq scores).  One workgroup per batch:
+// B (k <= 256, n <= 256) is converted to bf16 hi + lo parts into LDS,
+// [n][kp] with k contiguous and an XOR piece swizzle; each wavefront takes
+// 16-row tiles of A, loads the tile's whole K range from HBM once, splits it
+// into bf16 hi + lo in registers, and computes every 16-column tile of C
+// with 16x16x32 MFMAs (ah.bh + ah.bl + al.bh: ~16 bits of both operands).
+// A elements below the activity cutoff count as zero.
+// ---------------------------------------------------------------------------
+
+namespace sf {
+
+namespace {
+
+typedef __bf16 bmm_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float bmm_f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBmKsMax = 8;  // kp <= 256
+
+__device__ __forceinline__ uint16_t bm_bf16_bits(float f) {
+  const __hip_bfloat16 h = __float2bfloat16(f);
+  uint16_t u;
+  __builtin_memcpy(&u, &h, 2);
+  return u;
+}
+
+// Position (bf16 elements) of element k of row r in a [rows][kp] tile whose
+// 16-byte pieces are XOR-swizzled within each 64-byte group by (r >> 2) & 3.
+__device__ __forceinline__ int bm_pos(int r, int k, int kp) {
+  const int piece = k >> 3;
+  const int sw = (piece & ~3) | ((piece & 3) ^ ((r >> 2) & 3));
+  return r * kp + sw * 8 + (k & 7);
+}
+
+template <typename T, typename TOut, int KS>
+__global__ __launch_bounds__(256) void k_bmm_mfma(BmmArgs a) {
+  extern __shared__ __align__(16) uint16_t s_b[];  // hi [npad][kp], then lo
+  const int kp = KS * 32;
+  const int npad = (a.n + 15) & ~15;
+  uint16_t* s_bh = s_b;
+  uint16_t* s_bl = s_b + npad * kp;
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  const int g = lane >> 4, li = lane & 15;
+  const T* __restrict__ A = static_cast<const T*>(a.a);
+  const T* __restrict__ B = static_cast<const T*>(a.b);
+  TOut* __restrict__ C = static_cast<TOut*>(a.c);
+  const int M = a.m, K = a.k, N = a.n;
+  const int mtiles = (M + 15) / 16, ntiles = npad / 16;
+  // f32 rows of A 16-byte aligned: rows start at multiples of K floats.
+  const bool vec = sizeof(T) == 4 && (K & 3) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
+  for (int64_t bt = blockIdx.x; bt < a.batches; bt += gridDim.x) {
+    __syncthreads();  // the previous batch is done with s_b
+    const T* __restrict__ Bb = B + bt * a.b_stride_batch;
+    // Stage B: consecutive threads walk B's contiguous axis.
+    const bool kfast = a.b_stride_k == 1 && a.b_stride_n != 1;
+    for (int i = tid; i < npad * kp; i += 256) {
+      int kk, nn;
+      if (kfast) { nn = i / kp; kk = i - nn * kp; } else { kk = i / npad; nn = i - kk * npad; }
+      const float v = (kk < K && nn < N) ? to_f32<T>(Bb[(int64_t)kk * a.b_stride_k + (int64_t)nn * a.b_stride_n]) : 0.f;
+      const uint16_t h = bm_bf16_bits(v);
+      const uint16_t l = bm_bf16_bits(v - __uint_as_float((uint32_t)h << 16));
+      const int pos = bm_pos(nn, kk, kp);
+      s_bh[pos] = h;
+      s_bl[pos] = l;
+    }
+    __syncthreads();
+    const T* __restrict__ Ab = A + bt * (int64_t)M * K;
+    TOut* __restrict__ Cb = C + bt * (int64_t)M * N;
+    for (int mt = wave; mt < mtiles; mt += 4) {
+      const int row = mt * 16 + li;
+      const bool row_ok = row < M;
+      const T* __restrict__ ar = Ab + (int64_t)(row_ok ? row : 0) * K;
+      // The tile's whole K range: lane (li, g) holds k = 32 ks + 8 g .. +7.
+      float av[KS][8];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int kk0 = ks * 32 + 8 * g;
+        if (vec && kk0 + 8 <= K) {  // two 16-byte loads
+          const float4 t0 = *reinterpret_cast<const float4*>(ar + kk0);
+          const float4 t1 = *reinterpret_cast<const float4*>(ar + kk0 + 4);
+          av[ks][0] = t0.x; av[ks][1] = t0.y; av[ks][2] = t0.z; av[ks][3] = t0.w;
+          av[ks][4] = t1.x; av[ks][5] = t1.y; av[ks][6] = t1.z; av[ks][7] = t1.w;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) av[ks][j] = to_f32<T>(ar[kk0 + j < K ? kk0 + j : 0]);
+        }
+      }
+      bmm_bf16x8 ah[KS], al[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int kk = ks * 32 + 8 * g + j;
+          const float v = (row_ok && kk < K && fabsf(av[ks][j]) >= a.cutoff) ? av[ks][j] : 0.f;
+          const uint16_t h = bm_bf16_bits(v);
+          const uint16_t l = bm_bf16_bits(v - __uint_as_float((uint32_t)h << 16));
+          __bf16 hb, lb;
+          __builtin_memcpy(&hb, &h, 2);
+          __builtin_memcpy(&lb, &l, 2);
+          ah[ks][j] = hb;
+          al[ks][j] = lb;
+        }
+      for (int nt = 0; nt < ntiles; ++nt) {
+        bmm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const int col = nt * 16 + li;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int pos = bm_pos(col, ks * 32 + 8 * g, kp);
+          const bmm_bf16x8 bh = *reinterpret_cast<const bmm_bf16x8*>(&s_bh[pos]);
+          const bmm_bf16x8 bl = *reinterpret_cast<const bmm_bf16x8*>(&s_bl[pos]);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[ks], bh, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[ks], bl, acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[ks], bh, acc, 0, 0, 0);
+        }
+        // acc element i: row 16 mt + 4 g + i, column nt * 16 + li.
+        if (col < N) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = mt * 16 + 4 * g + i;
+            if (r < M) Cb[(int64_t)r * N + col] = from_f32<TOut>(acc[i] * a.alpha);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <typename T, typename TOut, int KS>
+int launch_bmm_mfma_t(const BmmArgs& a, hipStream_t stream) {
+  const size_t lds = (size_t)2 * ((a.n + 15) & ~15) * (KS * 32) * sizeof(uint16_t);
+  const int64_t cap = (int64_t)num_cus() * 8;
+  const int grid = (int)(a.batches < cap ? a.batches : cap);
+  if (grid == 0) return (int)hipSuccess;
+  hipLaunchKernelGGL((k_bmm_mfma<T, TOut, KS>), dim3(grid), dim3(256), lds, stream, a);
+  return (int)hipGetLastError();
+}
+
+template <typename T, typename TOut>
+int launch_bmm_mfma_o(const BmmArgs& a, hipStream_t stream) {
+  switch ((a.k + 31) / 32) {
+    case 1: return launch_bmm_mfma_t<T, TOut, 1>(a, stream);
+    case 2: return launch_bmm_mfma_t<T, TOut, 2>(a, stream);
+    case 3: return launch_bmm_mfma_t<T, TOut, 3>(a, stream);
+    case 4: return launch_bmm_mfma_t<T, TOut, 4>(a, stream);
+    case 5: return launch_bmm_mfma_t<T, TOut, 5>(a, stream);
+    case 6: return launch_bmm_mfma_t<T, TOut, 6>(a, stream);
+    case 7: return launch_bmm_mfma_t<T, TOut, 7>(a, stream);
+    default: return launch_bmm_mfma_t<T, TOut, 8>(a, stream);
+  }
+}
+
+template <typename T>
+int launch_bmm_mfma_d(const BmmArgs& a, int out_dtype, hipStream_t stream) {
+  if (out_dtype == SF_F32) return launch_bmm_mfma_o<T, float>(a, stream);
+  return launch_bmm_mfma_o<T, T>(a, stream);
+}
+
+}  // namespace
+
+bool bmm_mfma_supported(int k, int n) {
+  const int kp = (k + 31) / 32 * 32, npad = (n + 15) & ~15;
+  return k >= 1 && n >= 1 && kp <= 32 * kBmKsMax && (int64_t)npad * kp * 2 * 2 <= kBmmLdsBytes;
+}
+
+int launch_bmm_mfma(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  timing_begin(K_BMM_MFMA, stream);
+  const int rc = in_dtype == SF_F16    ? launch_bmm_mfma_d<__half>(a, out_dtype, stream)
+                 : in_dtype == SF_BF16 ? launch_bmm_mfma_d<__hip_bfloat16>(a, out_dtype, stream)
+                                       : launch_bmm_mfma_d<float>(a, out_dtype, stream);
+  timing_end(K_BMM_MFMA, stream);
+  return rc;
+}
+
+}  // namespace sf

@@ -195,7 +195,7 @@ int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                                      "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse",
-                                     "spike_attention", "linear_mfma"};
+                                     "spike_attention", "linear_mfma", "bmm_mfma"};
 
 }  // namespace
 
@@ -505,14 +505,20 @@ int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k, con
 
 int sf_bmm_supported(int32_t k, int32_t n) { return k >= 1 && n >= 1 && sf::bmm_column_blocks(k, n) > 0; }
 
-int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batches, int32_t m, int32_t k, int32_t n,
-                  int64_t b_stride_batch, int64_t b_stride_k, int64_t b_stride_n, float threshold, float alpha,
-                  void* c, int32_t out_dtype, void* stream) {
+int sf_bmm_mfma_supported(int32_t k, int32_t n) { return sf::bmm_mfma_supported(k, n) ? 1 : 0; }
+
+namespace {
+
+int bmm_common(const void* a, const void* b, int32_t in_dtype, int64_t batches, int32_t m, int32_t k, int32_t n,
+               int64_t b_stride_batch, int64_t b_stride_k, int64_t b_stride_n, float threshold, float alpha, void* c,
+               int32_t out_dtype, void* stream, bool mfma) {
   if (batches < 0 || m < 0 || k < 1 || n < 1) return fail(SF_ERR_INVALID, "bad bmm shape");
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
   if (out_dtype != in_dtype && out_dtype != SF_F32)
     return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
-  if (sf::bmm_column_blocks(k, n) == 0) return fail(SF_ERR_UNSUPPORTED, "k > 252: a 64-column block of B exceeds the 64 KB LDS budget");
+  if (mfma ? !sf::bmm_mfma_supported(k, n) : sf::bmm_column_blocks(k, n) == 0)
+    return fail(SF_ERR_UNSUPPORTED, mfma ? "k > 256 or B's bf16 copy exceeds the 64 KB LDS budget"
+                                         : "k > 252: a 64-column block of B exceeds the 64 KB LDS budget");
   if (b_stride_k < 0 || b_stride_n < 0 || b_stride_batch < 0) return fail(SF_ERR_INVALID, "negative stride");
   if (batches == 0 || m == 0) return SF_OK;
   if (a == nullptr || b == nullptr || c == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
@@ -529,9 +535,26 @@ int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batche
   args.b_stride_n = b_stride_n;
   args.cutoff = sf_activity_cutoff(threshold);
   args.alpha = alpha;
-  const int rc = sf::launch_bmm(args, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
-  if (rc != hipSuccess) return hip_fail(rc, "bmm_sparse launch");
+  const int rc = mfma ? sf::launch_bmm_mfma(args, in_dtype, out_dtype, static_cast<hipStream_t>(stream))
+                      : sf::launch_bmm(args, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, mfma ? "bmm_mfma launch" : "bmm_sparse launch");
   return SF_OK;
+}
+
+}  // namespace
+
+int sf_bmm_mfma(const void* a, const void* b, int32_t in_dtype, int64_t batches, int32_t m, int32_t k, int32_t n,
+                int64_t b_stride_batch, int64_t b_stride_k, int64_t b_stride_n, float threshold, float alpha, void* c,
+                int32_t out_dtype, void* stream) {
+  return bmm_common(a, b, in_dtype, batches, m, k, n, b_stride_batch, b_stride_k, b_stride_n, threshold, alpha, c,
+                    out_dtype, stream, true);
+}
+
+int sf_bmm_sparse(const void* a, const void* b, int32_t in_dtype, int64_t batches, int32_t m, int32_t k, int32_t n,
+                  int64_t b_stride_batch, int64_t b_stride_k, int64_t b_stride_n, float threshold, float alpha,
+                  void* c, int32_t out_dtype, void* stream) {
+  return bmm_common(a, b, in_dtype, batches, m, k, n, b_stride_batch, b_stride_k, b_stride_n, threshold, alpha, c,
+                    out_dtype, stream, false);
 }
 
 // ---- fused spike attention ----------------------------------------------------

@@ -143,6 +143,11 @@ constexpr int kBmmLdsBytes = 64 * 1024;  // staged B block per workgroup
 // 64-column block of k rows exceeds the LDS budget.
 int bmm_column_blocks(int k, int n);
 int launch_bmm(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+// The same product on the matrix cores (A's rows dense enough that every
+// 32-wide K slice of a 16-row tile is live): k <= 256 and B's bf16 hi + lo
+// copy within the LDS budget.
+bool bmm_mfma_supported(int k, int n);
+int launch_bmm_mfma(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
 // Sparse Linear on MFMA: x [m, k] row-major, W split into bf16 hi / lo
 // [c_out][kp] (k contiguous, kp = k rounded up to 32, zero padded).
@@ -181,7 +186,7 @@ void conv_geometry(ConvArgs& a, bool lif);
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_COUNT = 15 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_COUNT = 16 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

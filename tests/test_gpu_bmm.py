@@ -39,41 +39,55 @@ CASES = [  # (batches, m, k, n)
 ]
 
 
+def _expected_kernel(kernel, k, n):
+    mfma = kernel != "walk" and _lib.bmm_mfma_supported(k, n)
+    return "bmm_mfma" if mfma else "bmm_sparse"
+
+
 @pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("density", [0.0, 0.1, 0.6])
-def test_bmm_fp32_matches_dense(case, density):
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_bmm_fp32_matches_dense(case, density, kernel):
     bt, m, k, n = case
-    announce(f"bmm {case} p={density}")
+    announce(f"bmm {kernel} {case} p={density}")
     a = spikes((bt, m, k), density, seed=m + k)
     b = torch.randn(bt, k, n, generator=torch.Generator().manual_seed(n))
-    c, kernels = _run(a.to(DEV), b.to(DEV))
-    assert "bmm_sparse" in kernels, kernels
+    c, kernels = _run(a.to(DEV), b.to(DEV), kernel=kernel)
+    assert set(kernels) == {_expected_kernel(kernel, k, n)}, kernels
     ok, err, _ = close(c, olin.bmm_ref(a, b), **FP32_TOL)
     assert ok, f"max abs err {err}"
     assert native_loaded()
 
 
-def test_bmm_strided_b_equals_contiguous():
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_bmm_strided_b_equals_contiguous(kernel):
     a = spikes((24, 196, 32), 0.1, seed=1).to(DEV)
     k = spikes((24, 196, 32), 0.1, seed=2).to(DEV)
-    announce("bmm strided K^T")
-    c1, _ = _run(a, k.transpose(1, 2))
-    c2, _ = _run(a, k.transpose(1, 2).contiguous())
+    announce(f"bmm strided K^T {kernel}")
+    c1, _ = _run(a, k.transpose(1, 2), kernel=kernel)
+    c2, _ = _run(a, k.transpose(1, 2).contiguous(), kernel=kernel)
     assert torch.equal(c1, c2)
     ok, err, _ = close(c1, olin.bmm_ref(a.cpu(), k.cpu().transpose(1, 2)), **FP32_TOL)
     assert ok, f"max abs err {err}"
 
 
-def test_bmm_value_a_and_half():
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_bmm_value_a_and_half(kernel):
     g = torch.Generator().manual_seed(3)
     a = spikes((12, 196, 196), 0.3, seed=4) * torch.randint(1, 5, (12, 196, 196), generator=g).float() * 0.17
     b = spikes((12, 196, 32), 0.1, seed=5)
-    announce("bmm attn @ v")
-    c, _ = _run(a.to(DEV), b.to(DEV))
+    announce(f"bmm attn @ v {kernel}")
+    c, kernels = _run(a.to(DEV), b.to(DEV), kernel=kernel)
+    assert set(kernels) == {_expected_kernel(kernel, 196, 32)}
     ok, err, _ = close(c, olin.bmm_ref(a, b), **FP32_TOL)
     assert ok, f"max abs err {err}"
+    # Full fp32 mantissas in both operands: the hi + lo split keeps ~16 bits.
+    b2 = torch.randn(12, 196, 32, generator=g)
+    c2, _ = _run(a.to(DEV), b2.to(DEV), kernel=kernel)
+    ok, err, _ = close(c2, olin.bmm_ref(a, b2), **FP32_TOL)
+    assert ok, f"max abs err {err}"
     for dt in (torch.float16, torch.bfloat16):
-        c, _ = _run(a.to(DEV, dt), b.to(DEV, dt))
+        c, _ = _run(a.to(DEV, dt), b.to(DEV, dt), kernel=kernel)
         assert c.dtype == dt
         ok, err, _ = close(c, olin.bmm_ref(a.to(dt).float(), b.to(dt).float()), atol=1e-2, rtol=1e-2)
         assert ok, f"{dt}: max abs err {err}"
@@ -83,7 +97,7 @@ def test_bmm_large_k_falls_back():
     a = spikes((2, 8, 300), 0.1, seed=6)
     b = torch.randn(2, 300, 16, generator=torch.Generator().manual_seed(7))
     c, kernels = _run(a.to(DEV), b.to(DEV), return_tile_stats=True)
-    assert "bmm_sparse" not in kernels
+    assert not kernels
     ok, err, _ = close(c, olin.bmm_ref(a, b), **FP32_TOL)
     assert ok
 
