@@ -164,6 +164,27 @@ int sf_conv_lif_forward(const sf_conv_desc* desc, int32_t T, const void* x,
                         const float* v_init, void* spikes, float* v_out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Fused 1x1 stride-1 conv + multi-step LIF on a prescanned (or handed) spike
+ * map of the input: x [T, N, c_in, h, w] (desc->n = N) with its bitmap and
+ * flags over the T*N frames; x2 (optional, [T, N, c_out, h, w], in_dtype) is
+ * added into every step's current (a residual: LIF(conv(x) + x2)); spikes
+ * [T, N, c_out, h, w] in desc->out_dtype, v_out [N, c_out, h, w] f32 after
+ * step T, v_init as sf_conv_lif_forward.  out_bits / out_flags (both or
+ * neither) receive the spikes' spike map in the layout sf_prescan_pack
+ * produces for the T*N output frames (flags all zero), for the next sparse
+ * convolution.  c_out % 4 == 0.  The membrane is carried in the
+ * accumulators across the T steps (the update of sf_conv_lif_forward, equal
+ * to an unfused conv + LIF up to rounding).  Extends the reference's fused
+ * conv-LIF (Kernels/fused_conv_lif.py:310-484, 3x3 only there) to the 1x1
+ * convolutions of its bottleneck models, with the residual add and the
+ * spike map, which have no counterpart in the reference. */
+int sf_conv1x1_lif_sparse(const sf_conv_desc* desc, int32_t T,
+                          const uint32_t* bits, const uint32_t* flags,
+                          const void* x, const float* wt, const float* bias,
+                          const void* x2, const sf_lif_params* lif,
+                          const float* v_init, void* spikes, float* v_out,
+                          uint32_t* out_bits, uint32_t* out_flags, void* stream);
+
 /* ---- spiking neuron -------------------------------------------------------- */
 
 /* Multi-step LIF over T steps of n x c x hw neurons: x [T, n, c, hw] input
@@ -287,7 +308,7 @@ int sf_spike_attention(const void* q, const void* k, const void* v,
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
  * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep",
  * "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
- * "linear_mfma", "bmm_mfma").
+ * "linear_mfma", "bmm_mfma", "conv_lif_flat").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

@@ -167,3 +167,70 @@ def sparse_fused_conv_lif_forward(
     if return_avg_active_ratio:
         return spike, v_next, ms, (1.0 if ratio is None else ratio)
     return spike, v_next, ms
+
+
+def sparse_conv1x1_lif_multistep(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: Optional[torch.Tensor],
+    tau: float = 2.0,
+    v_threshold: float = 1.0,
+    v_reset: Optional[float] = 0.0,
+    decay_input: bool = True,
+    residual: Optional[torch.Tensor] = None,
+    threshold: float = PRESCAN_ACTIVITY_EPS,
+    v_init: Optional[torch.Tensor] = None,
+    w_tap: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+    emit_spike_map: bool = True,
+):
+    """Fused 1x1 conv + multi-step LIF (+ residual) on device tensors:
+    x [T, N, C, H, W] -> (spikes [T, N, C_out, H, W] in x.dtype, v_T
+    [N, C_out, H, W] f32), LIF(conv(x_t) + residual_t) at every step.
+
+    The input's spike map is taken from the neuron layer that produced x
+    when it handed one over (else x is prescanned into `workspace`); the
+    output's spike map is attached to the spikes for the next sparse conv.
+    One launch (sf_conv1x1_lif_sparse); the currents never reach HBM.
+    The membrane starts at v_init, or 0."""
+    from . import spike_map
+
+    if x.dim() != 5 or not x.is_cuda:
+        raise ValueError("sparse_conv1x1_lif_multistep takes a [T, N, C, H, W] device tensor")
+    T, N, C, H, W = (int(v) for v in x.shape)
+    C_OUT = int(weight.shape[0])
+    if tuple(weight.shape[1:]) != (C, 1, 1):
+        raise ValueError(f"weight {tuple(weight.shape)} is not a 1x1 kernel over {C} channels")
+    x = x.contiguous()
+    x4 = x.view(T * N, C, H, W)
+    if residual is not None:
+        if tuple(residual.shape) != (T, N, C_OUT, H, W):
+            raise ValueError(f"residual shape {tuple(residual.shape)} != {(T, N, C_OUT, H, W)}")
+        residual = residual.to(x.dtype).contiguous()
+    code = _lib.dtype_code(x.dtype)
+    desc = _lib.conv_desc(N, C, H, W, C_OUT, H, W, 1, 1, 0, code, code)
+    handed = spike_map.lookup(x4, threshold)
+    if handed is not None:
+        bits, flags = handed
+    else:
+        bits, flags = _lib.prescan_pack(x4, threshold)
+    wt = w_tap if w_tap is not None else _lib.tap_major_weight(weight)
+    b = None if bias is None else bias.detach().to(torch.float32).contiguous()
+    # V_0 = v_init, else 0 (as sparse_fused_conv_lif_multistep).
+    vi = None if v_init is None else v_init.detach().to(torch.float32).contiguous()
+    spikes = torch.empty((T, N, C_OUT, H, W), dtype=x.dtype, device=x.device)
+    v_out = torch.empty((N, C_OUT, H, W), dtype=torch.float32, device=x.device)
+    out_bits = out_flags = None
+    if emit_spike_map:
+        L = _lib.lib()
+        frames = T * N
+        out_bits = torch.empty(max(int(L.sf_prescan_bitmap_bytes(frames, C_OUT, H, W)) // 4, 1), dtype=torch.int32,
+                               device=x.device)
+        out_flags = torch.empty(max(int(L.sf_prescan_flags_bytes(frames, C_OUT, H, W)) // 4, 1), dtype=torch.int32,
+                                device=x.device)
+    _lib.conv1x1_lif_sparse(desc, T, bits, flags, x, wt, b, residual, lif_params(tau, v_threshold, v_reset,
+                                                                                 decay_input),
+                            vi, spikes, v_out, out_bits, out_flags)
+    if emit_spike_map:
+        spike_map.attach(spikes, T * N, C_OUT, H, W, out_bits, out_flags)
+    return spikes, v_out

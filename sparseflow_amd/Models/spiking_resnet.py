@@ -57,12 +57,21 @@ class SpikingBottleneck(nn.Module):
         self.bn3 = nn.BatchNorm2d(planes * self.expansion)
         self.downsample = downsample
         self.sn3 = _lif(**neuron)
+        # Set by fuse_conv_lif_: conv1 + sn1 and conv3 + (residual) + sn3 as
+        # single fused modules.
+        self.conv1_lif: Optional[nn.Module] = None
+        self.conv3_lif: Optional[nn.Module] = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        out = self.sn1(_seq(self.conv1, self.bn1, x))
+        if self.conv1_lif is not None:
+            out = self.conv1_lif(x)
+        else:
+            out = self.sn1(_seq(self.conv1, self.bn1, x))
         out = self.sn2(_seq(self.conv2, self.bn2, out))
-        out = _seq(self.conv3, self.bn3, out)
         identity = x if self.downsample is None else _seq(self.downsample[0], self.downsample[1], x)
+        if self.conv3_lif is not None:
+            return self.conv3_lif(out, identity)
+        out = _seq(self.conv3, self.bn3, out)
         return self.sn3(out, identity)  # LIF(out + identity), the add fused into the neuron pass
 
 
@@ -145,3 +154,25 @@ def fold_bn_(model: nn.Module) -> nn.Module:
             setattr(cparent, cname, fuse_conv_bn_eval(conv, bn))
             setattr(bparent, bname, nn.Identity())
     return model
+
+
+def fuse_conv_lif_(model: nn.Module) -> int:
+    """After optimize() and BN folding: run every bottleneck's 1x1 conv +
+    LIF pair (conv1 -> sn1, and conv3 -> + identity -> sn3) as one fused
+    kernel (Ops.sparse_fused_conv_lif.SparseConv1x1LIF), so the fp32 currents
+    of those layers never round-trip through HBM.  Spikes equal the unfused
+    model's up to threshold ties (the fused membrane update rounds
+    differently).  Returns the number of fused pairs; in place."""
+    from ..Ops.sparse_fused_conv_lif import SparseConv1x1LIF
+
+    n = 0
+    for mod in model.modules():
+        if not isinstance(mod, SpikingBottleneck):
+            continue
+        if isinstance(mod.bn1, nn.Identity) and SparseConv1x1LIF.eligible(mod.conv1, mod.sn1):
+            mod.conv1_lif = SparseConv1x1LIF(mod.conv1, mod.sn1)
+            n += 1
+        if isinstance(mod.bn3, nn.Identity) and SparseConv1x1LIF.eligible(mod.conv3, mod.sn3):
+            mod.conv3_lif = SparseConv1x1LIF(mod.conv3, mod.sn3)
+            n += 1
+    return n

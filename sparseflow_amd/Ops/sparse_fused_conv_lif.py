@@ -190,3 +190,47 @@ class FusedSparseConvLIF(nn.Module):
         return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, stride={self.stride}, "
                 f"padding={self.padding}, tau={self.tau}, v_threshold={self.v_threshold}, "
                 f"v_reset={self.v_reset}, block_size={bs}, fused=True, backend=hip_t_loop")
+
+
+class SparseConv1x1LIF(nn.Module):
+    """A 1x1 stride-1 SparseConv2d followed by its multi-step LIFNode (and an
+    optional residual added before the neuron), run as one fused kernel on
+    device tensors (Kernels.fused_conv_lif.sparse_conv1x1_lif_multistep).
+    Holds the two original modules: host tensors, and shapes the kernel does
+    not take, run them one after the other.  The membrane is the LIFNode's
+    `v` (so reset_net clears it)."""
+
+    def __init__(self, conv: nn.Module, lif: nn.Module):
+        super().__init__()
+        self.conv = conv
+        self.lif = lif
+
+    @staticmethod
+    def eligible(conv: nn.Module, lif: nn.Module) -> bool:
+        from ..neuron import LIFNode
+        from .sparse_conv2d import SparseConv2d
+
+        return (isinstance(conv, SparseConv2d) and isinstance(lif, LIFNode) and conv.kernel_size == (1, 1)
+                and conv.stride == (1, 1) and conv.padding == (0, 0) and conv.groups == 1
+                and conv.out_channels % 4 == 0 and lif.step_mode == "m")
+
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+        from ..Kernels.fused_conv_lif import sparse_conv1x1_lif_multistep
+
+        if x.dim() != 5 or not x.is_cuda or x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            T, N = x.shape[0], x.shape[1]
+            y = self.conv(x.flatten(0, 1))
+            y = y.reshape(T, N, *y.shape[1:])
+            return self.lif(y, residual) if residual is not None else self.lif(y)
+        lif = self.lif
+        v0 = lif.v if (lif.v is not None and lif.v.dim() == 4 and lif.v.device == x.device) else None
+        if v0 is None and lif.v_reset is not None and float(lif.v_reset) != 0.0:
+            # A fresh LIFNode starts at v_reset (hard reset), not 0.
+            T, N = x.shape[0], x.shape[1]
+            v0 = torch.full((N, self.conv.out_channels, x.shape[3], x.shape[4]), float(lif.v_reset),
+                            dtype=torch.float32, device=x.device)
+        spikes, lif.v = sparse_conv1x1_lif_multistep(
+            x, self.conv.weight, self.conv.bias, tau=lif.tau, v_threshold=lif.v_threshold, v_reset=lif.v_reset,
+            decay_input=lif.decay_input, residual=residual, threshold=self.conv.threshold, v_init=v0,
+            w_tap=self.conv._get_w_tap())
+        return spikes

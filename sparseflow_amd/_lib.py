@@ -50,6 +50,7 @@ EXPORTS = {
     "sf_conv2d_sparse": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_conv2d_forward": (c_int, [_P, _P, _P, _P, c_float, _P, c_size_t, _P, _P]),
     "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
+    "sf_conv1x1_lif_sparse": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_lif_multistep": (c_int, [_P, _P, c_int32, c_int32, c_int64, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P, _P,
                                  _P]),
     "sf_linear_bitmap_bytes": (c_size_t, [c_int64, c_int32]),
@@ -328,6 +329,16 @@ def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torc
     return spikes, v_out, (None if bits is None else (bits, flags))
 
 
+def conv1x1_lif_sparse(desc: ConvDesc, T: int, bits: torch.Tensor, flags: torch.Tensor, x: torch.Tensor,
+                       wt: torch.Tensor, bias: Optional[torch.Tensor], x2: Optional[torch.Tensor], lif: LifParams,
+                       v_init: Optional[torch.Tensor], spikes: torch.Tensor, v_out: torch.Tensor,
+                       out_bits: Optional[torch.Tensor], out_flags: Optional[torch.Tensor]) -> None:
+    rc = lib().sf_conv1x1_lif_sparse(ctypes.byref(desc), int(T), _ptr(bits), _ptr(flags), _ptr(x), _ptr(wt),
+                                     _ptr(bias), _ptr(x2), ctypes.byref(lif), _ptr(v_init), _ptr(spikes), _ptr(v_out),
+                                     _ptr(out_bits), _ptr(out_flags), _stream(x.device))
+    _check(rc, "sf_conv1x1_lif_sparse")
+
+
 # ---------------------------------------------------------------------------
 # Sparse linear / batched matmul
 # ---------------------------------------------------------------------------
@@ -434,7 +445,7 @@ def spike_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 
 KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                 "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
-                "linear_mfma", "bmm_mfma")
+                "linear_mfma", "bmm_mfma", "conv_lif_flat")
 
 
 def timing_enable(on: bool) -> None:

@@ -195,7 +195,7 @@ int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                                      "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse",
-                                     "spike_attention", "linear_mfma", "bmm_mfma"};
+                                     "spike_attention", "linear_mfma", "bmm_mfma", "conv_lif_flat"};
 
 }  // namespace
 
@@ -646,6 +646,39 @@ int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const f
   }
   rc = sf::launch_conv_lif(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "conv_lif launch");
+  return SF_OK;
+}
+
+int sf_conv1x1_lif_sparse(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags, const void* x,
+                          const float* wt, const float* bias, const void* x2, const sf_lif_params* lif,
+                          const float* v_init, void* spikes, float* v_out, uint32_t* out_bits, uint32_t* out_flags,
+                          void* stream) {
+  int rc = check_desc(d, false);
+  if (rc != SF_OK) return rc;
+  if (d->kernel != 1 || d->stride != 1) return fail(SF_ERR_UNSUPPORTED, "fused conv1x1-LIF: 1x1 stride 1 only");
+  if (d->c_out % 4 != 0) return fail(SF_ERR_UNSUPPORTED, "c_out must be a multiple of 4");
+  if (lif == nullptr) return fail(SF_ERR_INVALID, "lif params NULL");
+  if (T < 1) return fail(SF_ERR_INVALID, "T < 1");
+  if (!(lif->tau != 0.f)) return fail(SF_ERR_INVALID, "tau must be non-zero");
+  if ((out_bits == nullptr) != (out_flags == nullptr)) return fail(SF_ERR_INVALID, "out_bits and out_flags go together");
+  if (out_bits != nullptr && sf::words_per_pixel(d->c_out) > 64) return fail(SF_ERR_UNSUPPORTED, "c_out > 2048");
+  if (d->n == 0) return SF_OK;
+  if (bits == nullptr || flags == nullptr || x == nullptr || wt == nullptr || spikes == nullptr || v_out == nullptr)
+    return fail(SF_ERR_INVALID, "NULL pointer");
+  const int64_t frames = d->n * (int64_t)T;
+  sf::ConvArgs a = conv_args(d, frames, bits, flags, x, wt, bias, spikes, true);
+  a.v_out = v_out;
+  a.v_init = v_init;
+  a.T = T;
+  a.tau = lif->tau;
+  a.v_th = lif->v_threshold;
+  a.v_reset = lif->v_reset;
+  a.hard_reset = lif->hard_reset != 0;
+  a.decay_input = lif->decay_input != 0;
+  const sf::PackPlan op = sf::make_pack_plan(frames, d->c_out, d->h_out, d->w_out);
+  rc = sf::launch_conv_lif_flat(a, d->in_dtype, d->out_dtype, x2, out_bits, out_flags, op.cwp, op.chunk,
+                                op.chunks_per_frame, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "conv_lif_flat launch");
   return SF_OK;
 }
 

@@ -45,13 +45,14 @@ constexpr int kPxChunkBytes = kPxChunkCh * kPxRowBytes;    // 64 KB
 // which holds the 16-byte piece (q - row) mod 16 (channels 4 * piece .. +3).
 // Rows past C_in are skipped; channels past C_out read a valid but unrelated
 // address whose values are never stored.
+template <int NWAVES = kRowsWaves>
 __device__ __forceinline__ void load_chunk_px(char* buf, const float* __restrict__ wt, int c, int c_in, int c_out,
                                               int co0, int wave, int lane) {
   const int rows = min(kPxChunkCh, c_in - c * kPxChunkCh);
   const int units = (rows + 1) / 2;
 #pragma unroll
-  for (int j = 0; j < kPxChunkBytes / 1024 / kRowsWaves; ++j) {
-    const int u = wave + kRowsWaves * j;
+  for (int j = 0; j < kPxChunkBytes / 1024 / NWAVES; ++j) {
+    const int u = wave + NWAVES * j;
     if (u < units) {
       const int r = 2 * u + (lane >> 5);
       const int piece = ((lane & 31) - r) & 15;
@@ -228,6 +229,220 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
   }
 }
 
+// Output spike map of the fused LIF variant (the prescan layout of the
+// spikes: cwp words per pixel, chunk flags cleared).
+struct FlatLifOut {
+  uint32_t* bits;     // nullable
+  uint32_t* flags;
+  int cwp, chunk;
+  int64_t cpf;        // flag chunks per frame
+};
+
+// Fused 1x1 conv + multi-step LIF: a tile of 64 pixels of one sample runs all
+// T steps, the membrane carried in the accumulators between steps (seeded
+// with the decay form, as the 3x3 fused kernel does); an optional second
+// input x2 (a residual, same layout as the conv output) is added into the
+// current of each step.  Per step the lane stores its pixel's 64 spikes
+// (one channel per instruction) and, when requested, the two 32-channel
+// bitmap words of those spikes, so the next sparse convolution needs no
+// prescan.  The membrane after step T goes to v_out.
+// Eight wavefronts per workgroup (the membrane-carrying accumulators and the
+// step loop need more than the 128 registers a 16-wavefront group allows).
+constexpr int kLifWaves = 8;
+
+template <int CW, typename TIn, typename TOut>
+__global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, const uint32_t* __restrict__ bits,
+                                                                   const uint32_t* __restrict__ flags,
+                                                                   const TIn* __restrict__ x,
+                                                                   const float* __restrict__ wt,
+                                                                   const float* __restrict__ bias_p,
+                                                                   const TIn* __restrict__ x2,
+                                                                   TOut* __restrict__ spikes, FlatLifOut o,
+                                                                   int groups, int nchunks) {
+  typedef typename PxWord<CW>::type WT;
+  constexpr int NW = PxWord<CW>::count;
+  constexpr int BITS = 8 * (int)sizeof(WT);
+  extern __shared__ __align__(16) char smem[];
+  const int lane0 = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = blockIdx.x % groups;
+  const int co0 = grp * 64;
+  const int hw = a.hw_in;
+  const int tpf = (hw + 63) / 64;
+  const int total = (int)a.n * tpf;  // a.n = samples; the T steps run inside a tile
+  const int nblk = (int)(gridDim.x / groups);
+  const bool resident = nchunks <= 2;
+  const LifCoef L = lif_coef(a);
+
+  if (resident) {
+    for (int c = 0; c < nchunks; ++c)
+      load_chunk_px<kLifWaves>(smem + c * kPxChunkBytes, wt, c, a.c_in, a.c_out, co0, wave, lane0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  for (int pass = (int)(blockIdx.x / groups); pass * kLifWaves < total; pass += nblk) {
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int t = pass * kLifWaves + wave;
+    const bool valid = t < total;
+    const int sample = valid ? t / tpf : 0;
+    const int p0 = valid ? (t - sample * tpf) * 64 : 0;
+    const int npx = min(64, hw - p0);
+    const bool mine = valid && lane < npx;
+    const float* __restrict__ bias_t = bias_p;
+    int hw_t = hw, c_out_t = a.c_out;
+    asm volatile("" : "+s"(bias_t), "+s"(hw_t), "+s"(c_out_t));
+    const int nco = min(64, c_out_t - co0);
+    // Loads use the pixel and channel clamped into range (valid addresses;
+    // values of channels past C_out are never stored), stores are guarded.
+    const int lc = min(lane, npx - 1);
+    float acc[64];
+#pragma unroll
+    for (int co = 0; co < 64; ++co) acc[co] = 0.f;
+    if (a.v_init != nullptr && valid) {
+      const float* vp = a.v_init + ((int64_t)sample * c_out_t + co0) * hw_t + p0 + lc;
+#pragma unroll
+      for (int co = 0; co < 64; ++co) {
+        // Groups of eight loads: all 64 in flight would need 64 more registers.
+        if (co % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+        acc[co] = vp[(int64_t)min(co, nco - 1) * hw_t];
+      }
+    }
+    for (int st = 0; st < a.T; ++st) {
+      const int64_t frame = (int64_t)st * a.n + sample;
+      lif_seed<64>(acc, L, bias_t, co0, c_out_t);
+      if (x2 != nullptr && valid) {
+        const TIn* rp = x2 + (frame * c_out_t + co0) * hw_t + p0 + lc;
+#pragma unroll
+        for (int co = 0; co < 64; ++co) {
+          if (co % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+          acc[co] += to_f32<TIn>(rp[(int64_t)min(co, nco - 1) * hw_t]);
+        }
+      }
+      bool value = false;
+      if (valid) {
+        const int64_t c_a = p0 / a.chunk, c_b = (p0 + npx - 1) / a.chunk;
+        const uint32_t* __restrict__ fl = flags + frame * a.chunks_per_frame;
+        uint32_t f = 0u;
+        for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
+        value = f != 0u;
+      }
+      const TIn* xp = x + frame * a.c_in * hw + p0 + lane;
+      if (!resident) {
+        __syncthreads();  // the previous step/pass is done with both buffers
+        load_chunk_px<kLifWaves>(smem, wt, 0, a.c_in, a.c_out, co0, wave, lane);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+      }
+      for (int c = 0; c < nchunks; ++c) {
+        if (!resident && c + 1 < nchunks)
+          load_chunk_px<kLifWaves>(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, lane);
+        if (mine) {
+          WT w[NW];
+          const WT* __restrict__ bp = reinterpret_cast<const WT*>(bits + (frame * hw + p0 + lane) * a.cwp + c * CW);
+#pragma unroll
+          for (int j = 0; j < NW; ++j) w[j] = bp[j];
+          const char* chunk = smem + (resident ? c : (c & 1)) * kPxChunkBytes;
+#pragma unroll
+          for (int j = 0; j < NW; ++j) {
+            WT m = w[j];
+            while (m) {
+              const int r = j * BITS + px_first_bit(m);
+              m &= m - 1;
+              float xv = 1.f;
+              if (value) xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * hw]);
+              px_add_row(acc, chunk, r, xv);
+            }
+          }
+        }
+        if (!resident) {
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+        }
+      }
+      // H, spike, reset: the spikes are collected as two 32-channel words
+      // (the bitmap words of the spike map), then stored from them; the
+      // membrane stays in acc.
+      uint32_t w0 = 0u, w1 = 0u;
+#pragma unroll
+      for (int co = 0; co < 64; ++co) {
+        const float h = L.decay_input ? acc[co] * L.inv_tau : acc[co];
+        const bool fire = h >= L.v_th;
+        if (co < 32) w0 |= (fire ? 1u : 0u) << co;
+        else w1 |= (fire ? 1u : 0u) << (co - 32);
+        acc[co] = L.hard ? (fire ? L.v_reset : h) : h - (fire ? L.v_th : 0.f);
+      }
+      if (nco < 32) w0 &= (1u << nco) - 1u;
+      if (nco < 64) w1 &= nco > 32 ? (1u << (nco - 32)) - 1u : 0u;
+      if (mine) {
+        TOut* sp = spikes + (frame * c_out_t + co0) * hw_t + p0 + lane;
+        if (nco >= 64) {
+#pragma unroll
+          for (int co = 0; co < 64; ++co)
+            sp[(int64_t)co * hw_t] = from_f32<TOut>((float)(((co < 32 ? w0 : w1) >> (co & 31)) & 1u));
+        } else {
+          for (int co = 0; co < nco; ++co)
+            sp[(int64_t)co * hw_t] = from_f32<TOut>((float)(((co < 32 ? w0 : w1) >> (co & 31)) & 1u));
+        }
+      }
+      if (o.bits != nullptr && mine) {
+        uint32_t* ob = o.bits + (frame * hw_t + p0 + lane) * o.cwp;
+        const int w_0 = co0 / 32;
+        ob[w_0] = w0;
+        if (w_0 + 1 < o.cwp) ob[w_0 + 1] = w1;
+        if (grp == groups - 1)  // the words past the last group's channels
+          for (int wd = w_0 + 2; wd < o.cwp; ++wd) ob[wd] = 0u;
+      }
+      if (o.bits != nullptr && valid && grp == 0 && lane == 0 && p0 % o.chunk == 0)
+        o.flags[frame * o.cpf + p0 / o.chunk] = 0u;  // spikes are binary
+    }
+    if (mine) {
+      float* vp = a.v_out + ((int64_t)sample * c_out_t + co0) * hw_t + p0 + lane;
+      if (nco >= 64) {
+#pragma unroll
+        for (int co = 0; co < 64; ++co) vp[(int64_t)co * hw_t] = acc[co];
+      } else {
+#pragma unroll
+        for (int co = 0; co < 64; ++co)
+          if (co < nco) vp[(int64_t)co * hw_t] = acc[co];
+      }
+    }
+  }
+}
+
+template <int CW, typename TIn, typename TOut>
+int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hipStream_t stream) {
+  const int groups = (a.c_out + 63) / 64;
+  const int nchunks = CW < kPxChunkWords ? 1 : a.cwp / kPxChunkWords;
+  const int last_units = (min(kPxChunkCh, a.c_in - (nchunks - 1) * kPxChunkCh) + 1) / 2;
+  const size_t lds = nchunks <= 2 ? (size_t)(nchunks - 1) * kPxChunkBytes + (size_t)last_units * 1024
+                                  : (size_t)2 * kPxChunkBytes;
+  const int64_t tiles = a.n * (int64_t)((a.hw_in + 63) / 64);
+  const int64_t need = (tiles + kLifWaves - 1) / kLifWaves;
+  const int per_group = (int)(need < num_cus() ? need : num_cus());
+  const int grid = groups * (per_group > 0 ? per_group : 1);
+  auto kern = k_conv_flat_lif<CW, TIn, TOut>;
+  static bool attr_done = false;
+  if (!attr_done) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              kMaxLdsBytes);
+    attr_done = true;
+  }
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kLifWaves), lds, stream, a, a.bits, a.flags,
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<const TIn*>(x2),
+                     static_cast<TOut*>(a.y), o, groups, nchunks);
+  return (int)hipGetLastError();
+}
+
+template <typename TIn, typename TOut>
+int launch_flat_lif_d(const ConvArgs& a, const void* x2, const FlatLifOut& o, hipStream_t stream) {
+  switch (a.cwp) {
+    case 1: return launch_flat_lif_t<1, TIn, TOut>(a, x2, o, stream);
+    case 2: return launch_flat_lif_t<2, TIn, TOut>(a, x2, o, stream);
+    default: return launch_flat_lif_t<4, TIn, TOut>(a, x2, o, stream);
+  }
+}
+
 template <int CW, typename TIn, bool ROWS>
 int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
@@ -284,6 +499,23 @@ int launch_linear_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream
                  : in_dtype == SF_BF16 ? launch_flat_d<__hip_bfloat16, true>(a, out_dtype, stream)
                                        : launch_flat_d<float, true>(a, out_dtype, stream);
   timing_end(K_LINEAR, stream);
+  return rc;
+}
+
+int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, uint32_t* out_bits,
+                         uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf, hipStream_t stream) {
+  FlatLifOut o{out_bits, out_flags, out_cwp, out_chunk, out_cpf};
+  timing_begin(K_LIF_FLAT, stream);
+  int rc;
+  if (in_dtype == SF_F16)
+    rc = out_dtype == SF_F32 ? launch_flat_lif_d<__half, float>(a, x2, o, stream)
+                             : launch_flat_lif_d<__half, __half>(a, x2, o, stream);
+  else if (in_dtype == SF_BF16)
+    rc = out_dtype == SF_F32 ? launch_flat_lif_d<__hip_bfloat16, float>(a, x2, o, stream)
+                             : launch_flat_lif_d<__hip_bfloat16, __hip_bfloat16>(a, x2, o, stream);
+  else
+    rc = launch_flat_lif_d<float, float>(a, x2, o, stream);
+  timing_end(K_LIF_FLAT, stream);
   return rc;
 }
 

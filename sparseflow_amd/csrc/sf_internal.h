@@ -106,6 +106,15 @@ int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
 // applicability as px3_applicable with stride 1).
 int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Fused 1x1 s1 conv + multi-step LIF on the flat pixel-tile kernel (a: n =
+// samples, T steps, bits of the T*n input frames); x2: optional residual
+// (conv-output layout, x's dtype) added into each step's current; out_bits /
+// out_flags: optional spike map of the output in the prescan layout
+// (out_cwp words per pixel, flag chunks of out_chunk pixels, out_cpf per
+// frame).
+int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, uint32_t* out_bits,
+                         uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf, hipStream_t stream);
+
 // Standalone multi-step LIF over T steps of n x c x hw neurons (x2: optional
 // second input summed into the current; bits: optional spike map output in
 // the prescan layout with cwp words per pixel, with its nflags chunk flags
@@ -186,7 +195,7 @@ void conv_geometry(ConvArgs& a, bool lif);
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_COUNT = 16 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_LIF_FLAT = 16, K_COUNT = 17 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

@@ -141,31 +141,6 @@ __device__ __forceinline__ void px3_store(const float (&acc)[CO], TOut* __restri
   }
 }
 
-// Multi-step LIF on the accumulators.  The membrane lives in the accumulator
-// registers between steps, stored in the form that the next step's taps are
-// added to:
-//   decay_input:  acc = (tau - 1) V + V_r + b + sum  ->  H = acc / tau
-//   otherwise:    acc = (1 - 1/tau) V + V_r / tau + b + sum  ->  H = acc
-// (the same H as V + (I - (V - V_r)) / tau, resp. V - (V - V_r) / tau + I,
-// with I = b + sum, up to rounding).
-struct LifCoef {
-  float a, vr_term, inv_tau, v_th, v_reset;
-  bool hard, decay_input;
-};
-
-template <int CO>
-__device__ __forceinline__ void lif_seed(float (&acc)[CO], const LifCoef& L, const float* __restrict__ bias, int co0,
-                                         int c_out) {
-  if (bias != nullptr) {
-    // Channels past C_out read the last bias (never stored).
-#pragma unroll
-    for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], L.vr_term + bias[min(co0 + co, c_out - 1)]);
-  } else {
-#pragma unroll
-    for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], L.vr_term);
-  }
-}
-
 // H, spike and reset of one step: the spike of channel co goes straight to
 // sp[co * hw] (when the lane's pixel exists), the new membrane stays in acc.
 template <int CO, typename TOut>
@@ -203,17 +178,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
   const int nblk = (int)(gridDim.x / groups);
   const bool resident = nchunks <= LY::resident_chunks;
   const int steps = LIF ? a.T : 1;
-  LifCoef L;
-  L.inv_tau = 1.f / a.tau;
-  L.decay_input = a.decay_input != 0;
-  L.hard = a.hard_reset != 0;
-  L.v_th = a.v_th;
-  L.v_reset = a.v_reset;
-  {
-    const float vr = L.hard ? a.v_reset : 0.f;
-    L.a = L.decay_input ? a.tau - 1.f : 1.f - L.inv_tau;
-    L.vr_term = L.decay_input ? vr : vr * L.inv_tau;
-  }
+  const LifCoef L = lif_coef(a);
 
   if (resident) {
     for (int c = 0; c < nchunks; ++c)

@@ -1,0 +1,145 @@
+"""Fused 1x1 conv + multi-step LIF (+ residual) with spike-map output
+(sf_conv1x1_lif_sparse through Kernels.fused_conv_lif.sparse_conv1x1_lif_multistep),
+and the Spiking-ResNet50 fusion built on it.
+
+Bar: spikes equal the float64 closed form except at threshold ties
+(|H_ref - v_th| <= 1e-5, a neuron dropped from its first legitimate flip),
+membranes within 1e-4; the output spike map equals the prescan of the
+spikes bit for bit with all flags zero."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import conv as oconv
+from oracle import lif as olif
+from oracle import prescan as opre
+from sparseflow_amd import _lib
+from sparseflow_amd.Kernels import spike_map
+from sparseflow_amd.Kernels.fused_conv_lif import sparse_conv1x1_lif_multistep
+from tests.gpu_helpers import DEV, announce, bits_numpy, native_loaded, spikes
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # (T, N, C, H, W, Co, density, tau, v_th, v_reset, decay_input, bias, residual, gain)
+    (4, 2, 64, 14, 14, 64, 0.1, 2.0, 1.0, 0.0, True, True, True, 3.0),
+    (3, 2, 256, 7, 9, 128, 0.05, 2.0, 1.0, 0.0, True, False, True, 4.0),
+    (2, 3, 96, 5, 13, 68, 0.2, 1.5, 0.5, None, True, True, False, 2.0),    # soft reset, ragged C_out
+    (3, 2, 300, 6, 6, 32, 0.1, 2.0, 1.0, 0.0, False, True, True, 3.0),    # streamed weight chunks
+    (2, 2, 40, 8, 8, 260, 0.2, 3.0, 0.8, -0.2, True, True, True, 3.0),    # v_reset != 0, 5 output groups
+    (16, 2, 64, 56, 56, 256, 0.02, 2.0, 1.0, 0.0, True, False, True, 5.0),  # layer1 conv3 shape (fewer frames)
+]
+
+
+def _ref(x, w, b, res, tau, v_th, v_reset, decay_input, v0=None):
+    T = x.shape[0]
+    I = np.stack([oconv.sparse_conv2d_ref(x[t], w, b, 1, 0).numpy() for t in range(T)])
+    if res is not None:
+        I = I + res.double().numpy()
+    return olif.lif_multistep(I, tau, v_th, v_reset, decay_input,
+                              v0=None if v0 is None else v0.double().numpy(), dtype=np.float64)
+
+
+def _check(spk, v, s_ref, v_ref, h_ref, v_th):
+    bad, comparable = olif.compare_spikes(spk.cpu().numpy() > 0.5, s_ref, h_ref, v_th)
+    assert bad == 0, f"{bad} spike mismatches away from threshold ties"
+    alive = comparable[-1] & ~(((spk.cpu().numpy() > 0.5) != s_ref)[-1])
+    err = np.abs(v.double().cpu().numpy() - v_ref)[alive]
+    assert (err <= 1e-4 + 1e-4 * np.abs(v_ref[alive])).all(), f"max membrane err {err.max()}"
+    assert alive.mean() > 0.99
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_conv1x1_lif_matches_closed_form(case):
+    T, N, C, H, W, Co, p, tau, v_th, v_reset, dec, has_b, has_r, gain = case
+    announce(f"conv1x1 lif {case}")
+    g = torch.Generator().manual_seed(C + Co)
+    x = spikes((T, N, C, H, W), p, seed=T * 7 + C)
+    w = torch.randn(Co, C, 1, 1, generator=g) * gain / C ** 0.5
+    b = torch.randn(Co, generator=g) * 0.1 if has_b else None
+    r = spikes((T, N, Co, H, W), 0.3, seed=Co) if has_r else None
+    spike_map.clear()
+    spk, v = sparse_conv1x1_lif_multistep(x.to(DEV), w.to(DEV), None if b is None else b.to(DEV), tau=tau,
+                                          v_threshold=v_th, v_reset=v_reset, decay_input=dec,
+                                          residual=None if r is None else r.to(DEV))
+    torch.cuda.synchronize()
+    s_ref, v_ref, h_ref = _ref(x, w, b, r, tau, v_th, v_reset, dec)
+    _check(spk, v, s_ref, v_ref, h_ref, v_th)
+    assert 0.0 < float(spk.float().mean()) < 1.0
+    # The output spike map is the prescan of the spikes.
+    handed = spike_map.lookup(spk.view(T * N, Co, H, W), 1e-6)
+    assert handed is not None
+    cwp = opre.words_per_pixel(Co)
+    want = opre.bitmap(spk.view(T * N, Co, H, W).cpu().numpy(), 1e-6)
+    assert np.array_equal(bits_numpy(handed[0], T * N, H * W, cwp), want)
+    nfl = int(_lib.lib().sf_prescan_flags_bytes(T * N, Co, H, W)) // 4
+    assert int(handed[1][:nfl].abs().sum()) == 0
+    assert native_loaded()
+
+
+def test_conv1x1_lif_value_input_v_init_and_handed_map():
+    T, N, C, H, W, Co = 3, 2, 64, 10, 10, 64
+    g = torch.Generator().manual_seed(5)
+    x = spikes((T, N, C, H, W), 0.1, seed=6)
+    x[1, 0, :, 3] = x[1, 0, :, 3] * 2.0          # non-binary chunk: the value path
+    w = torch.randn(Co, C, 1, 1, generator=g) * 0.6
+    v0 = torch.rand(N, Co, H, W, generator=g) * 0.5
+    announce("conv1x1 lif value path + v_init")
+    spike_map.clear()
+    spk, v = sparse_conv1x1_lif_multistep(x.to(DEV), w.to(DEV), None, v_init=v0.to(DEV))
+    s_ref, v_ref, h_ref = _ref(x, w, None, None, 2.0, 1.0, 0.0, True, v0=v0)
+    _check(spk, v, s_ref, v_ref, h_ref, 1.0)
+    # Chained: the spikes' handed map feeds a second fused layer, which must
+    # give what it gives from a fresh prescan.
+    w2 = torch.randn(32, Co, 1, 1, generator=g) * 0.8
+    s2a, v2a = sparse_conv1x1_lif_multistep(spk, w2.to(DEV), None)
+    s2b, v2b = sparse_conv1x1_lif_multistep(spk.clone(), w2.to(DEV), None)
+    assert torch.equal(s2a, s2b) and torch.equal(v2a, v2b)
+
+
+def test_resnet50_fused_matches_unfused():
+    import copy
+
+    import sparseflow_amd as sf
+    from sparseflow_amd.Models import fold_bn_, fuse_conv_lif_, spiking_resnet50
+    from sparseflow_amd.neuron import LIFNode, reset_net
+
+    announce("resnet50 fused conv-LIF")
+    torch.manual_seed(0)
+    m = spiking_resnet50(T=2, num_classes=10)
+    with torch.no_grad():
+        for mod in m.modules():
+            if isinstance(mod, torch.nn.Conv2d):
+                mod.weight.mul_(3.0)
+    m = fold_bn_(m).to(DEV)
+    x = torch.randn(2, 3, 64, 64, generator=torch.Generator().manual_seed(1)).to(DEV)
+    sf.optimize(m, sample_input=x, verbose=False)
+    fused = copy.deepcopy(m)
+    n_fused = fuse_conv_lif_(fused)
+    assert n_fused >= 8
+
+    def record(model):
+        outs, hooks = {}, []
+        for name, mod in model.named_modules():
+            if isinstance(mod, LIFNode):
+                hooks.append(mod.register_forward_hook(
+                    lambda _m, _i, o, n=name: outs.__setitem__(n, o.detach().clone())))
+        return outs, hooks
+
+    with torch.no_grad():
+        reset_net(m)
+        ref = m(x)
+        reset_net(fused)
+        rec, hooks = record(fused)
+        _lib.timing_reset()
+        _lib.timing_enable(True)
+        out = fused(x)
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+        _lib.timing_enable(False)
+        for h in hooks:
+            h.remove()
+    assert stats["conv_lif_flat"][0] == n_fused
+    assert torch.allclose(out, ref, atol=1e-2, rtol=1e-2), (out - ref).abs().max()
+    assert any(float(s.float().mean()) > 0.01 for s in rec.values())
