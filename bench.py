@@ -242,7 +242,7 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
     import copy
 
     import sparseflow_amd as sf
-    from sparseflow_amd.Models import fold_bn_, spiking_resnet50
+    from sparseflow_amd.Models import fold_bn_, fuse_conv_lif_, spiking_resnet50
     from sparseflow_amd.neuron import LIFNode, reset_net
 
     t0 = time.time()
@@ -274,11 +274,18 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
     torch.cuda.synchronize()
     log(f"[bench] e2e: first forward done at {time.time() - t0:.1f} s")
     with torch.no_grad():
+        ums = time_gpu(lambda: run(model), steps, warmup)
+        log(f"[bench] e2e: unfused {ums:.2f} ms per forward ({time.time() - t0:.1f} s)")
+        # Bottleneck 1x1 conv + LIF pairs as one fused launch each.
+        n_fused = fuse_conv_lif_(model)
+        fout = run(model)
         ms = time_gpu(lambda: run(model), steps, warmup)
-        log(f"[bench] e2e: {ms:.2f} ms per forward ({time.time() - t0:.1f} s)")
+        log(f"[bench] e2e: fused ({n_fused} conv-LIF pairs) {ms:.2f} ms per forward ({time.time() - t0:.1f} s)")
         res = {
             "workload": E2E_WORKLOAD, "T": T, "batch": batch, "ms_per_forward": ms,
             "images_per_s": batch / (ms * 1e-3), "sparse_convs": n_sparse,
+            "fused_conv_lif_pairs": n_fused, "unfused_ms_per_forward": ums,
+            "max_abs_logit_diff_fused_vs_unfused": float((fout - out).abs().max()),
             "mean_spike_density": sum(densities.values()) / max(1, len(densities)),
             "spike_density_by_layer": {k: round(v, 5) for k, v in densities.items()},
         }

@@ -250,7 +250,8 @@ struct FlatLifOut {
 // step loop need more than the 128 registers a 16-wavefront group allows).
 constexpr int kLifWaves = 8;
 
-template <int CW, typename TIn, typename TOut>
+// VEC: C_out % 64 == 0 and H*W % 4 == 0 (four-pixel vector spike stores).
+template <int CW, typename TIn, typename TOut, bool VEC>
 __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                    const uint32_t* __restrict__ flags,
                                                                    const TIn* __restrict__ x,
@@ -273,6 +274,12 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
   const int nblk = (int)(gridDim.x / groups);
   const bool resident = nchunks <= 2;
   const LifCoef L = lif_coef(a);
+  __shared__ float s_seed[64];  // vr_term + bias of the group's channels
+  if (threadIdx.x < 64) {
+    const int c = min(co0 + (int)threadIdx.x, a.c_out - 1);
+    s_seed[threadIdx.x] = L.vr_term + (bias_p != nullptr ? bias_p[c] : 0.f);
+  }
+  __syncthreads();
 
   if (resident) {
     for (int c = 0; c < nchunks; ++c)
@@ -289,44 +296,59 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
     const int p0 = valid ? (t - sample * tpf) * 64 : 0;
     const int npx = min(64, hw - p0);
     const bool mine = valid && lane < npx;
-    const float* __restrict__ bias_t = bias_p;
     int hw_t = hw, c_out_t = a.c_out;
-    asm volatile("" : "+s"(bias_t), "+s"(hw_t), "+s"(c_out_t));
-    const int nco = min(64, c_out_t - co0);
+    asm volatile("" : "+s"(hw_t), "+s"(c_out_t));
+    int nco = VEC ? 64 : min(64, c_out_t - co0);
     // Loads use the pixel and channel clamped into range (valid addresses;
     // values of channels past C_out are never stored), stores are guarded.
     const int lc = min(lane, npx - 1);
     float acc[64];
 #pragma unroll
     for (int co = 0; co < 64; ++co) acc[co] = 0.f;
+    // Per-sample / per-frame planes [c_out, hw] through buffer descriptors.
+    const uint32_t vplane = (uint32_t)c_out_t * (uint32_t)hw_t * 4u;
     if (a.v_init != nullptr && valid) {
-      const float* vp = a.v_init + ((int64_t)sample * c_out_t + co0) * hw_t + p0 + lc;
+      const auto vr = buf_rsrc(a.v_init + (int64_t)sample * c_out_t * hw_t, vplane);
 #pragma unroll
-      for (int co = 0; co < 64; ++co) {
-        // Groups of eight loads: all 64 in flight would need 64 more registers.
-        if (co % 8 == 0) __builtin_amdgcn_sched_barrier(0);
-        acc[co] = vp[(int64_t)min(co, nco - 1) * hw_t];
-      }
+      for (int co = 0; co < 64; ++co) acc[co] = BufIO<float>::load(vr, (p0 + lc) * 4, (co0 + min(co, nco - 1)) * hw_t * 4);
     }
+    // Step st+1's residual, first-chunk bitmap words and flag are loaded one
+    // step ahead.  The vector memory counter retires in issue order, so with
+    // one store per channel plane (64 per step) they are issued before the
+    // stores; the vector-store path issues them after its 18 stores, which
+    // keeps the residual registers free while the store values are built.
+    // The residual stays in its input type until it is added (a conversion
+    // next to the load would wait for it).
+    TIn res[64];
+    WT bw[NW];
+    uint32_t fv = 0u;
+    auto fetch = [&](int st) {
+      const int64_t frame = (int64_t)st * a.n + sample;
+      if (x2 != nullptr) {
+        constexpr int B = (int)sizeof(TIn);
+        const auto rr = buf_rsrc(x2 + frame * c_out_t * hw_t, (uint32_t)c_out_t * (uint32_t)hw_t * B);
+#pragma unroll
+        for (int co = 0; co < 64; ++co) res[co] = BufIO<TIn>::load(rr, (p0 + lc) * B, (co0 + min(co, nco - 1)) * hw_t * B);
+      }
+      const WT* __restrict__ bp = reinterpret_cast<const WT*>(bits + (frame * hw + p0 + lc) * a.cwp);
+#pragma unroll
+      for (int j = 0; j < NW; ++j) bw[j] = bp[j];
+      // A 64-pixel tile lies in one flag chunk (chunks are multiples of 64).
+      fv = flags[frame * a.chunks_per_frame + p0 / a.chunk];
+    };
+    if (valid) fetch(0);
     for (int st = 0; st < a.T; ++st) {
       const int64_t frame = (int64_t)st * a.n + sample;
-      lif_seed<64>(acc, L, bias_t, co0, c_out_t);
-      if (x2 != nullptr && valid) {
-        const TIn* rp = x2 + (frame * c_out_t + co0) * hw_t + p0 + lc;
+      // Keep the per-channel offset arithmetic inside the step (hoisted, its
+      // 64 scalar offsets would spill).
+      asm volatile("" : "+s"(hw_t), "+s"(c_out_t));
+      nco = VEC ? 64 : min(64, c_out_t - co0);
+      lif_seed_lds<64>(acc, L, s_seed);
+      if (x2 != nullptr) {
 #pragma unroll
-        for (int co = 0; co < 64; ++co) {
-          if (co % 8 == 0) __builtin_amdgcn_sched_barrier(0);
-          acc[co] += to_f32<TIn>(rp[(int64_t)min(co, nco - 1) * hw_t]);
-        }
+        for (int co = 0; co < 64; ++co) acc[co] += to_f32<TIn>(res[co]);
       }
-      bool value = false;
-      if (valid) {
-        const int64_t c_a = p0 / a.chunk, c_b = (p0 + npx - 1) / a.chunk;
-        const uint32_t* __restrict__ fl = flags + frame * a.chunks_per_frame;
-        uint32_t f = 0u;
-        for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
-        value = f != 0u;
-      }
+      const bool value = valid && fv != 0u;
       const TIn* xp = x + frame * a.c_in * hw + p0 + lane;
       if (!resident) {
         __syncthreads();  // the previous step/pass is done with both buffers
@@ -339,9 +361,14 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
           load_chunk_px<kLifWaves>(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, lane);
         if (mine) {
           WT w[NW];
-          const WT* __restrict__ bp = reinterpret_cast<const WT*>(bits + (frame * hw + p0 + lane) * a.cwp + c * CW);
+          if (c == 0) {
 #pragma unroll
-          for (int j = 0; j < NW; ++j) w[j] = bp[j];
+            for (int j = 0; j < NW; ++j) w[j] = bw[j];
+          } else {
+            const WT* __restrict__ bp = reinterpret_cast<const WT*>(bits + (frame * hw + p0 + lane) * a.cwp + c * CW);
+#pragma unroll
+            for (int j = 0; j < NW; ++j) w[j] = bp[j];
+          }
           const char* chunk = smem + (resident ? c : (c & 1)) * kPxChunkBytes;
 #pragma unroll
           for (int j = 0; j < NW; ++j) {
@@ -374,15 +401,51 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
       }
       if (nco < 32) w0 &= (1u << nco) - 1u;
       if (nco < 64) w1 &= nco > 32 ? (1u << (nco - 32)) - 1u : 0u;
-      if (mine) {
-        TOut* sp = spikes + (frame * c_out_t + co0) * hw_t + p0 + lane;
+      if (!VEC && valid && st + 1 < a.T) fetch(st + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (VEC) {
+        // Lane l stores pixels p0 + 4*(l & 15) .. +3 of channel 4*i + (l >> 4),
+        // i = 0..15: sixteen vector stores per step instead of 64 (the four
+        // pixels' spike words are gathered from their lanes).  npx is a
+        // multiple of 4 here.
+        const int src = 4 * (lane & 15);
+        uint32_t g0[4], g1[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          g0[j] = __shfl(w0, src + j);
+          g1[j] = __shfl(w1, src + j);
+        }
+        if (valid && src < npx) {
+          constexpr int B = (int)sizeof(TOut);
+          const auto sr = buf_rsrc(spikes + frame * c_out_t * hw_t, (uint32_t)c_out_t * (uint32_t)hw_t * B);
+          const int cq = lane >> 4;
+          const int vo = ((co0 + cq) * hw_t + p0 + src) * B;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int sh = 4 * (i & 7) + cq;
+            const uint32_t* g = i < 8 ? g0 : g1;
+            const uint32_t q = ((g[0] >> sh) & 1u) | (((g[1] >> sh) & 1u) << 1) | (((g[2] >> sh) & 1u) << 2) |
+                               (((g[3] >> sh) & 1u) << 3);
+            store_bits4<TOut>(q, sr, vo + 4 * i * hw_t * B);
+          }
+        }
+      } else if (mine) {  // one channel plane per store
+        constexpr int B = (int)sizeof(TOut);
+        const auto sr = buf_rsrc(spikes + frame * c_out_t * hw_t, (uint32_t)c_out_t * (uint32_t)hw_t * B);
+        const int vo = (p0 + lane) * B;
         if (nco >= 64) {
 #pragma unroll
-          for (int co = 0; co < 64; ++co)
-            sp[(int64_t)co * hw_t] = from_f32<TOut>((float)(((co < 32 ? w0 : w1) >> (co & 31)) & 1u));
+          for (int co = 0; co < 64; ++co) {
+            // Groups of eight: the residual loads in flight already hold 64
+            // registers, so the 0/1 values are not all materialised first.
+            if (co % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+            BufIO<TOut>::store(from_f32<TOut>((float)(((co < 32 ? w0 : w1) >> (co & 31)) & 1u)), sr, vo,
+                               (co0 + co) * hw_t * B);
+          }
         } else {
           for (int co = 0; co < nco; ++co)
-            sp[(int64_t)co * hw_t] = from_f32<TOut>((float)(((co < 32 ? w0 : w1) >> (co & 31)) & 1u));
+            BufIO<TOut>::store(from_f32<TOut>((float)(((co < 32 ? w0 : w1) >> (co & 31)) & 1u)), sr, vo,
+                               (co0 + co) * hw_t * B);
         }
       }
       if (o.bits != nullptr && mine) {
@@ -395,22 +458,26 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
       }
       if (o.bits != nullptr && valid && grp == 0 && lane == 0 && p0 % o.chunk == 0)
         o.flags[frame * o.cpf + p0 / o.chunk] = 0u;  // spikes are binary
+      if (VEC && valid && st + 1 < a.T) {
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(st + 1);
+      }
     }
     if (mine) {
-      float* vp = a.v_out + ((int64_t)sample * c_out_t + co0) * hw_t + p0 + lane;
+      const auto vr = buf_rsrc(a.v_out + (int64_t)sample * c_out_t * hw_t, vplane);
       if (nco >= 64) {
 #pragma unroll
-        for (int co = 0; co < 64; ++co) vp[(int64_t)co * hw_t] = acc[co];
+        for (int co = 0; co < 64; ++co) BufIO<float>::store(acc[co], vr, (p0 + lane) * 4, (co0 + co) * hw_t * 4);
       } else {
 #pragma unroll
         for (int co = 0; co < 64; ++co)
-          if (co < nco) vp[(int64_t)co * hw_t] = acc[co];
+          if (co < nco) BufIO<float>::store(acc[co], vr, (p0 + lane) * 4, (co0 + co) * hw_t * 4);
       }
     }
   }
 }
 
-template <int CW, typename TIn, typename TOut>
+template <int CW, typename TIn, typename TOut, bool VEC>
 int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
   const int nchunks = CW < kPxChunkWords ? 1 : a.cwp / kPxChunkWords;
@@ -421,11 +488,13 @@ int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hi
   const int64_t need = (tiles + kLifWaves - 1) / kLifWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_flat_lif<CW, TIn, TOut>;
+  auto kern = k_conv_flat_lif<CW, TIn, TOut, VEC>;
   static bool attr_done = false;
   if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kMaxLdsBytes);
+    // The kernel also holds 256 B of static LDS (the per-channel seed).
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes - 1024);
+    if (e != hipSuccess) return (int)e;
     attr_done = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kLifWaves), lds, stream, a, a.bits, a.flags,
@@ -434,12 +503,18 @@ int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hi
   return (int)hipGetLastError();
 }
 
+template <int CW, typename TIn, typename TOut>
+int launch_flat_lif_v(const ConvArgs& a, const void* x2, const FlatLifOut& o, hipStream_t stream) {
+  if (a.c_out % 64 == 0 && a.hw_in % 4 == 0) return launch_flat_lif_t<CW, TIn, TOut, true>(a, x2, o, stream);
+  return launch_flat_lif_t<CW, TIn, TOut, false>(a, x2, o, stream);
+}
+
 template <typename TIn, typename TOut>
 int launch_flat_lif_d(const ConvArgs& a, const void* x2, const FlatLifOut& o, hipStream_t stream) {
   switch (a.cwp) {
-    case 1: return launch_flat_lif_t<1, TIn, TOut>(a, x2, o, stream);
-    case 2: return launch_flat_lif_t<2, TIn, TOut>(a, x2, o, stream);
-    default: return launch_flat_lif_t<4, TIn, TOut>(a, x2, o, stream);
+    case 1: return launch_flat_lif_v<1, TIn, TOut>(a, x2, o, stream);
+    case 2: return launch_flat_lif_v<2, TIn, TOut>(a, x2, o, stream);
+    default: return launch_flat_lif_v<4, TIn, TOut>(a, x2, o, stream);
   }
 }
 
@@ -505,6 +580,7 @@ int launch_linear_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream
 int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, uint32_t* out_bits,
                          uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf, hipStream_t stream) {
   FlatLifOut o{out_bits, out_flags, out_cwp, out_chunk, out_cpf};
+  if (a.chunk <= 0 || a.chunk % 64 != 0) return (int)hipErrorInvalidValue;  // one flag per 64-pixel tile
   timing_begin(K_LIF_FLAT, stream);
   int rc;
   if (in_dtype == SF_F16)

@@ -120,6 +120,67 @@ __device__ __forceinline__ void tile_store(float (&acc)[64], void* __restrict__ 
 //   otherwise:    acc = (1 - 1/tau) V + V_r / tau + b + sum  ->  H = acc
 // (the same H as V + (I - (V - V_r)) / tau, resp. V - (V - V_r) / tau + I,
 // with I = b + sum, up to rounding).
+// Raw buffer access (gfx9 descriptor: 32-bit untyped, no swizzle): the
+// per-lane byte offset sits in one VGPR and a uniform byte offset in an
+// SGPR, so 64 channel planes of one pixel need no per-channel 64-bit
+// addresses.  Offsets past num_records read 0 / drop the store.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)min(bytes, 0x7fffffffu), 0x00020000);
+}
+template <typename T>
+struct BufIO;
+template <>
+struct BufIO<float> {
+  static __device__ __forceinline__ float load(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+  }
+  static __device__ __forceinline__ void store(float v, __amdgpu_buffer_rsrc_t r, int vo, int so) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, vo, so, 0);
+  }
+};
+template <>
+struct BufIO<__half> {
+  static __device__ __forceinline__ __half load(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(__half, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
+  }
+  static __device__ __forceinline__ void store(__half v, __amdgpu_buffer_rsrc_t r, int vo, int so) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, vo, so, 0);
+  }
+};
+template <>
+struct BufIO<__hip_bfloat16> {
+  static __device__ __forceinline__ __hip_bfloat16 load(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(__hip_bfloat16, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
+  }
+  static __device__ __forceinline__ void store(__hip_bfloat16 v, __amdgpu_buffer_rsrc_t r, int vo, int so) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, vo, so, 0);
+  }
+};
+
+// Four consecutive 0/1 values (bits 0..3 of q) as one 16-byte (f32) or
+// 8-byte (f16 / bf16) buffer store.  The whole offset goes in the VGPR and
+// soffset is the constant 0: with an SGPR soffset the compiler adds no wait
+// state between a 16-byte store and a VALU write of its data registers, and
+// on gfx950 the last lanes of each 16-lane group then store the overwritten
+// value.
+typedef unsigned int sf_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int sf_u32x2 __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ void store_bits4(uint32_t q, __amdgpu_buffer_rsrc_t r, int vo) {
+  asm volatile("" : "+v"(vo));  // keep the offset in the VGPR operand
+  constexpr int so = 0;
+  if constexpr (sizeof(T) == 4) {
+    constexpr uint32_t one = 0x3f800000u;  // 1.0f
+    const sf_u32x4 v = {(q & 1u) ? one : 0u, (q & 2u) ? one : 0u, (q & 4u) ? one : 0u, (q & 8u) ? one : 0u};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, vo, so, 0);
+  } else {
+    constexpr uint32_t one = std::is_same<T, __half>::value ? 0x3c00u : 0x3f80u;  // 1.0 in f16 / bf16
+    const sf_u32x2 v = {((q & 1u) ? one : 0u) | ((q & 2u) ? one << 16 : 0u),
+                        ((q & 4u) ? one : 0u) | ((q & 8u) ? one << 16 : 0u)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, vo, so, 0);
+  }
+}
+
 struct LifCoef {
   float a, vr_term, inv_tau, v_th, v_reset;
   bool hard, decay_input;
@@ -136,6 +197,14 @@ __device__ __forceinline__ void lif_seed(float (&acc)[CO], const LifCoef& L, con
 #pragma unroll
     for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], L.vr_term);
   }
+}
+
+// Seed from per-channel constants staged in LDS (vr_term + bias): LDS
+// reads do not queue behind the wave's outstanding global stores.
+template <int CO>
+__device__ __forceinline__ void lif_seed_lds(float (&acc)[CO], const LifCoef& L, const float* seed) {
+#pragma unroll
+  for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], seed[co]);
 }
 
 // LIF coefficients from the launch arguments.

@@ -143,3 +143,27 @@ def test_resnet50_fused_matches_unfused():
     assert stats["conv_lif_flat"][0] == n_fused
     assert torch.allclose(out, ref, atol=1e-2, rtol=1e-2), (out - ref).abs().max()
     assert any(float(s.float().mean()) > 0.01 for s in rec.values())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hw", [(12, 12), (7, 9)])
+def test_conv1x1_lif_half_types_match_f32(dtype, hw):
+    # Binary spikes and residual are exact in f16 / bf16 and the sum is f32,
+    # so the spikes and the membrane equal the f32 run (vector-store path for
+    # H*W % 4 == 0, per-channel stores otherwise).
+    T, N, C, Co = 3, 2, 64, 128
+    H, W = hw
+    announce(f"conv1x1 lif {dtype} {hw}")
+    g = torch.Generator().manual_seed(11)
+    x = spikes((T, N, C, H, W), 0.15, seed=12)
+    r = spikes((T, N, Co, H, W), 0.3, seed=13)
+    w = torch.randn(Co, C, 1, 1, generator=g) * 0.5
+    b = torch.randn(Co, generator=g) * 0.1
+    spike_map.clear()
+    s32, v32 = sparse_conv1x1_lif_multistep(x.to(DEV), w.to(DEV), b.to(DEV), residual=r.to(DEV))
+    spike_map.clear()
+    s16, v16 = sparse_conv1x1_lif_multistep(x.to(DEV, dtype), w.to(DEV), b.to(DEV), residual=r.to(DEV, dtype))
+    torch.cuda.synchronize()
+    assert s16.dtype == dtype
+    assert torch.equal(s16.float(), s32) and torch.equal(v16, v32)
+    assert 0.0 < float(s32.mean()) < 1.0
