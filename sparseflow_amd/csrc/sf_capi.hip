@@ -356,7 +356,10 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
     if (rc != hipSuccess) return hip_fail(rc, "conv_rows launch");
     return SF_OK;
   }
-  if (sf::rows_kc_applicable(a)) {
+  // The row-band kernel where the pixel-tile kernel would have to stream its
+  // weights (C_in > 128 at 28x28 / 14x14); measured faster there, slower
+  // where the pixel-tile weights stay resident.
+  if (sf::rows_kc_applicable(a) && !(sf::px3_applicable(a) && sf::px3_resident(a))) {
     rc = sf::launch_conv_rows_kc(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
     if (rc != hipSuccess) return hip_fail(rc, "conv_rows_kc launch");
     return SF_OK;

@@ -140,6 +140,14 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
   const int total = (int)a.n * tpf;
   const int nblk = (int)(gridDim.x / groups);
   const bool resident = nchunks <= 2;
+  // The group's bias in LDS: read per pass from global memory it would be a
+  // vector load that waits for every store the wavefront still has in flight.
+  __shared__ float s_bias[64];
+  if (threadIdx.x < 64) {
+    const int co = co0 + (int)threadIdx.x;
+    s_bias[threadIdx.x] = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
+  }
+  __syncthreads();
 
   if (resident) {
     for (int c = 0; c < nchunks; ++c)
@@ -158,12 +166,11 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
     const bool mine = valid && lane < npx;  // this lane's pixel exists
     // Per-channel values (bias, store offsets) are formed in every pass,
     // not kept live across the loop: the accumulators need the registers.
-    const float* __restrict__ bias_t = bias_p;
     int hw_t = hw, c_out_t = a.c_out;
-    asm volatile("" : "+s"(bias_t), "+s"(hw_t), "+s"(c_out_t));
+    asm volatile("" : "+s"(hw_t), "+s"(c_out_t));
     float acc[64];
 #pragma unroll
-    for (int co = 0; co < 64; ++co) acc[co] = (bias_t != nullptr && co0 + co < c_out_t) ? bias_t[co0 + co] : 0.f;
+    for (int co = 0; co < 64; ++co) acc[co] = s_bias[co];
     bool value = false;
     if (valid) {
       const int64_t c_a = p0 / a.chunk, c_b = (p0 + npx - 1) / a.chunk;
@@ -534,8 +541,10 @@ int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   auto kern = k_conv_flat<CW, TIn, ROWS>;
   static bool attr_done = false;
   if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kMaxLdsBytes);
+    // 1 KB of the LDS is left to the kernel's static arrays.
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes - 1024);
+    if (e != hipSuccess) return (int)e;
     attr_done = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,

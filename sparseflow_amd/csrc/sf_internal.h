@@ -101,6 +101,8 @@ int launch_conv_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t
 
 // Pixel-tile Stage 2 for 3x3 convolutions (stride 1 or 2, C_out % 4 == 0).
 bool px3_applicable(const ConvArgs& a);
+// The weights stay resident in LDS for the whole launch (C_in <= 128).
+bool px3_resident(const ConvArgs& a);
 int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 // Fused conv + multi-step LIF on the pixel-tile formulation (3x3 s1; same
 // applicability as px3_applicable with stride 1).

@@ -44,9 +44,11 @@ template <int CO>
 struct Px3Layout {
   static constexpr int pieces = CO / 4;                         // logical pieces per row
   static constexpr int stride = CO == 64 ? 17 : pieces;         // pieces per row in LDS
+  static constexpr int xmask = CO == 64 ? 0 : (pieces >= 8 ? 7 : pieces - 1);  // piece swizzle
   static constexpr int units = (kPx3Rows * stride + 63) / 64;   // 1 KB load units per chunk
   static constexpr int chunk_bytes = units * 1024;
-  static constexpr int resident_chunks = kMaxLdsBytes / chunk_bytes;  // chunks that fit at once
+  // Chunks that fit at once (1 KB of the LDS is left to static arrays).
+  static constexpr int resident_chunks = (kMaxLdsBytes - 1024) / chunk_bytes;
 };
 
 // Direct-to-LDS loads of weight chunk c (output channels co0 .. co0+CO-1).
@@ -65,7 +67,7 @@ __device__ __forceinline__ void load_chunk_px3(char* buf, const float* __restric
       const int pos = u * 64 + lane;
       const int r = pos / L::stride;
       const int q = pos - r * L::stride;
-      const int s = CO == 64 ? q : (q ^ ((r >> 1) & 7));  // logical piece stored at position q
+      const int s = CO == 64 ? q : (q ^ ((r >> 1) & L::xmask));  // logical piece stored at position q
       const int row = c * kPx3Rows + r;
       const int col = co0 + 4 * s;
       const float* src =
@@ -80,7 +82,7 @@ template <int CO>
 __device__ __forceinline__ void px3_add_row(float (&acc)[CO], const char* chunk, int r, float xv) {
   typedef Px3Layout<CO> L;
   const char* rowp = chunk + (r * L::stride) * 16;
-  const int key = CO == 64 ? 0 : ((r >> 1) & 7) << 4;
+  const int key = CO == 64 ? 0 : ((r >> 1) & L::xmask) << 4;
 #pragma unroll
   for (int s = 0; s < L::pieces; ++s) {
     // Groups of four pieces: the scheduler may not hoist more than 16
@@ -179,6 +181,16 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
   const bool resident = nchunks <= LY::resident_chunks;
   const int steps = LIF ? a.T : 1;
   const LifCoef L = lif_coef(a);
+  // The group's bias (LIF: v_reset term + bias) in LDS: read per pass from
+  // global memory it would be a vector load that waits for every store the
+  // wavefront still has in flight.
+  __shared__ float s_seed[CO];
+  if (threadIdx.x < CO) {
+    const int co = co0 + (int)threadIdx.x;
+    const float b = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
+    s_seed[threadIdx.x] = LIF ? L.vr_term + b : b;
+  }
+  __syncthreads();
 
   if (resident) {
     for (int c = 0; c < nchunks; ++c)
@@ -205,9 +217,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
     const int ih0 = oh * a.s - 1, iw0 = ow * a.s - 1;
     // Per-channel values (bias, store offsets) are formed in every pass,
     // not kept live across the loop: the accumulators need the registers.
-    const float* __restrict__ bias_t = bias_p;
     int hwo_t = hwo, c_out_t = a.c_out;
-    asm volatile("" : "+s"(bias_t), "+s"(hwo_t), "+s"(c_out_t));
+    asm volatile("" : "+s"(hwo_t), "+s"(c_out_t));
     const int nco = min(CO, c_out_t - co0);
     float acc[CO];
     if constexpr (LIF) {
@@ -223,11 +234,11 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
       }
     } else {
 #pragma unroll
-      for (int co = 0; co < CO; ++co) acc[co] = (bias_t != nullptr && co0 + co < c_out_t) ? bias_t[co0 + co] : 0.f;
+      for (int co = 0; co < CO; ++co) acc[co] = s_seed[co];
     }
     for (int st = 0; st < steps; ++st) {
       const int64_t frame = LIF ? (int64_t)st * a.n + sample : sample;
-      if constexpr (LIF) lif_seed<CO>(acc, L, bias_t, co0, c_out_t);
+      if constexpr (LIF) lif_seed_lds<CO>(acc, L, s_seed);
       bool value = false;
       if (valid) {
         const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
@@ -324,8 +335,9 @@ int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   auto kern = k_conv_px3<TIn, TOut, CO, LIF>;
   static bool attr_done = false;
   if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kMaxLdsBytes);
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes - 1024);
+    if (e != hipSuccess) return (int)e;
     attr_done = true;
   }
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
@@ -333,10 +345,23 @@ int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
+template <int CO>
+int launch_px3_co(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  if (in_dtype == SF_F16) return launch_px3_t<__half, float, CO, false>(a, out_dtype, stream);
+  if (in_dtype == SF_BF16) return launch_px3_t<__hip_bfloat16, float, CO, false>(a, out_dtype, stream);
+  return launch_px3_t<float, float, CO, false>(a, out_dtype, stream);
+}
+
+// Output channels per workgroup slice: 64, or 32 where that keeps the
+// weights resident in LDS (64 < C_in <= 128), which removes the per-pass
+// chunk streaming and its barriers at the cost of walking the spikes once
+// per slice.  (A 16-channel slice, resident up to C_in = 256, walks too
+// often: slower than streaming.)
 int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
-  if (in_dtype == SF_F16) return launch_px3_t<__half, float, 64, false>(a, out_dtype, stream);
-  if (in_dtype == SF_BF16) return launch_px3_t<__hip_bfloat16, float, 64, false>(a, out_dtype, stream);
-  return launch_px3_t<float, float, 64, false>(a, out_dtype, stream);
+  const int nch = (a.c_in + kPx3Ch - 1) / kPx3Ch;
+  if (nch > Px3Layout<64>::resident_chunks && nch <= Px3Layout<32>::resident_chunks)
+    return launch_px3_co<32>(a, in_dtype, out_dtype, stream);
+  return launch_px3_co<64>(a, in_dtype, out_dtype, stream);
 }
 
 // Fused LIF: 32 output channels per workgroup.  The membrane shares the
@@ -359,6 +384,11 @@ int launch_px3_lif(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t s
 }
 
 }  // namespace
+
+bool px3_resident(const ConvArgs& a) {
+  const int nch = (a.c_in + kPx3Ch - 1) / kPx3Ch;
+  return nch <= Px3Layout<32>::resident_chunks;
+}
 
 bool px3_applicable(const ConvArgs& a) {
   return a.k == 3 && a.p == 1 && (a.s == 1 || a.s == 2) && a.c_out % 4 == 0 && a.cwp <= 64 &&

@@ -50,6 +50,8 @@ CASES = [
     (2, 33, 2, 14, 64),     # two-row frames: one tile per frame
     (1, 300, 14, 14, 64),   # last chunk partially filled
     (17, 128, 14, 14, 192), # passes whose last tiles are past the end
+    (4, 160, 28, 28, 128),  # C_in > 128: the row-band kernel at 28x28
+    (3, 192, 10, 14, 100),  # C_in > 128, last tile two rows, ragged group
 ]
 
 
@@ -62,7 +64,9 @@ def test_rows_kc_fp32_matches_dense(case, density):
     w = _weights(Co, C, seed=C + Co)
     b = torch.randn(Co, generator=torch.Generator().manual_seed(3)) * 0.1
     y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV))
-    expect = "conv_px3" if (H * W) % 4 else "conv_rows_kc"
+    # The pixel-tile kernel takes odd planes and C_in <= 128 (its weights then
+    # stay resident in LDS); the row-band kernel the rest.
+    expect = "conv_px3" if (H * W) % 4 or C <= 128 else "conv_rows_kc"
     assert expect in kernels and len(kernels) == 2, kernels  # prescan_pack + one conv kernel
     ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
     assert ok, f"max abs err {err}"
@@ -70,8 +74,8 @@ def test_rows_kc_fp32_matches_dense(case, density):
 
 
 def test_rows_kc_all_ones_input():
-    x = torch.ones(2, 128, 6, 14)
-    w = _weights(64, 128, seed=9)
+    x = torch.ones(2, 160, 6, 14)
+    w = _weights(64, 160, seed=9)
     announce("rows_kc all-ones")
     y, kernels = _run(x.to(DEV), w.to(DEV), None)
     assert "conv_rows_kc" in kernels
@@ -95,8 +99,8 @@ def test_rows_kc_value_path_only_where_flagged():
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_rows_kc_half_activations(dtype):
-    x = spikes((4, 128, 14, 14), 0.05, seed=11)
-    w = _weights(128, 128, seed=12)
+    x = spikes((4, 160, 14, 14), 0.05, seed=11)
+    w = _weights(128, 160, seed=12)
     b = torch.linspace(-0.5, 0.5, 128)
     announce(f"rows_kc {dtype}")
     y, kernels = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV))
@@ -110,8 +114,8 @@ def test_rows_kc_half_activations(dtype):
 
 
 def test_rows_kc_deterministic_bitwise():
-    x = spikes((32, 128, 28, 28), 0.02, seed=13).to(DEV)
-    w = _weights(128, 128, seed=14).to(DEV)
+    x = spikes((32, 160, 28, 28), 0.02, seed=13).to(DEV)
+    w = _weights(128, 160, seed=14).to(DEV)
     announce("rows_kc determinism")
     y1, _ = _run(x, w, None)
     y2, _ = _run(x, w, None)
