@@ -359,13 +359,19 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
       const TIn* xp = x + frame * a.c_in * hw + p0 + lane;
       if (!resident) {
         __syncthreads();  // the previous step/pass is done with both buffers
-        load_chunk_px<kLifWaves>(smem, wt, 0, a.c_in, a.c_out, co0, wave, lane);
+        // Streaming addresses formed here (hoisted, they would be spilled).
+        int ll = lane;
+        asm volatile("" : "+v"(ll));
+        load_chunk_px<kLifWaves>(smem, wt, 0, a.c_in, a.c_out, co0, wave, ll);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
       }
       for (int c = 0; c < nchunks; ++c) {
-        if (!resident && c + 1 < nchunks)
-          load_chunk_px<kLifWaves>(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, lane);
+        if (!resident && c + 1 < nchunks) {
+          int ll = lane;
+          asm volatile("" : "+v"(ll));
+          load_chunk_px<kLifWaves>(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, ll);
+        }
         if (mine) {
           WT w[NW];
           if (c == 0) {

@@ -250,15 +250,23 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
       if (mine) px3_load_words(wn, bf, a, ih0, iw0, 0);
       if (!resident) {
         __syncthreads();  // the previous step/pass is done with both buffers
-        load_chunk_px3<CO>(smem, wt, 0, krows, a.c_out, co0, wave, lane);
+        // The streaming addresses are formed here, not hoisted to the pass
+        // start: kept live they would be spilled to scratch on every pass,
+        // resident or not.
+        int ll = lane;
+        asm volatile("" : "+v"(ll));
+        load_chunk_px3<CO>(smem, wt, 0, krows, a.c_out, co0, wave, ll);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
       }
       for (int c = 0; c < nchunks; ++c) {
         // Stream chunk c+1 into the other buffer; it was last read during
         // chunk c-1, which every wavefront finished before the last barrier.
-        if (!resident && c + 1 < nchunks)
-          load_chunk_px3<CO>(smem + ((c + 1) & 1) * LY::chunk_bytes, wt, c + 1, krows, a.c_out, co0, wave, lane);
+        if (!resident && c + 1 < nchunks) {
+          int ll = lane;
+          asm volatile("" : "+v"(ll));
+          load_chunk_px3<CO>(smem + ((c + 1) & 1) * LY::chunk_bytes, wt, c + 1, krows, a.c_out, co0, wave, ll);
+        }
         if (mine) {
           // This chunk's words were loaded during the previous chunk's walk;
           // start the next chunk's loads now.
