@@ -185,6 +185,21 @@ int sf_conv1x1_lif_sparse(const sf_conv_desc* desc, int32_t T,
                           const float* v_init, void* spikes, float* v_out,
                           uint32_t* out_bits, uint32_t* out_flags, void* stream);
 
+/* sf_conv1x1_lif_sparse with a binary residual (values 0 / 1 only, e.g. the
+ * spikes entering a bottleneck) given by its spike map instead of its
+ * values: res_bits in the layout of out_bits
+ * (sf_bitmap_words_per_pixel(c_out) words per pixel of the T*n frames).  The
+ * results equal those of sf_conv1x1_lif_sparse on the residual's values; the
+ * residual costs 1/32 of its fp32 bytes.  Same reference interface as
+ * sf_conv1x1_lif_sparse (the identity add of the reference models'
+ * bottlenecks, Benchmark/bench_4test.py:166-197). */
+int sf_conv1x1_lif_sparse_binres(const sf_conv_desc* desc, int32_t T,
+                                 const uint32_t* bits, const uint32_t* flags,
+                                 const void* x, const float* wt, const float* bias,
+                                 const uint32_t* res_bits, const sf_lif_params* lif,
+                                 const float* v_init, void* spikes, float* v_out,
+                                 uint32_t* out_bits, uint32_t* out_flags, void* stream);
+
 /* ---- spiking neuron -------------------------------------------------------- */
 
 /* Multi-step LIF over T steps of n x c x hw neurons: x [T, n, c, hw] input

@@ -209,6 +209,13 @@ def sparse_conv1x1_lif_multistep(
         residual = residual.to(x.dtype).contiguous()
     code = _lib.dtype_code(x.dtype)
     desc = _lib.conv_desc(N, C, H, W, C_OUT, H, W, 1, 1, 0, code, code)
+    # A residual that is itself a registered spike tensor (the spikes entering
+    # a bottleneck) is read from its bitmap: 1/32 of its fp32 bytes.
+    res_bits = None
+    if residual is not None:
+        rmap = spike_map.lookup(residual.view(T * N, C_OUT, H, W), threshold)
+        if rmap is not None:
+            res_bits = rmap[0]
     handed = spike_map.lookup(x4, threshold)
     if handed is not None:
         bits, flags = handed
@@ -230,7 +237,7 @@ def sparse_conv1x1_lif_multistep(
                                 device=x.device)
     _lib.conv1x1_lif_sparse(desc, T, bits, flags, x, wt, b, residual, lif_params(tau, v_threshold, v_reset,
                                                                                  decay_input),
-                            vi, spikes, v_out, out_bits, out_flags)
+                            vi, spikes, v_out, out_bits, out_flags, res_bits=res_bits)
     if emit_spike_map:
         spike_map.attach(spikes, T * N, C_OUT, H, W, out_bits, out_flags)
     return spikes, v_out

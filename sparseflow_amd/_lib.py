@@ -51,6 +51,7 @@ EXPORTS = {
     "sf_conv2d_forward": (c_int, [_P, _P, _P, _P, c_float, _P, c_size_t, _P, _P]),
     "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
     "sf_conv1x1_lif_sparse": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "sf_conv1x1_lif_sparse_binres": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_lif_multistep": (c_int, [_P, _P, c_int32, c_int32, c_int64, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P, _P,
                                  _P]),
     "sf_linear_bitmap_bytes": (c_size_t, [c_int64, c_int32]),
@@ -332,7 +333,17 @@ def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torc
 def conv1x1_lif_sparse(desc: ConvDesc, T: int, bits: torch.Tensor, flags: torch.Tensor, x: torch.Tensor,
                        wt: torch.Tensor, bias: Optional[torch.Tensor], x2: Optional[torch.Tensor], lif: LifParams,
                        v_init: Optional[torch.Tensor], spikes: torch.Tensor, v_out: torch.Tensor,
-                       out_bits: Optional[torch.Tensor], out_flags: Optional[torch.Tensor]) -> None:
+                       out_bits: Optional[torch.Tensor], out_flags: Optional[torch.Tensor],
+                       res_bits: Optional[torch.Tensor] = None) -> None:
+    """res_bits: a binary residual's spike map, read instead of x2
+    (sf_conv1x1_lif_sparse_binres)."""
+    if res_bits is not None:
+        rc = lib().sf_conv1x1_lif_sparse_binres(ctypes.byref(desc), int(T), _ptr(bits), _ptr(flags), _ptr(x),
+                                                _ptr(wt), _ptr(bias), _ptr(res_bits), ctypes.byref(lif),
+                                                _ptr(v_init), _ptr(spikes), _ptr(v_out), _ptr(out_bits),
+                                                _ptr(out_flags), _stream(x.device))
+        _check(rc, "sf_conv1x1_lif_sparse_binres")
+        return
     rc = lib().sf_conv1x1_lif_sparse(ctypes.byref(desc), int(T), _ptr(bits), _ptr(flags), _ptr(x), _ptr(wt),
                                      _ptr(bias), _ptr(x2), ctypes.byref(lif), _ptr(v_init), _ptr(spikes), _ptr(v_out),
                                      _ptr(out_bits), _ptr(out_flags), _stream(x.device))

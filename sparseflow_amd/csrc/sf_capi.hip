@@ -652,10 +652,10 @@ int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const f
   return SF_OK;
 }
 
-int sf_conv1x1_lif_sparse(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags, const void* x,
-                          const float* wt, const float* bias, const void* x2, const sf_lif_params* lif,
-                          const float* v_init, void* spikes, float* v_out, uint32_t* out_bits, uint32_t* out_flags,
-                          void* stream) {
+static int conv1x1_lif_impl(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags,
+                            const void* x, const float* wt, const float* bias, const void* x2,
+                            const uint32_t* res_bits, const sf_lif_params* lif, const float* v_init, void* spikes,
+                            float* v_out, uint32_t* out_bits, uint32_t* out_flags, void* stream) {
   int rc = check_desc(d, false);
   if (rc != SF_OK) return rc;
   if (d->kernel != 1 || d->stride != 1) return fail(SF_ERR_UNSUPPORTED, "fused conv1x1-LIF: 1x1 stride 1 only");
@@ -679,10 +679,27 @@ int sf_conv1x1_lif_sparse(const sf_conv_desc* d, int32_t T, const uint32_t* bits
   a.hard_reset = lif->hard_reset != 0;
   a.decay_input = lif->decay_input != 0;
   const sf::PackPlan op = sf::make_pack_plan(frames, d->c_out, d->h_out, d->w_out);
-  rc = sf::launch_conv_lif_flat(a, d->in_dtype, d->out_dtype, x2, out_bits, out_flags, op.cwp, op.chunk,
+  rc = sf::launch_conv_lif_flat(a, d->in_dtype, d->out_dtype, x2, res_bits, out_bits, out_flags, op.cwp, op.chunk,
                                 op.chunks_per_frame, static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "conv_lif_flat launch");
   return SF_OK;
+}
+
+int sf_conv1x1_lif_sparse(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags, const void* x,
+                          const float* wt, const float* bias, const void* x2, const sf_lif_params* lif,
+                          const float* v_init, void* spikes, float* v_out, uint32_t* out_bits, uint32_t* out_flags,
+                          void* stream) {
+  return conv1x1_lif_impl(d, T, bits, flags, x, wt, bias, x2, nullptr, lif, v_init, spikes, v_out, out_bits,
+                          out_flags, stream);
+}
+
+int sf_conv1x1_lif_sparse_binres(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags,
+                                 const void* x, const float* wt, const float* bias, const uint32_t* res_bits,
+                                 const sf_lif_params* lif, const float* v_init, void* spikes, float* v_out,
+                                 uint32_t* out_bits, uint32_t* out_flags, void* stream) {
+  if (d != nullptr && d->n > 0 && res_bits == nullptr) return fail(SF_ERR_INVALID, "res_bits NULL");
+  return conv1x1_lif_impl(d, T, bits, flags, x, wt, bias, nullptr, res_bits, lif, v_init, spikes, v_out, out_bits,
+                          out_flags, stream);
 }
 
 int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T, int64_t n, int32_t c, int64_t hw,

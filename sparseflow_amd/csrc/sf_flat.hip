@@ -243,6 +243,9 @@ struct FlatLifOut {
   uint32_t* flags;
   int cwp, chunk;
   int64_t cpf;        // flag chunks per frame
+  // Nullable: a binary residual given by its spike map (same layout as bits),
+  // read instead of x2: two words per pixel instead of 64 values.
+  const uint32_t* rbits;
 };
 
 // Fused 1x1 conv + multi-step LIF: a tile of 64 pixels of one sample runs all
@@ -328,10 +331,14 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
     // next to the load would wait for it).
     TIn res[64];
     WT bw[NW];
-    uint32_t fv = 0u;
+    uint32_t fv = 0u, rw0 = 0u, rw1 = 0u;
     auto fetch = [&](int st) {
       const int64_t frame = (int64_t)st * a.n + sample;
-      if (x2 != nullptr) {
+      if (o.rbits != nullptr) {
+        const uint32_t* rp = o.rbits + (frame * hw_t + p0 + lc) * o.cwp + co0 / 32;
+        rw0 = rp[0];
+        rw1 = co0 / 32 + 1 < o.cwp ? rp[1] : 0u;
+      } else if (x2 != nullptr) {
         constexpr int B = (int)sizeof(TIn);
         const auto rr = buf_rsrc(x2 + frame * c_out_t * hw_t, (uint32_t)c_out_t * (uint32_t)hw_t * B);
 #pragma unroll
@@ -351,7 +358,11 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
       asm volatile("" : "+s"(hw_t), "+s"(c_out_t));
       nco = VEC ? 64 : min(64, c_out_t - co0);
       lif_seed_lds<64>(acc, L, s_seed);
-      if (x2 != nullptr) {
+      if (o.rbits != nullptr) {
+        // The same sums as adding the 0 / 1 values.
+#pragma unroll
+        for (int co = 0; co < 64; ++co) acc[co] += (((co < 32 ? rw0 : rw1) >> (co & 31)) & 1u) ? 1.f : 0.f;
+      } else if (x2 != nullptr) {
 #pragma unroll
         for (int co = 0; co < 64; ++co) acc[co] += to_f32<TIn>(res[co]);
       }
@@ -592,9 +603,10 @@ int launch_linear_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream
   return rc;
 }
 
-int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, uint32_t* out_bits,
-                         uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf, hipStream_t stream) {
-  FlatLifOut o{out_bits, out_flags, out_cwp, out_chunk, out_cpf};
+int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, const uint32_t* res_bits,
+                         uint32_t* out_bits, uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf,
+                         hipStream_t stream) {
+  FlatLifOut o{out_bits, out_flags, out_cwp, out_chunk, out_cpf, res_bits};
   if (a.chunk <= 0 || a.chunk % 64 != 0) return (int)hipErrorInvalidValue;  // one flag per 64-pixel tile
   timing_begin(K_LIF_FLAT, stream);
   int rc;

@@ -113,9 +113,11 @@ int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStrea
 // (conv-output layout, x's dtype) added into each step's current; out_bits /
 // out_flags: optional spike map of the output in the prescan layout
 // (out_cwp words per pixel, flag chunks of out_chunk pixels, out_cpf per
-// frame).
-int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, uint32_t* out_bits,
-                         uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf, hipStream_t stream);
+// frame); res_bits: optional binary residual as its spike map in that same
+// layout, read instead of x2.
+int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, const uint32_t* res_bits,
+                         uint32_t* out_bits, uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf,
+                         hipStream_t stream);
 
 // Standalone multi-step LIF over T steps of n x c x hw neurons (x2: optional
 // second input summed into the current; bits: optional spike map output in

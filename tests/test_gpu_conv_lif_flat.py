@@ -167,3 +167,34 @@ def test_conv1x1_lif_half_types_match_f32(dtype, hw):
     assert s16.dtype == dtype
     assert torch.equal(s16.float(), s32) and torch.equal(v16, v32)
     assert 0.0 < float(s32.mean()) < 1.0
+
+
+def test_conv1x1_lif_binary_residual_from_its_spike_map(monkeypatch):
+    # A residual that is a registered spike tensor is read from its bitmap
+    # (sf_conv1x1_lif_sparse_binres); the results equal the values path.
+    T, N, C, H, W, Co = 3, 2, 64, 12, 12, 128
+    announce("conv1x1 lif binary residual from its spike map")
+    g = torch.Generator().manual_seed(21)
+    x = spikes((T, N, C, H, W), 0.2, seed=22)
+    w1 = torch.randn(Co, C, 1, 1, generator=g) * 0.6
+    w2 = torch.randn(Co, C, 1, 1, generator=g) * 0.6
+    b2 = torch.randn(Co, generator=g) * 0.1
+    spike_map.clear()
+    res, _ = sparse_conv1x1_lif_multistep(x.to(DEV), w1.to(DEV), None)   # registered spikes
+    assert spike_map.lookup(res.view(T * N, Co, H, W), 1e-6) is not None
+    assert 0.0 < float(res.mean()) < 1.0
+    used = []
+    real = _lib.conv1x1_lif_sparse
+
+    def spy(*args, **kw):
+        used.append(kw.get("res_bits") is not None)
+        return real(*args, **kw)
+
+    monkeypatch.setattr(_lib, "conv1x1_lif_sparse", spy)
+    s_b, v_b = sparse_conv1x1_lif_multistep(x.to(DEV), w2.to(DEV), b2.to(DEV), residual=res)
+    s_v, v_v = sparse_conv1x1_lif_multistep(x.to(DEV), w2.to(DEV), b2.to(DEV), residual=res.clone())
+    torch.cuda.synchronize()
+    assert used == [True, False]
+    assert torch.equal(s_b, s_v) and torch.equal(v_b, v_v)
+    s_ref, v_ref, h_ref = _ref(x, w2, b2, res.cpu(), 2.0, 1.0, 0.0, True)
+    _check(s_b, v_b, s_ref, v_ref, h_ref, 1.0)
