@@ -256,13 +256,17 @@ struct FlatLifOut {
 // (one channel per instruction) and, when requested, the two 32-channel
 // bitmap words of those spikes, so the next sparse convolution needs no
 // prescan.  The membrane after step T goes to v_out.
-// Eight wavefronts per workgroup (the membrane-carrying accumulators and the
-// step loop need more than the 128 registers a 16-wavefront group allows).
-constexpr int kLifWaves = 8;
+// Four or eight wavefronts per workgroup (the membrane-carrying accumulators
+// and the step loop need more than the 128 registers a 16-wavefront group
+// allows).
 
 // VEC: C_out % 64 == 0 and H*W % 4 == 0 (four-pixel vector spike stores).
-template <int CW, typename TIn, typename TOut, bool VEC>
-__global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, const uint32_t* __restrict__ bits,
+// XV: a residual given by its values (x2); without it the 64 prefetch
+// registers of the residual are not allocated.
+// NWV: wavefronts per workgroup (4 where the weights are small enough for
+// three workgroups per CU, else 8).
+template <int CW, typename TIn, typename TOut, bool VEC, bool XV, int NWV>
+__global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(XV ? 2 : 3, 8))) void k_conv_flat_lif(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                    const uint32_t* __restrict__ flags,
                                                                    const TIn* __restrict__ x,
                                                                    const float* __restrict__ wt,
@@ -293,14 +297,14 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
 
   if (resident) {
     for (int c = 0; c < nchunks; ++c)
-      load_chunk_px<kLifWaves>(smem + c * kPxChunkBytes, wt, c, a.c_in, a.c_out, co0, wave, lane0);
+      load_chunk_px<NWV>(smem + c * kPxChunkBytes, wt, c, a.c_in, a.c_out, co0, wave, lane0);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  for (int pass = (int)(blockIdx.x / groups); pass * kLifWaves < total; pass += nblk) {
+  for (int pass = (int)(blockIdx.x / groups); pass * NWV < total; pass += nblk) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
-    const int t = pass * kLifWaves + wave;
+    const int t = pass * NWV + wave;
     const bool valid = t < total;
     const int sample = valid ? t / tpf : 0;
     const int p0 = valid ? (t - sample * tpf) * 64 : 0;
@@ -329,7 +333,7 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
     // keeps the residual registers free while the store values are built.
     // The residual stays in its input type until it is added (a conversion
     // next to the load would wait for it).
-    TIn res[64];
+    TIn res[XV ? 64 : 1];
     WT bw[NW];
     uint32_t fv = 0u, rw0 = 0u, rw1 = 0u;
     auto fetch = [&](int st) {
@@ -338,7 +342,7 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
         const uint32_t* rp = o.rbits + (frame * hw_t + p0 + lc) * o.cwp + co0 / 32;
         rw0 = rp[0];
         rw1 = co0 / 32 + 1 < o.cwp ? rp[1] : 0u;
-      } else if (x2 != nullptr) {
+      } else if (XV && x2 != nullptr) {
         constexpr int B = (int)sizeof(TIn);
         const auto rr = buf_rsrc(x2 + frame * c_out_t * hw_t, (uint32_t)c_out_t * (uint32_t)hw_t * B);
 #pragma unroll
@@ -362,7 +366,7 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
         // The same sums as adding the 0 / 1 values.
 #pragma unroll
         for (int co = 0; co < 64; ++co) acc[co] += (((co < 32 ? rw0 : rw1) >> (co & 31)) & 1u) ? 1.f : 0.f;
-      } else if (x2 != nullptr) {
+      } else if (XV && x2 != nullptr) {
 #pragma unroll
         for (int co = 0; co < 64; ++co) acc[co] += to_f32<TIn>(res[co]);
       }
@@ -373,7 +377,7 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
         // Streaming addresses formed here (hoisted, they would be spilled).
         int ll = lane;
         asm volatile("" : "+v"(ll));
-        load_chunk_px<kLifWaves>(smem, wt, 0, a.c_in, a.c_out, co0, wave, ll);
+        load_chunk_px<NWV>(smem, wt, 0, a.c_in, a.c_out, co0, wave, ll);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
       }
@@ -381,7 +385,7 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
         if (!resident && c + 1 < nchunks) {
           int ll = lane;
           asm volatile("" : "+v"(ll));
-          load_chunk_px<kLifWaves>(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, ll);
+          load_chunk_px<NWV>(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, ll);
         }
         if (mine) {
           WT w[NW];
@@ -501,7 +505,7 @@ __global__ __launch_bounds__(64 * kLifWaves) void k_conv_flat_lif(ConvArgs a, co
   }
 }
 
-template <int CW, typename TIn, typename TOut, bool VEC>
+template <int CW, typename TIn, typename TOut, bool VEC, bool XV, int NWV>
 int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
   const int nchunks = CW < kPxChunkWords ? 1 : a.cwp / kPxChunkWords;
@@ -509,10 +513,11 @@ int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hi
   const size_t lds = nchunks <= 2 ? (size_t)(nchunks - 1) * kPxChunkBytes + (size_t)last_units * 1024
                                   : (size_t)2 * kPxChunkBytes;
   const int64_t tiles = a.n * (int64_t)((a.hw_in + 63) / 64);
-  const int64_t need = (tiles + kLifWaves - 1) / kLifWaves;
-  const int per_group = (int)(need < num_cus() ? need : num_cus());
+  const int64_t need = (tiles + NWV - 1) / NWV;
+  const int64_t cap = (int64_t)num_cus() * (NWV == 4 ? 3 : 1);  // resident workgroups
+  const int per_group = (int)(need < cap ? need : cap);
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_flat_lif<CW, TIn, TOut, VEC>;
+  auto kern = k_conv_flat_lif<CW, TIn, TOut, VEC, XV, NWV>;
   static bool attr_done = false;
   if (!attr_done) {
     // The kernel also holds 256 B of static LDS (the per-channel seed).
@@ -521,7 +526,7 @@ int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hi
     if (e != hipSuccess) return (int)e;
     attr_done = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kLifWaves), lds, stream, a, a.bits, a.flags,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NWV), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<const TIn*>(x2),
                      static_cast<TOut*>(a.y), o, groups, nchunks);
   return (int)hipGetLastError();
@@ -529,8 +534,19 @@ int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hi
 
 template <int CW, typename TIn, typename TOut>
 int launch_flat_lif_v(const ConvArgs& a, const void* x2, const FlatLifOut& o, hipStream_t stream) {
-  if (a.c_out % 64 == 0 && a.hw_in % 4 == 0) return launch_flat_lif_t<CW, TIn, TOut, true>(a, x2, o, stream);
-  return launch_flat_lif_t<CW, TIn, TOut, false>(a, x2, o, stream);
+  const bool vec = a.c_out % 64 == 0 && a.hw_in % 4 == 0;
+  const bool xv = x2 != nullptr && o.rbits == nullptr;
+  // Three 4-wave workgroups per CU when their weights fit three times in LDS
+  // (C_in <= 96) and no value residual takes the registers.
+  const bool small = !xv && a.c_in <= 96;
+  if (vec) {
+    if (xv) return launch_flat_lif_t<CW, TIn, TOut, true, true, 8>(a, x2, o, stream);
+    return small ? launch_flat_lif_t<CW, TIn, TOut, true, false, 4>(a, x2, o, stream)
+                 : launch_flat_lif_t<CW, TIn, TOut, true, false, 8>(a, x2, o, stream);
+  }
+  if (xv) return launch_flat_lif_t<CW, TIn, TOut, false, true, 8>(a, x2, o, stream);
+  return small ? launch_flat_lif_t<CW, TIn, TOut, false, false, 4>(a, x2, o, stream)
+               : launch_flat_lif_t<CW, TIn, TOut, false, false, 8>(a, x2, o, stream);
 }
 
 template <typename TIn, typename TOut>
