@@ -181,23 +181,15 @@ __device__ __forceinline__ void store_bits4(uint32_t q, __amdgpu_buffer_rsrc_t r
   }
 }
 
+// The LIF charge step in the accumulators: with acc = a * V + vr_term + I,
+//   decay_input:  H = V + (I - (V - Vr)) / tau = acc / tau  (a = tau - 1, vr_term = Vr)
+//   otherwise:    H = V - (V - Vr) / tau + I  = acc        (a = 1 - 1/tau, vr_term = Vr / tau)
+// (Vr = v_reset for hard reset, 0 for soft reset), so the current I (bias +
+// spike sums + residual) is accumulated on top of the seeded membrane.
 struct LifCoef {
   float a, vr_term, inv_tau, v_th, v_reset;
   bool hard, decay_input;
 };
-
-template <int CO>
-__device__ __forceinline__ void lif_seed(float (&acc)[CO], const LifCoef& L, const float* __restrict__ bias, int co0,
-                                         int c_out) {
-  if (bias != nullptr) {
-    // Channels past C_out read the last bias (never stored).
-#pragma unroll
-    for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], L.vr_term + bias[min(co0 + co, c_out - 1)]);
-  } else {
-#pragma unroll
-    for (int co = 0; co < CO; ++co) acc[co] = fmaf(L.a, acc[co], L.vr_term);
-  }
-}
 
 // Seed from per-channel constants staged in LDS (vr_term + bias): LDS
 // reads do not queue behind the wave's outstanding global stores.
