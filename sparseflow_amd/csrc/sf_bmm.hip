@@ -44,7 +44,10 @@ __global__ __launch_bounds__(64 * kBmmWaves) void k_bmm(BmmArgs a) {
     const int nbw = min(NB, N - n0);
     __syncthreads();  // the previous item is done with the staged block
     const T* __restrict__ Bb = B + bt * a.b_stride_batch;
+    // Unrolled so that eight global loads are in flight per thread (the LDS
+    // stores do not alias them).
     if (a.b_stride_n == 1) {
+#pragma unroll 8
       for (int i = threadIdx.x; i < K * NB; i += 64 * kBmmWaves) {
         const int kk = i / NB, j = i - kk * NB;
         sb[kk * LD + j] = j < nbw ? to_f32<T>(Bb[(int64_t)kk * a.b_stride_k + n0 + j]) : 0.f;
@@ -52,6 +55,7 @@ __global__ __launch_bounds__(64 * kBmmWaves) void k_bmm(BmmArgs a) {
     } else {
       // Consecutive threads take consecutive k (the contiguous axis of a
       // transposed B).
+#pragma unroll 8
       for (int i = threadIdx.x; i < K * NB; i += 64 * kBmmWaves) {
         const int j = i / K, kk = i - j * K;
         sb[kk * LD + j] = j < nbw ? to_f32<T>(Bb[(int64_t)kk * a.b_stride_k + (int64_t)(n0 + j) * a.b_stride_n]) : 0.f;
@@ -195,17 +199,35 @@ __global__ __launch_bounds__(256) void k_bmm_mfma(BmmArgs a) {
   for (int64_t bt = blockIdx.x; bt < a.batches; bt += gridDim.x) {
     __syncthreads();  // the previous batch is done with s_b
     const T* __restrict__ Bb = B + bt * a.b_stride_batch;
-    // Stage B: consecutive threads walk B's contiguous axis.
+    // Stage B: consecutive threads walk B's contiguous axis, sixteen loads in
+    // flight per thread (one at a time, the staging was a chain of up to a
+    // few hundred dependent global loads).
     const bool kfast = a.b_stride_k == 1 && a.b_stride_n != 1;
-    for (int i = tid; i < npad * kp; i += 256) {
-      int kk, nn;
-      if (kfast) { nn = i / kp; kk = i - nn * kp; } else { kk = i / npad; nn = i - kk * npad; }
-      const float v = (kk < K && nn < N) ? to_f32<T>(Bb[(int64_t)kk * a.b_stride_k + (int64_t)nn * a.b_stride_n]) : 0.f;
-      const uint16_t h = bm_bf16_bits(v);
-      const uint16_t l = bm_bf16_bits(v - __uint_as_float((uint32_t)h << 16));
-      const int pos = bm_pos(nn, kk, kp);
-      s_bh[pos] = h;
-      s_bl[pos] = l;
+    const int nb = npad * kp;
+    constexpr int U = 16;
+    for (int i0 = tid; i0 < nb; i0 += 256 * U) {
+      float v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + 256 * u;
+        int kk, nn;
+        if (kfast) { nn = i / kp; kk = i - nn * kp; } else { kk = i / npad; nn = i - kk * npad; }
+        v[u] = (i < nb && kk < K && nn < N) ? to_f32<T>(Bb[(int64_t)kk * a.b_stride_k + (int64_t)nn * a.b_stride_n])
+                                            : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + 256 * u;
+        if (i < nb) {
+          int kk, nn;
+          if (kfast) { nn = i / kp; kk = i - nn * kp; } else { kk = i / npad; nn = i - kk * npad; }
+          const uint16_t h = bm_bf16_bits(v[u]);
+          const uint16_t l = bm_bf16_bits(v[u] - __uint_as_float((uint32_t)h << 16));
+          const int pos = bm_pos(nn, kk, kp);
+          s_bh[pos] = h;
+          s_bl[pos] = l;
+        }
+      }
     }
     __syncthreads();
     const T* __restrict__ Ab = A + bt * (int64_t)M * K;
