@@ -88,8 +88,10 @@ __device__ __forceinline__ bool rows_value_path(const ConvArgs& a, const uint32_
 
 // The bitmap, flags, x and weights are passed as separate restrict-qualified
 // arguments so that their uniform loads compile to scalar (SMEM) loads.
-template <typename TIn, typename TOut, int W, int CWP>
-__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, const uint32_t* __restrict__ bits,
+// NWR wavefronts per workgroup: 16, or 4 when 16-wave workgroups would leave
+// CUs idle (few rows: the weights are then loaded by more workgroups).
+template <typename TIn, typename TOut, int W, int CWP, int NWR>
+__global__ __launch_bounds__(64 * NWR) void k_conv_rows(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                const uint32_t* __restrict__ flags,
                                                                const TIn* __restrict__ x, const float* __restrict__ wt,
                                                                const float* __restrict__ bias_p, TOut* __restrict__ y,
@@ -102,18 +104,52 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows(ConvArgs a, const
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = blockIdx.x % groups;
   const int co0 = grp * 64;
-  for (int i = threadIdx.x; i < krows * 64; i += 64 * kRowsWaves) {
-    const int r = i >> 6, c = i & 63;
-    wl[i] = (co0 + c < a.c_out) ? wt[(int64_t)r * a.c_out + co0 + c] : 0.f;
+  // Weights straight from global memory into LDS (direct loads, 1 KB = four
+  // 64-channel rows per wavefront instruction, all in flight; 16-byte pieces
+  // of a row need C_out % 4 == 0); columns past C_out are then zeroed.
+  // Otherwise eight loads in flight per thread through registers.
+  if (a.c_out % 4 != 0) {
+    const int nw = krows * 64;
+    const int c = threadIdx.x & 63;  // the stride is a multiple of 64
+    const bool cok = co0 + c < a.c_out;
+    const int cc = cok ? co0 + c : 0;
+    for (int i0 = threadIdx.x; i0 < nw; i0 += 64 * NWR * 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + 64 * NWR * u;
+        const int r = (i < nw ? i : 0) >> 6;
+        v[u] = wt[(int64_t)r * a.c_out + cc];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = i0 + 64 * NWR * u;
+        if (i < nw) wl[i] = cok ? v[u] : 0.f;
+      }
+    }
+  } else {
+    const int units = (krows + 3) / 4;
+    for (int u = wave; u < units; u += NWR) {
+      const int r = u * 4 + (lane >> 4);
+      const int col = co0 + 4 * (lane & 15);
+      const float* src = (r < krows && col < a.c_out) ? wt + (int64_t)r * a.c_out + col : wt;
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(smem + u * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    if (co0 + 64 > a.c_out) {
+      __syncthreads();
+      for (int i = threadIdx.x; i < krows * 64; i += 64 * NWR)
+        if (co0 + (i & 63) >= a.c_out) wl[i] = 0.f;
+    }
   }
   __syncthreads();
   const char* wlb = smem + lane * 4;
   const float bias = (bias_p != nullptr && co0 + lane < a.c_out) ? bias_p[co0 + lane] : 0.f;
   const int rows_total = (int)(a.n * a.h_out);
-  const int wpg = (int)(gridDim.x / groups) * kRowsWaves;
+  const int wpg = (int)(gridDim.x / groups) * NWR;
   const int q = lane & (QP - 1);
   const int cbase = lane & ~(QP - 1);
-  for (int t = (int)(blockIdx.x / groups) * kRowsWaves + wave; t < rows_total; t += wpg) {
+  for (int t = (int)(blockIdx.x / groups) * NWR + wave; t < rows_total; t += wpg) {
     const int frame = t / a.h_out;
     const int oh = t - frame * a.h_out;
     float acc[4 * QP];
@@ -338,30 +374,34 @@ int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stre
   return (int)hipGetLastError();
 }
 
-template <typename TIn, typename TOut, int W, int CWP>
+template <typename TIn, typename TOut, int W, int CWP, int NWR>
 int launch_rows_t(const ConvArgs& a, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
   const int krows = a.c_in * 9;
-  const size_t lds = (size_t)krows * 64 * sizeof(float);
+  const size_t lds = (size_t)((krows + 3) / 4) * 1024;  // whole 1 KB load units
   const int64_t rows_total = a.n * (int64_t)a.h_out;
-  const int64_t need = (rows_total + kRowsWaves - 1) / kRowsWaves;
+  const int64_t need = (rows_total + NWR - 1) / NWR;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_rows<TIn, TOut, W, CWP>;
+  auto kern = k_conv_rows<TIn, TOut, W, CWP, NWR>;
   static bool attr_done = false;
   if (!attr_done) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               kMaxLdsBytes);
     attr_done = true;
   }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NWR), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, krows);
   return (int)hipGetLastError();
 }
 
 template <typename TIn, typename TOut>
 int launch_rows_d(const ConvArgs& a, hipStream_t stream) {
-  return a.cwp == 1 ? launch_rows_t<TIn, TOut, 32, 1>(a, stream) : launch_rows_t<TIn, TOut, 32, 2>(a, stream);
+  const int groups = (a.c_out + 63) / 64;
+  const bool few = a.n * (int64_t)a.h_out * groups < (int64_t)kRowsWaves * num_cus();
+  if (few) return a.cwp == 1 ? launch_rows_t<TIn, TOut, 32, 1, 4>(a, stream) : launch_rows_t<TIn, TOut, 32, 2, 4>(a, stream);
+  return a.cwp == 1 ? launch_rows_t<TIn, TOut, 32, 1, kRowsWaves>(a, stream)
+                    : launch_rows_t<TIn, TOut, 32, 2, kRowsWaves>(a, stream);
 }
 
 }  // namespace
