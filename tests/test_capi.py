@@ -153,3 +153,27 @@ def test_linear_bmm_attention_sizes_and_validation():
     assert L.sf_spike_attention(p, p, p, 0, 2, 196, 12, 48, st, 0.2, 1e-6, p, st, 0, None) == _lib.SF_ERR_UNSUPPORTED
     assert L.sf_spike_attention(p, p, p, 0, 0, 196, 12, 32, st, 0.2, 1e-6, p, st, 0, None) == _lib.SF_OK
     assert L.sf_spike_attention(p, p, p, 0, 2, 196, 12, 32, None, 0.2, 1e-6, p, st, 0, None) == _lib.SF_ERR_INVALID
+
+
+def test_fused_conv1x1_lif_validation_without_touching_the_device():
+    L = _lib.lib()
+    d = ctypes.c_void_p(16)
+    lif = _lib.LifParams(2.0, 1.0, 0.0, 1, 1)
+    ok = _lib.conv_desc(2, 64, 8, 8, 64, 8, 8, 1, 1, 0, 0, 0)
+    k3 = _lib.conv_desc(2, 64, 8, 8, 64, 8, 8, 3, 1, 1, 0, 0)
+    args = (d, d, d, d, None)  # bits, flags, x, wt, bias
+    for fn, extra in ((L.sf_conv1x1_lif_sparse, None), (L.sf_conv1x1_lif_sparse_binres, d)):
+        # 3x3 is not this entry's pattern; T < 1 and a NULL spikes pointer are invalid.
+        assert _status(fn, ctypes.byref(k3), 2, *args, extra, ctypes.byref(lif), None, d, d, None, None, None) \
+            == _lib.SF_ERR_UNSUPPORTED
+        assert _status(fn, ctypes.byref(ok), 0, *args, extra, ctypes.byref(lif), None, d, d, None, None, None) \
+            == _lib.SF_ERR_INVALID
+        assert _status(fn, ctypes.byref(ok), 2, *args, extra, ctypes.byref(lif), None, None, d, None, None, None) \
+            == _lib.SF_ERR_INVALID
+        # out_bits and out_flags go together.
+        assert _status(fn, ctypes.byref(ok), 2, *args, extra, ctypes.byref(lif), None, d, d, d, None, None) \
+            == _lib.SF_ERR_INVALID
+    # The binary-residual entry needs its residual map.
+    assert _status(L.sf_conv1x1_lif_sparse_binres, ctypes.byref(ok), 2, *args, None, ctypes.byref(lif), None, d, d,
+                   None, None, None) == _lib.SF_ERR_INVALID
+    assert b"res_bits" in L.sf_last_error()
