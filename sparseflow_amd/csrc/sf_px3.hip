@@ -236,6 +236,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
 #pragma unroll
       for (int co = 0; co < CO; ++co) acc[co] = s_seed[co];
     }
+    // First-chunk bitmap words of the next step are loaded before this step's
+    // spike stores (the vector memory counter retires in issue order).
+    uint32_t wn[9];
+    if (mine) px3_load_words(wn, bits + (LIF ? sample : sample) * a.hw_in * a.cwp, a, ih0, iw0, 0);
     for (int st = 0; st < steps; ++st) {
       const int64_t frame = LIF ? (int64_t)st * a.n + sample : sample;
       if constexpr (LIF) lif_seed_lds<CO>(acc, L, s_seed);
@@ -246,8 +250,6 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
       }
       const uint32_t* __restrict__ bf = bits + frame * a.hw_in * a.cwp;
       const TIn* __restrict__ xf = x + frame * a.c_in * a.hw_in;
-      uint32_t wn[9];
-      if (mine) px3_load_words(wn, bf, a, ih0, iw0, 0);
       if (!resident) {
         __syncthreads();  // the previous step/pass is done with both buffers
         // The streaming addresses are formed here, not hoisted to the pass
@@ -309,10 +311,46 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
         }
       }
       if constexpr (LIF) {
-        // H, spike and the reset; the spikes of this step are stored now and
-        // the membrane stays in acc.
-        const int64_t sb = (frame * c_out_t + co0) * hwo_t + p0 + lane;
-        lif_step<CO>(acc, L, static_cast<TOut*>(y) + sb, hwo_t, nco, mine);
+        // H, spike and the reset: the spikes are collected as one word per
+        // 32 channels (the membrane stays in acc), the next step's words are
+        // requested, then the spikes are stored.
+        static_assert(!LIF || CO <= 32, "one spike word per lane");
+        uint32_t sw = 0u;
+#pragma unroll
+        for (int co = 0; co < CO; ++co) {
+          const float h = L.decay_input ? acc[co] * L.inv_tau : acc[co];
+          const bool fire = h >= L.v_th;
+          sw |= (fire ? 1u : 0u) << co;
+          acc[co] = L.hard ? (fire ? L.v_reset : h) : h - (fire ? L.v_th : 0.f);
+        }
+        if (st + 1 < steps && mine)
+          px3_load_words(wn, bits + (frame + a.n) * a.hw_in * a.cwp, a, ih0, iw0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        TOut* __restrict__ spk = static_cast<TOut*>(y) + (frame * c_out_t + co0) * hwo_t;
+        if (nco == 32 && CO == 32 && (hwo_t & 3) == 0) {
+          // Lane l stores pixels p0 + 4*(l & 15) .. +3 of channel 4*i + (l >> 4):
+          // eight vector stores instead of 32 (npx is a multiple of 4).
+          const int src = 4 * (lane & 15);
+          uint32_t gw[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) gw[j] = __shfl(sw, src + j);
+          if (valid && src < npx) {
+            constexpr int B = (int)sizeof(TOut);
+            const auto sr = buf_rsrc(spk, (uint32_t)c_out_t * (uint32_t)hwo_t * B);
+            const int cq = lane >> 4;
+            const int vo = ((cq) * hwo_t + p0 + src) * B;
+#pragma unroll
+            for (int i = 0; i < CO / 4; ++i) {
+              const int sh = 4 * i + cq;
+              const uint32_t q = ((gw[0] >> sh) & 1u) | (((gw[1] >> sh) & 1u) << 1) | (((gw[2] >> sh) & 1u) << 2) |
+                                 (((gw[3] >> sh) & 1u) << 3);
+              store_bits4<TOut>(q, sr, vo + 4 * i * hwo_t * B);
+            }
+          }
+        } else if (mine) {
+          for (int co = 0; co < nco; ++co)
+            spk[(int64_t)co * hwo_t + p0 + lane] = from_f32<TOut>(((sw >> co) & 1u) ? 1.f : 0.f);
+        }
       }
     }
     if (mine) {
