@@ -207,7 +207,10 @@ __device__ __forceinline__ void load_chunk(char* buf, const float* __restrict__ 
 }
 
 struct KcTile {
-  const uint32_t* rowbits;  // bitmap word `chunk` of input row oh0 - 1 (may lie outside the frame)
+  // The chunk's bitmap words of the (TH + 2) x W halo positions, position p
+  // in lane p & 63 of vw0 (p < 64) or vw1: fetched with two vector loads and
+  // read on the scalar unit with readlane at compile-time lanes.
+  uint32_t vw0, vw1;
   const void* x;            // x plane of the frame (value path)
   int64_t xrow;             // element offset of input row oh0 - 1 within a channel plane
   const char* wlb;          // LDS weight chunk + lane offset
@@ -248,15 +251,28 @@ __device__ __forceinline__ void kc_batch_walk(float (&acc)[64], const uint32_t (
   }
 }
 
+template <int P>
+__device__ __forceinline__ uint32_t kc_word(const KcTile& k) {
+  static_assert(P < 128, "halo positions fit two words per lane");
+  return __builtin_amdgcn_readlane(P < 64 ? k.vw0 : k.vw1, P & 63);
+}
+
+template <int P, int U, int NB>
+__device__ __forceinline__ void kc_fill(uint32_t (&mw)[8], const KcTile& k) {
+  if constexpr (U < NB) {
+    mw[U] = kc_word<P + U>(k);
+    kc_fill<P, U + 1, NB>(mw, k);
+  }
+}
+
 template <int TH, int W, int IA, int B0>
-__device__ __forceinline__ void kc_row(float (&acc)[64], const uint32_t* __restrict__ rp, const KcTile& k) {
+__device__ __forceinline__ void kc_row(float (&acc)[64], const KcTile& k) {
   if constexpr (B0 < W) {
     constexpr int NB = (W - B0) < 8 ? (W - B0) : 8;
     uint32_t mw[8];
-#pragma unroll
-    for (int u = 0; u < NB; ++u) mw[u] = rp[(B0 + u) * k.cwp];
+    kc_fill<IA * W + B0, 0, NB>(mw, k);
     kc_batch_walk<TH, W, IA, B0, 0, NB>(acc, mw, k);
-    kc_row<TH, W, IA, B0 + 8>(acc, rp, k);
+    kc_row<TH, W, IA, B0 + 8>(acc, k);
   }
 }
 
@@ -264,9 +280,23 @@ template <int TH, int W, int IA>
 __device__ __forceinline__ void kc_rows(float (&acc)[64], const KcTile& k) {
   if constexpr (IA < TH + 2) {
     const int ih = k.oh0 - 1 + IA;
-    if (ih >= 0 && ih < k.h) kc_row<TH, W, IA, 0>(acc, k.rowbits + (int64_t)IA * W * k.cwp, k);
+    if (ih >= 0 && ih < k.h) kc_row<TH, W, IA, 0>(acc, k);
     kc_rows<TH, W, IA + 1>(acc, k);
   }
+}
+
+// Chunk c's words of the tile's halo positions (rows oh0 - 1 .. oh0 + TH of
+// the frame; rows outside it read position 0 and are never walked).
+template <int TH, int W>
+__device__ __forceinline__ void kc_load_words(uint32_t& v0, uint32_t& v1, const uint32_t* __restrict__ fbits,
+                                              int oh0, int h, int cwp, int lane, int c) {
+  constexpr int NP = (TH + 2) * W;
+  const int p0 = lane, p1 = 64 + lane;
+  const int ih0 = oh0 - 1 + p0 / W, ih1 = oh0 - 1 + p1 / W;
+  const bool ok0 = p0 < NP && ih0 >= 0 && ih0 < h, ok1 = p1 < NP && ih1 >= 0 && ih1 < h;
+  const int64_t q0 = ok0 ? (int64_t)(oh0 - 1) * W + p0 : 0, q1 = ok1 ? (int64_t)(oh0 - 1) * W + p1 : 0;
+  v0 = fbits[q0 * cwp + c];
+  v1 = fbits[q1 * cwp + c];
 }
 
 template <int TH, int W>
@@ -318,6 +348,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
     k.x = static_cast<const char*>(x) + (int64_t)frame * a.c_in * a.hw_in * in_size;
     k.xrow = (int64_t)(oh0 - 1) * W;
     k.value = valid && rows_value_path(a, flags, frame, oh0 - 1, oh0 + TH);
+    // Chunk 0's halo words; chunk c+1's are requested while chunk c is walked.
+    const uint32_t* __restrict__ fbits = bits + (int64_t)frame * a.hw_in * a.cwp;
+    uint32_t nw0 = 0u, nw1 = 0u;
+    if (valid) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.cwp, lane, 0);
     if (!resident) {
       __syncthreads();  // the previous pass is done with both buffers
       load_chunk(smem, wt, 0, krows, a.c_out, co0, wave, lane);
@@ -330,7 +364,9 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
       if (!resident && c + 1 < nchunks)
         load_chunk(smem + ((c + 1) & 1) * kChunkBytes, wt, c + 1, krows, a.c_out, co0, wave, lane);
       if (valid) {
-        k.rowbits = bits + ((int64_t)frame * a.hw_in + (int64_t)(oh0 - 1) * W) * a.cwp + c;
+        k.vw0 = nw0;
+        k.vw1 = nw1;
+        if (c + 1 < nchunks) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.cwp, lane, c + 1);
         k.c0 = c * 32;
         k.wlb = smem + (c & 1) * kChunkBytes + lane * 4;
         kc_rows<TH, W, 0>(acc, k);
