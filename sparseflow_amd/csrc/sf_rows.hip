@@ -26,17 +26,33 @@ namespace sf {
 namespace {
 
 
-// Accumulate the spikes of input row ih (= oh - 1 + IA) into acc.
+// Word of halo position p (lane p & 63 of v0 for p < 64, else of v1) on the
+// scalar unit; p is a compile-time constant once the walks are unrolled.
+template <typename M>
+__device__ __forceinline__ M rl_word(M v0, M v1, int p) {
+  const M v = p < 64 ? v0 : v1;
+  if constexpr (sizeof(M) == 8) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, p & 63);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), p & 63);
+    return ((M)hi << 32) | lo;
+  } else {
+    return __builtin_amdgcn_readlane(v, p & 63);
+  }
+}
+
+// Accumulate the spikes of input row ih (= oh - 1 + IA) into acc; the
+// words of the three input rows were fetched with vector loads (v0, v1).
 template <int W, int QP, int CWP, int IA, bool VALUE, typename TIn>
-__device__ __forceinline__ void scatter_row(float (&acc)[4 * QP], const typename Word<CWP>::type* __restrict__ rp,
-                                            const char* wlb, const TIn* __restrict__ xrow, int hw_in) {
+__device__ __forceinline__ void scatter_row(float (&acc)[4 * QP], typename Word<CWP>::type v0,
+                                            typename Word<CWP>::type v1, const char* wlb,
+                                            const TIn* __restrict__ xrow, int hw_in) {
   typedef typename Word<CWP>::type M;
-  constexpr int CH = 8;  // positions per scalar-load batch
+  constexpr int CH = 8;  // positions per batch
 #pragma unroll
   for (int ib0 = 0; ib0 < W; ib0 += CH) {
     M mw[CH];
 #pragma unroll
-    for (int u = 0; u < CH; ++u) mw[u] = rp[ib0 + u];
+    for (int u = 0; u < CH; ++u) mw[u] = rl_word<M>(v0, v1, IA * W + ib0 + u);
 #pragma unroll
     for (int u = 0; u < CH; ++u) {
       const int ib = ib0 + u;
@@ -67,11 +83,22 @@ __device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArg
   typedef typename Word<CWP>::type M;
   const M* __restrict__ fb = bits + frame * (int64_t)a.hw_in;
   const TIn* __restrict__ xf = x + frame * (int64_t)a.c_in * a.hw_in;
+  // Words of the 3 x W halo positions (rows oh-1 .. oh+1), position p in lane
+  // p & 63 of v0 / v1: two vector loads instead of batches of dependent
+  // scalar loads; rows outside the frame are never walked.
+  const int lane = lane_id();
+  M v0 = 0, v1 = 0;
+  {
+    const int p0 = lane, p1 = 64 + lane;
+    const int ih0 = oh - 1 + p0 / W, ih1 = oh - 1 + p1 / W;
+    if (p0 < 3 * W && ih0 >= 0 && ih0 < a.h_in) v0 = fb[(int64_t)(oh - 1) * W + p0];
+    if (p1 < 3 * W && ih1 >= 0 && ih1 < a.h_in) v1 = fb[(int64_t)(oh - 1) * W + p1];
+  }
   if (oh >= 1)
-    scatter_row<W, QP, CWP, 0, VALUE, TIn>(acc, fb + (oh - 1) * W, wlb, xf + (oh - 1) * W, a.hw_in);
-  scatter_row<W, QP, CWP, 1, VALUE, TIn>(acc, fb + oh * W, wlb, xf + oh * W, a.hw_in);
+    scatter_row<W, QP, CWP, 0, VALUE, TIn>(acc, v0, v1, wlb, xf + (oh - 1) * W, a.hw_in);
+  scatter_row<W, QP, CWP, 1, VALUE, TIn>(acc, v0, v1, wlb, xf + oh * W, a.hw_in);
   if (oh + 1 < a.h_in)
-    scatter_row<W, QP, CWP, 2, VALUE, TIn>(acc, fb + (oh + 1) * W, wlb, xf + (oh + 1) * W, a.hw_in);
+    scatter_row<W, QP, CWP, 2, VALUE, TIn>(acc, v0, v1, wlb, xf + (oh + 1) * W, a.hw_in);
 }
 
 // OR of the non-binary chunk flags covering input rows oh-1 .. oh+1.
