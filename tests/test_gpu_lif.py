@@ -82,12 +82,15 @@ def test_fused_lif_v_init_and_single_step_chain():
     assert torch.equal(vs, v)
 
 
-def test_fused_lif_half_input():
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_lif_half_input(dtype):
+    # 12x12 planes and full 32-channel slices: the four-pixel vector spike
+    # stores in f16 / bf16.
     x = spikes((3, 2, 64, 12, 12), 0.05, seed=5)
     w = torch.randn(64, 64, 3, 3, generator=torch.Generator().manual_seed(4)) * 0.25
-    announce("lif fp16")
-    spk, v, _ = sparse_fused_conv_lif_multistep(x.to(DEV, torch.float16), w.to(DEV), None)
-    assert spk.dtype == torch.float16 and v.dtype == torch.float32
+    announce(f"lif {dtype}")
+    spk, v, _ = sparse_fused_conv_lif_multistep(x.to(DEV, dtype), w.to(DEV), None)
+    assert spk.dtype == dtype and v.dtype == torch.float32
     _check(spk.float(), v, x, w, None, 3, 2.0, 1.0, 0.0, True)
 
 
