@@ -98,8 +98,8 @@ def sparse_fused_conv_lif_multistep(
     wt = w_tap if w_tap is not None else _lib.tap_major_weight(weight)
     b = None if bias is None else bias.detach().to(torch.float32).contiguous()
     vi = None if v_init is None else v_init.detach().to(torch.float32).contiguous()
-    if vi is not None and tuple(vi.shape) != (N, C_OUT, H_OUT, W_OUT):
-        raise ValueError(f"v_init shape {tuple(vi.shape)} != {(N, C_OUT, H_OUT, W_OUT)}")
+    if vi is not None and (tuple(vi.shape) != (N, C_OUT, H_OUT, W_OUT) or vi.device != x.device):
+        raise ValueError(f"v_init shape {tuple(vi.shape)} on {vi.device} != {(N, C_OUT, H_OUT, W_OUT)} on {x.device}")
     code = _lib.dtype_code(x.dtype)
     desc = _lib.conv_desc(N, C, H, W, C_OUT, H_OUT, W_OUT, kernel_size, 1, padding, code, code)
     need = _lib.conv_lif_workspace_size(desc, T)
@@ -223,8 +223,11 @@ def sparse_conv1x1_lif_multistep(
         bits, flags = _lib.prescan_pack(x4, threshold)
     wt = w_tap if w_tap is not None else _lib.tap_major_weight(weight)
     b = None if bias is None else bias.detach().to(torch.float32).contiguous()
-    # V_0 = v_init, else 0 (as sparse_fused_conv_lif_multistep).
+    # V_0 = v_init, else 0 (as sparse_fused_conv_lif_multistep).  The C ABI
+    # takes a bare pointer, so a membrane of another shape is refused here.
     vi = None if v_init is None else v_init.detach().to(torch.float32).contiguous()
+    if vi is not None and (tuple(vi.shape) != (N, C_OUT, H, W) or vi.device != x.device):
+        raise ValueError(f"v_init shape {tuple(vi.shape)} on {vi.device} != {(N, C_OUT, H, W)} on {x.device}")
     spikes = torch.empty((T, N, C_OUT, H, W), dtype=x.dtype, device=x.device)
     v_out = torch.empty((N, C_OUT, H, W), dtype=torch.float32, device=x.device)
     out_bits = out_flags = None

@@ -63,13 +63,16 @@ class SpikingBottleneck(nn.Module):
         self.conv3_lif: Optional[nn.Module] = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.conv1_lif is not None:
+        # A fused pair is used only while it still wraps this block's conv: a
+        # dispatch pass that swapped the conv by name (for a static-zero one)
+        # makes the pair stale, and the unfused modules then run.
+        if self.conv1_lif is not None and self.conv1_lif.conv is self.conv1:
             out = self.conv1_lif(x)
         else:
             out = self.sn1(_seq(self.conv1, self.bn1, x))
         out = self.sn2(_seq(self.conv2, self.bn2, out))
         identity = x if self.downsample is None else _seq(self.downsample[0], self.downsample[1], x)
-        if self.conv3_lif is not None:
+        if self.conv3_lif is not None and self.conv3_lif.conv is self.conv3:
             return self.conv3_lif(out, identity)
         out = _seq(self.conv3, self.bn3, out)
         return self.sn3(out, identity)  # LIF(out + identity), the add fused into the neuron pass

@@ -16,8 +16,6 @@ carries it but never uses it, Ops/sparse_conv2d.py:114-119).
 from __future__ import annotations
 
 import math
-import time
-from dataclasses import dataclass
 from typing import Optional
 
 import torch
@@ -28,28 +26,8 @@ from .. import _lib
 from ..Kernels.conv2d import BACKEND_NAME, _select_tile_sizes, choose_group_size, sparse_conv2d_forward
 from ..Utils import config as _config
 from ..Utils.block_selector import select_block_size
+from ._runtime import DispatchAudit, FallbackPolicy, PathProfile, WeightLayout, bias_rows
 from .static_zero_conv2d import ZERO_BACKEND_FAMILY, make_zero_conv_output  # noqa: F401
-
-
-@dataclass
-class _ProfileStats:
-    calls: int = 0
-    zero_path_hits: int = 0
-    sparse_path_hits: int = 0
-    dense_path_hits: int = 0
-    triton_supported_calls: int = 0  # name kept for readers of the reference stats
-    total_ms: float = 0.0
-    policy_ms: float = 0.0
-    reshape_ms: float = 0.0
-    buffer_ms: float = 0.0
-    sparse_kernel_ms: float = 0.0
-    dense_fallback_ms: float = 0.0
-    output_pack_ms: float = 0.0
-    last_path: str = "none"
-    last_total_ms: float = 0.0
-    last_sparse_kernel_ms: float = 0.0
-    last_dense_fallback_ms: float = 0.0
-    last_avg_active_ratio: float = -1.0
 
 
 def _pair(v):
@@ -101,40 +79,26 @@ class SparseConv2d(nn.Module):
             bound = 1 / math.sqrt(fan_in) if fan_in > 0 else 0
             nn.init.uniform_(self.bias, -bound, bound)
 
-        self._w_tap = None
-        self._w_tap_key = None
+        self._w_tap = WeightLayout(_lib.tap_major_weight)
         self._workspace = None
         self._last_sparse_ms = 0.0
         self._last_dense_ms = 0.0
-        self._last_avg_active_ratio = -1.0
-        self._dense_threshold = float(dense_threshold)
-        self._warmup_left = int(max(0, warmup_steps))
-        self._calib_every = int(max(1, calib_every))
-        self._ema_decay = float(ema_decay)
-        self._zero_streak_needed = int(max(1, zero_streak_needed))
-        self._forward_count = 0
         self._inference_mode = False
-        # Runtime fallback policy (Ops/sparse_conv2d.py:449-496): an EMA of
-        # the active-group ratio forces dense above dense_threshold, a streak
-        # of all-zero inputs forces the zero output.  Off unless enabled in
-        # Utils.config or per module via `runtime_policy`, as in the reference.
-        self.runtime_policy = bool(_config.ENABLE_RUNTIME_FALLBACK_POLICY)
-        self._ema_active_ratio = None
-        self._zero_streak = 0
-        self._force_dense = False
-        self._force_zero = False
-        self._runtime_dispatch_seen = 0
-        self._runtime_dispatch_mismatch = 0
-
+        # Runtime fallback policy (dense above an averaged active ratio, the
+        # bias-only output after a run of all-zero inputs; sticky zero as in
+        # Ops/sparse_conv2d.py:449-496).  Off unless enabled in Utils.config
+        # or per module through `runtime_policy`.
+        self.policy = FallbackPolicy(_config.ENABLE_RUNTIME_FALLBACK_POLICY, warmup_steps, calib_every, ema_decay,
+                                     dense_threshold, zero_streak_needed, zero_sticky=True)
+        self._audit = DispatchAudit()
+        self._profile = PathProfile("SparseConv2d")
+        self._profile.enabled = bool(profile_runtime)
         self.collect_diag = False
         self._last_diag = {}
-        self.profile_runtime = bool(profile_runtime)
-        self._profile = _ProfileStats()
         self.backend_family = "sparse_kernel"
         self.diag_path = "conv2d_two_stage_hip"
         self.fallback_reason = ""
-        self.meta_source = "measured"
-        self.diag_source = "measured"
+        self.meta_source = self.diag_source = "measured"
         self.support_status = "supported"
         self.score_family = "conv"
         # "sparse" (library kernels) or "dense" (F.conv2d), set per layer by
@@ -154,30 +118,28 @@ class SparseConv2d(nn.Module):
             self.collect_diag = False
             self.profile_runtime = False
 
-    # ---- profiling ----------------------------------------------------------
-    def _stamp(self):
-        if self.profile_runtime and self.weight.is_cuda:
-            torch.cuda.synchronize(self.weight.device)
-        return time.perf_counter()
+    @property
+    def runtime_policy(self) -> bool:
+        return self.policy.enabled
 
-    def _elapsed_ms(self, t0):
-        if self.profile_runtime and self.weight.is_cuda:
-            torch.cuda.synchronize(self.weight.device)
-        return (time.perf_counter() - t0) * 1000.0
+    @runtime_policy.setter
+    def runtime_policy(self, on: bool) -> None:
+        self.policy.enabled = bool(on)
+
+    @property
+    def profile_runtime(self) -> bool:
+        return self._profile.enabled
+
+    @profile_runtime.setter
+    def profile_runtime(self, on: bool) -> None:
+        self._profile.enabled = bool(on)
+
+    @property
+    def _last_avg_active_ratio(self) -> float:
+        return self.policy.last_ratio
 
     def get_profile_summary(self):
-        p = self._profile
-        if p.calls == 0:
-            return "SparseConv2d runtime profile: no calls"
-        avg = lambda v: v / max(1, p.calls)  # noqa: E731
-        return (
-            "SparseConv2d runtime profile\n"
-            f"  calls={p.calls}, last_path={p.last_path}\n"
-            f"  hits: zero={p.zero_path_hits}, sparse={p.sparse_path_hits}, dense={p.dense_path_hits}\n"
-            f"  avg: total={avg(p.total_ms):.3f}, sparse_kernel={avg(p.sparse_kernel_ms):.3f}, "
-            f"dense_fallback={avg(p.dense_fallback_ms):.3f}\n"
-            f"  last: total={p.last_total_ms:.3f}, path={p.last_path}, active_ratio={p.last_avg_active_ratio:.4f}"
-        )
+        return self._profile.summary()
 
     # ---- helpers --------------------------------------------------------------
     def _supports_sparse(self) -> bool:
@@ -194,13 +156,8 @@ class SparseConv2d(nn.Module):
 
     def _get_w_tap(self):
         """fp32 tap-major weight [C_in*k*k, C_out], rebuilt when the weight
-        changes (the reference keys its fp16 cache on weight._version,
-        Ops/sparse_conv2d.py:339-350)."""
-        key = (self.weight._version, self.weight.data_ptr(), self.weight.device)
-        if self._w_tap is None or self._w_tap_key != key:
-            self._w_tap = _lib.tap_major_weight(self.weight)
-            self._w_tap_key = key
-        return self._w_tap
+        changes."""
+        return self._w_tap(self.weight)
 
     def _get_workspace(self, x4d):
         n, c, h, w = (int(v) for v in x4d.shape)
@@ -211,14 +168,11 @@ class SparseConv2d(nn.Module):
             self._workspace = ws
         return ws
 
-    def _zero_output_4d(self, x):
-        h_out, w_out = self._output_hw(int(x.shape[2]), int(x.shape[3]))
-        return make_zero_conv_output(int(x.shape[0]), self.out_channels, h_out, w_out, self.bias, x.device, x.dtype)
-
-    def _zero_output_5d(self, x):
-        T, B = int(x.shape[0]), int(x.shape[1])
-        y = self._zero_output_4d(x.reshape(T * B, *x.shape[2:]))
-        return y.reshape(T, B, *y.shape[1:])
+    def _zero_output(self, x):
+        """Bias-only output for x (4-D or 5-D): the exact result of an
+        all-zero input."""
+        h_out, w_out = self._output_hw(int(x.shape[-2]), int(x.shape[-1]))
+        return bias_rows(self.bias, tuple(x.shape[:-3]), self.out_channels, (h_out, w_out), x.dtype, x.device)
 
     @classmethod
     def from_dense(cls, conv: nn.Conv2d, block_size=None, threshold=1e-6, return_ms=False, **kwargs):
@@ -236,115 +190,46 @@ class SparseConv2d(nn.Module):
                 sparse.bias.copy_(conv.bias)
         return sparse
 
-    # ---- runtime policy (Ops/sparse_conv2d.py:323-334,449-496) ---------------------
-    def _should_collect_ratio(self) -> bool:
-        if not self.runtime_policy or self._inference_mode:
-            return False
-        if self._warmup_left > 0:
-            return True
-        return (self._forward_count % self._calib_every) == 0
-
-    def _update_policy(self, avg_active_ratio):
-        if avg_active_ratio is None:
-            return
-        self._last_avg_active_ratio = float(avg_active_ratio)
-        if not self.runtime_policy:
-            return
-        if self._warmup_left > 0:
-            self._warmup_left -= 1
-            self._ema_active_ratio = avg_active_ratio
-            return
-        if self._ema_active_ratio is None:
-            self._ema_active_ratio = avg_active_ratio
-        else:
-            self._ema_active_ratio = self._ema_decay * self._ema_active_ratio + (1 - self._ema_decay) * avg_active_ratio
-        self._zero_streak = self._zero_streak + 1 if avg_active_ratio == 0.0 else 0
-        if self._zero_streak >= self._zero_streak_needed:
-            self._force_zero = True
-        self._force_dense = self._ema_active_ratio > self._dense_threshold
-
-    def _record_runtime_dispatch(self, runtime_backend: str):
-        """Count forwards whose path differs from the dispatch decision
-        stamped on the module (sf_dispatch_decision / sf_backend_mode)."""
-        expected = str(getattr(self, "sf_dispatch_decision", getattr(self, "sf_backend_mode", ""))).strip().lower()
-        if not expected:
-            return
-        self._runtime_dispatch_seen += 1
-        if expected != runtime_backend:
-            self._runtime_dispatch_mismatch += 1
-
     # ---- forward ----------------------------------------------------------------
     def forward(self, x: torch.Tensor):
-        self.fallback_reason = ""
-        if self.profile_runtime:
-            self._profile.calls += 1
-            t_total = self._stamp()
         if x.dim() not in (4, 5):
             raise ValueError(f"Expected 4D or 5D input, got {x.dim()}D")
-        if self.runtime_policy and self._force_zero:
-            y = self._zero_output_5d(x) if x.dim() == 5 else self._zero_output_4d(x)
+        t0 = self._profile.start(x.device)
+        self.fallback_reason = ""
+        forced = self.policy.forced
+        if forced == FallbackPolicy.ZERO:
+            y = self._zero_output(x)
             self._last_sparse_ms = 0.0
             self.fallback_reason = "force_zero"
-            self._record_runtime_dispatch("staticzero")
-            if self.profile_runtime:
-                self._profile.zero_path_hits += 1
-                self._profile.last_path = "zero(force)"
-                ms = self._elapsed_ms(t_total)
-                self._profile.total_ms += ms
-                self._profile.last_total_ms = ms
+            self._audit.record(self, "staticzero")
+            self._profile.finish("zero(force)", self._profile.elapsed(t0, x.device), self.policy.last_ratio)
             return y
-        if x.dim() == 5:
-            T, B = int(x.shape[0]), int(x.shape[1])
-            x4d = x.reshape(T * B, *x.shape[2:])
-        elif x.dim() == 4:
-            x4d = x
-        else:
-            raise ValueError(f"Expected 4D or 5D input, got {x.dim()}D")
-
-        forced_dense = self.runtime_policy and self._force_dense
-        need_ratio = x4d.is_cuda and not forced_dense and self._should_collect_ratio()
-        self._forward_count += 1
-
+        x4d = x.reshape(-1, *x.shape[-3:]) if x.dim() == 5 else x
         ratio = None
-        if x4d.is_cuda and self._supports_sparse() and self.backend_mode != "dense" and not forced_dense:
-            y4d, backend, ratio = self._hip_forward(x4d, need_ratio)
+        if x4d.is_cuda and self._supports_sparse() and self.backend_mode != "dense" and forced is None:
+            y4d, backend, ratio = self._hip_forward(x4d, self.policy.wants_ratio(self._inference_mode))
             path = {"dense_fallback": "dense(fallback)", "zero_tiles_only": "zero(tile_compaction)"}.get(
                 backend, "sparse")
-            self._record_runtime_dispatch({"dense_fallback": "dense", "zero_tiles_only": "staticzero"}.get(
+            self._audit.record(self, {"dense_fallback": "dense", "zero_tiles_only": "staticzero"}.get(
                 backend, "sparse"))
-            if self.profile_runtime:
-                if path == "sparse":
-                    self._profile.sparse_path_hits += 1
-                elif path.startswith("zero"):
-                    self._profile.zero_path_hits += 1
-                else:
-                    self._profile.dense_path_hits += 1
         else:
             y4d = self._fallback_forward(x4d)
             path = "dense"
-            self.fallback_reason = ("force_dense" if forced_dense else
+            self.fallback_reason = ("force_dense" if forced == FallbackPolicy.DENSE else
                                     "dispatch_dense" if self.backend_mode == "dense" else "module_dense_path")
-            self._record_runtime_dispatch("dense")
-            if self.profile_runtime:
-                self._profile.dense_path_hits += 1
-
-        self._update_policy(ratio)
-        if self.runtime_policy and self._force_zero and ratio == 0.0:
-            y4d = self._zero_output_4d(x4d)
-            path = "zero(promoted)"
-            self.fallback_reason = "zero_promoted"
-
-        y = y4d.reshape(T, B, *y4d.shape[1:]) if x.dim() == 5 else y4d
-        if self.profile_runtime:
-            self._profile.last_path = path
-            self._profile.last_avg_active_ratio = self._last_avg_active_ratio
-            ms = self._elapsed_ms(t_total)
-            self._profile.total_ms += ms
-            self._profile.last_total_ms = ms
+            self._audit.record(self, "dense")
+        self.policy.forwards += 1
+        self.policy.observe(ratio)
+        if ratio == 0.0 and self.policy.forced == FallbackPolicy.ZERO:
+            # This forward's input was already all-zero, so its output is the
+            # bias-only output the zero path would give.
+            path, self.fallback_reason = "zero(promoted)", "zero_promoted"
+        y = y4d.reshape(*x.shape[:2], *y4d.shape[1:]) if x.dim() == 5 else y4d
+        self._profile.finish(path, self._profile.elapsed(t0, x.device), self.policy.last_ratio)
         if self.collect_diag:
-            self._last_diag["runtime_dispatch_seen"] = int(self._runtime_dispatch_seen)
-            self._last_diag["runtime_dispatch_mismatch"] = int(self._runtime_dispatch_mismatch)
-            self._last_diag["fallback_reason"] = str(self.fallback_reason)
+            self._last_diag.update(runtime_dispatch_seen=self._audit.seen,
+                                   runtime_dispatch_mismatch=self._audit.mismatch,
+                                   fallback_reason=str(self.fallback_reason))
         return y
 
     def _hip_forward(self, x4d, need_ratio=False):
@@ -377,9 +262,7 @@ class SparseConv2d(nn.Module):
             self._last_sparse_ms, self._last_dense_ms = 0.0, float(ms)
         else:
             self._last_sparse_ms, self._last_dense_ms = float(ms), 0.0
-        if self.profile_runtime:
-            self._profile.sparse_kernel_ms += self._last_sparse_ms
-            self._profile.last_sparse_kernel_ms = self._last_sparse_ms
+        self._profile.add("sparse_kernel", self._last_sparse_ms)
         if want_diag:
             self._collect_diag(x4d, ms, ratio, stats, meta)
         return y, backend, ratio
@@ -429,14 +312,11 @@ class SparseConv2d(nn.Module):
         self._last_diag = diag
 
     def _fallback_forward(self, x):
-        if self.profile_runtime:
-            t0 = self._stamp()
+        t0 = self._profile.start(x.device)
         y = F.conv2d(x, self.weight, self.bias, self.stride, self.padding, self.dilation, self.groups)
         self._last_sparse_ms = 0.0
-        self._last_dense_ms = self._elapsed_ms(t0) if self.profile_runtime else 0.0
-        if self.profile_runtime:
-            self._profile.dense_fallback_ms += self._last_dense_ms
-            self._profile.last_dense_fallback_ms = self._last_dense_ms
+        self._last_dense_ms = self._profile.elapsed(t0, x.device)
+        self._profile.add("dense_fallback", self._last_dense_ms)
         return y
 
     def extra_repr(self):

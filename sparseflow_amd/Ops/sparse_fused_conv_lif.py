@@ -214,21 +214,31 @@ class SparseConv1x1LIF(nn.Module):
                 and conv.stride == (1, 1) and conv.padding == (0, 0) and conv.groups == 1
                 and conv.out_channels % 4 == 0 and lif.step_mode == "m")
 
+    def runs_fused(self, x: torch.Tensor) -> bool:
+        """The fused kernel runs for [T, N, C, H, W] device tensors of a
+        supported dtype, unless a dispatch decision put the conv on the
+        dense path (then conv and neuron run one after the other, so the
+        decision is honoured)."""
+        return (x.dim() == 5 and x.is_cuda and x.dtype in (torch.float32, torch.float16, torch.bfloat16)
+                and getattr(self.conv, "backend_mode", "sparse") != "dense")
+
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         from ..Kernels.fused_conv_lif import sparse_conv1x1_lif_multistep
 
-        if x.dim() != 5 or not x.is_cuda or x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        if not self.runs_fused(x):
             T, N = x.shape[0], x.shape[1]
             y = self.conv(x.flatten(0, 1))
             y = y.reshape(T, N, *y.shape[1:])
             return self.lif(y, residual) if residual is not None else self.lif(y)
         lif = self.lif
-        v0 = lif.v if (lif.v is not None and lif.v.dim() == 4 and lif.v.device == x.device) else None
+        N = int(x.shape[1])
+        state = (N, self.conv.out_channels, int(x.shape[3]), int(x.shape[4]))
+        # The neuron's membrane carries over only at the same shape and device;
+        # otherwise it starts afresh, as LIFNode itself does on a new shape.
+        v0 = lif.v if (lif.v is not None and tuple(lif.v.shape) == state and lif.v.device == x.device) else None
         if v0 is None and lif.v_reset is not None and float(lif.v_reset) != 0.0:
             # A fresh LIFNode starts at v_reset (hard reset), not 0.
-            T, N = x.shape[0], x.shape[1]
-            v0 = torch.full((N, self.conv.out_channels, x.shape[3], x.shape[4]), float(lif.v_reset),
-                            dtype=torch.float32, device=x.device)
+            v0 = torch.full(state, float(lif.v_reset), dtype=torch.float32, device=x.device)
         spikes, lif.v = sparse_conv1x1_lif_multistep(
             x, self.conv.weight, self.conv.bias, tau=lif.tau, v_threshold=lif.v_threshold, v_reset=lif.v_reset,
             decay_input=lif.decay_input, residual=residual, threshold=self.conv.threshold, v_init=v0,

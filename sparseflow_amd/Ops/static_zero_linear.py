@@ -1,46 +1,47 @@
-"""StaticZeroLinear: exact-zero Linear backend (drop-in for
-Ops/static_zero_linear.py).  For an all-zero input a Linear is
-y = bias (or 0), so the output is the bias broadcast over the input's
-leading dimensions, with no read of the input values."""
+"""StaticZeroLinear: the exact-zero Linear backend (drop-in for
+Ops/static_zero_linear.py).
+
+A layer that dispatch found to receive only all-zero input computes
+y = x @ W^T + b = b, so this module never reads the input values: it returns
+the bias repeated over the input's leading dimensions (zeros without a bias)
+in the input's dtype.  Inputs of rank < 2 are refused, as in the reference.
+"""
 
 from __future__ import annotations
 
-from typing import Any, Dict, Optional
+from typing import Optional
 
 import torch
 import torch.nn as nn
 
+from ._runtime import bias_rows
+
 
 class StaticZeroLinear(nn.Module):
+    backend_family = "exact_zero"
+    diag_path = "staticzero_linear"
+
     def __init__(self, out_features: int, bias: Optional[torch.Tensor] = None):
         super().__init__()
         self.out_features = int(out_features)
-        if bias is not None:
-            self.register_buffer("bias_buf", bias.detach().float().clone())
-        else:
-            self.bias_buf = None
-        self._forward_count = 0
-        self.backend_family = "exact_zero"
-        self.diag_path = "staticzero_linear"
+        self.register_buffer("bias_buf", None if bias is None else bias.detach().float().clone())
         self.fallback_reason = ""
+        self.calls = 0
 
     @classmethod
     def from_linear(cls, linear: nn.Linear) -> "StaticZeroLinear":
-        return cls(out_features=linear.out_features, bias=linear.bias).to(linear.weight.device)
+        return cls(linear.out_features, linear.bias).to(linear.weight.device)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.dim() < 2:
-            raise ValueError(f"StaticZeroLinear expects dim>=2 input, got {x.dim()}D")
-        self._forward_count += 1
-        shape = (*x.shape[:-1], self.out_features)
-        if self.bias_buf is None:
-            return torch.zeros(shape, dtype=x.dtype, device=x.device)
-        return self.bias_buf.to(device=x.device, dtype=x.dtype).expand(shape).clone()
+            raise ValueError(f"StaticZeroLinear takes [..., in_features] input of rank >= 2, not {tuple(x.shape)}")
+        self.calls += 1
+        return bias_rows(self.bias_buf, tuple(x.shape[:-1]), self.out_features, (), x.dtype, x.device)
 
-    def get_diag(self) -> Dict[str, Any]:
-        return {"backend_family": self.backend_family, "zero_reason": "static_zero_input_linear",
-                "diag_path": self.diag_path, "has_bias": self.bias_buf is not None,
-                "out_features": self.out_features, "forward_count": self._forward_count}
+    def get_diag(self) -> dict:
+        return dict(backend_family=self.backend_family, diag_path=self.diag_path,
+                    zero_reason="static_zero_input_linear", out_features=self.out_features,
+                    has_bias=self.bias_buf is not None, forward_count=self.calls)
 
     def extra_repr(self) -> str:
-        return f"out_features={self.out_features}, has_bias={self.bias_buf is not None}"
+        return f"out_features={self.out_features}, bias={'yes' if self.bias_buf is not None else 'no'}, exact_zero"

@@ -108,33 +108,50 @@ def test_dispatch_all_layers_accepts_targets():
 
 
 def test_runtime_policy_state_machine():
-    # Ops/sparse_conv2d.py:462-496: warmup seeds the EMA, a zero streak
-    # forces the zero path, an EMA above the dense threshold forces dense.
+    # Ops/sparse_conv2d.py:462-496: warmup seeds the average, a zero streak
+    # forces the zero path (sticky for the conv), an average above the dense
+    # threshold forces dense.
     m = SparseConv2d(8, 8, 3, 1, 1, warmup_steps=2, zero_streak_needed=2, ema_decay=0.5, dense_threshold=0.85)
     m.runtime_policy = True
-    assert m._should_collect_ratio()
-    m._update_policy(0.9)
-    m._update_policy(0.9)
-    assert m._warmup_left == 0 and not m._force_dense
-    m._update_policy(0.9)
-    assert m._force_dense and abs(m._ema_active_ratio - 0.9) < 1e-12
-    m._update_policy(0.0)            # EMA 0.45 -> not dense; streak 1
-    assert not m._force_dense and not m._force_zero
-    m._update_policy(0.0)
-    assert m._force_zero
-    m._forward_count = 31
-    assert not m._should_collect_ratio()
-    m._forward_count = 32
-    assert m._should_collect_ratio()
+    pol = m.policy
+    assert pol.wants_ratio(False) and not pol.wants_ratio(True)
+    pol.observe(0.9)
+    pol.observe(0.9)
+    assert pol.warmup_left == 0 and pol.forced is None
+    pol.observe(0.9)
+    assert pol.forced == "dense" and abs(pol.average - 0.9) < 1e-12
+    pol.observe(0.0)            # average 0.45 -> not dense; streak 1
+    assert pol.forced is None
+    pol.observe(0.0)
+    assert pol.forced == "zero"
+    pol.observe(0.5)            # sticky for the conv module
+    assert pol.forced == "zero"
+    pol.forwards = 31
+    assert not pol.wants_ratio(False)
+    pol.forwards = 32
+    assert pol.wants_ratio(False)
     off = SparseConv2d(8, 8, 3, 1, 1)
-    assert not off.runtime_policy and not off._should_collect_ratio()
-    off._update_policy(0.0)
-    assert off._last_avg_active_ratio == 0.0 and not off._force_zero
+    assert not off.runtime_policy and not off.policy.wants_ratio(False)
+    off.policy.observe(0.0)
+    assert off._last_avg_active_ratio == 0.0 and off.policy.forced is None
+
+
+def test_runtime_policy_linear_zero_choice_clears():
+    # The Linear module's zero choice lasts only while inputs stay all-zero
+    # (Ops/sparse_linear.py:397-405).
+    from sparseflow_amd.Ops.sparse_linear import SparseLinear
+
+    m = SparseLinear(8, 8, warmup_steps=0, zero_streak_needed=1, ema_decay=0.5)
+    m.runtime_policy = True
+    m.policy.observe(0.0)
+    assert m.policy.forced == "zero"
+    m.policy.observe(0.2)
+    assert m.policy.forced is None
 
 
 def test_runtime_policy_force_zero_output_on_cpu():
     m = SparseConv2d(4, 6, 3, 1, 1, bias=True)
-    m.runtime_policy, m._force_zero = True, True
+    m.runtime_policy, m.policy.choice = True, "zero"
     x = torch.randn(2, 3, 4, 5, 5)
     y = m(x)
     assert y.shape == (2, 3, 6, 5, 5) and m.fallback_reason == "force_zero"

@@ -198,3 +198,69 @@ def test_conv1x1_lif_binary_residual_from_its_spike_map(monkeypatch):
     assert torch.equal(s_b, s_v) and torch.equal(v_b, v_v)
     s_ref, v_ref, h_ref = _ref(x, w2, b2, res.cpu(), 2.0, 1.0, 0.0, True)
     _check(s_b, v_b, s_ref, v_ref, h_ref, 1.0)
+
+
+def _fused_pair(C, Co, v_reset, seed):
+    from sparseflow_amd.neuron import LIFNode
+    from sparseflow_amd.Ops.sparse_conv2d import SparseConv2d
+    from sparseflow_amd.Ops.sparse_fused_conv_lif import SparseConv1x1LIF
+
+    g = torch.Generator().manual_seed(seed)
+    conv = torch.nn.Conv2d(C, Co, 1, bias=True)
+    with torch.no_grad():
+        conv.weight.copy_(torch.randn(Co, C, 1, 1, generator=g) * 0.7)
+        conv.bias.copy_(torch.randn(Co, generator=g) * 0.1)
+    sc = SparseConv2d.from_dense(conv).to(DEV)
+    lif = LIFNode(step_mode="m", v_reset=v_reset)
+    return SparseConv1x1LIF(sc, lif), sc, LIFNode(step_mode="m", v_reset=v_reset)
+
+
+@pytest.mark.parametrize("v_reset", [0.0, -0.3])
+def test_conv1x1_lif_module_batch_change_without_reset(v_reset):
+    # Batch 2 then batch 4 with no reset_net in between: the fused module must
+    # start the second call from a fresh membrane (as the unfused LIFNode
+    # does on a new shape), not read the batch-2 membrane past its end.
+    T, C, Co, H, W = 3, 64, 64, 8, 8
+    announce(f"conv1x1 lif module batch 2 -> 4, v_reset={v_reset}")
+    fused, conv, lif_ref = _fused_pair(C, Co, v_reset, seed=31)
+    for N, seed in ((2, 32), (4, 33), (4, 34)):
+        x = spikes((T, N, C, H, W), 0.2, seed=seed).to(DEV)
+        spike_map.clear()
+        s_f = fused(x)
+        y = conv(x.flatten(0, 1)).reshape(T, N, Co, H, W)
+        s_u = lif_ref(y)
+        torch.cuda.synchronize()
+        assert tuple(fused.lif.v.shape) == (N, Co, H, W)
+        mism = float((s_f != s_u).float().mean())
+        assert mism < 1e-3, f"N={N}: {mism} of spikes differ from the unfused pair"
+        assert torch.allclose(fused.lif.v, lif_ref.v, atol=1e-4, rtol=1e-4)
+        assert 0.0 < float(s_f.mean()) < 1.0
+
+
+def test_conv1x1_lif_rejects_mismatched_v_init():
+    T, N, C, H, W, Co = 2, 2, 32, 6, 6, 32
+    x = spikes((T, N, C, H, W), 0.2, seed=41).to(DEV)
+    w = torch.randn(Co, C, 1, 1).to(DEV)
+    with pytest.raises(ValueError):
+        sparse_conv1x1_lif_multistep(x, w, None, v_init=torch.zeros(N - 1, Co, H, W, device=DEV))
+    with pytest.raises(ValueError):
+        sparse_conv1x1_lif_multistep(x, w, None, v_init=torch.zeros(N, Co, H + 1, W, device=DEV))
+
+
+def test_conv1x1_lif_module_honours_dense_dispatch():
+    # A dispatch decision that puts the conv on the dense path runs the conv
+    # and the neuron one after the other: no fused launch.
+    T, N, C, Co, H, W = 2, 2, 64, 64, 8, 8
+    announce("conv1x1 lif module with a dense dispatch decision")
+    fused, conv, lif_ref = _fused_pair(C, Co, 0.0, seed=51)
+    conv.backend_mode = "dense"
+    x = spikes((T, N, C, H, W), 0.2, seed=52).to(DEV)
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    s_f = fused(x)
+    torch.cuda.synchronize()
+    stats = _lib.timing_collect()
+    _lib.timing_enable(False)
+    assert stats.get("conv_lif_flat", (0,))[0] == 0
+    s_u = lif_ref(conv(x.flatten(0, 1)).reshape(T, N, Co, H, W))
+    assert torch.equal(s_f, s_u)

@@ -93,7 +93,7 @@ def test_runtime_policy_on_device():
     x0 = torch.zeros(4, 32, 16, 16, device=DEV)
     for _ in range(3):
         y = z(x0)
-    assert z._last_avg_active_ratio == 0.0 and z._force_zero
+    assert z._last_avg_active_ratio == 0.0 and z.policy.forced == "zero"
     xs = (torch.rand(4, 32, 16, 16, generator=torch.Generator().manual_seed(5)) < 0.05).float().to(DEV)
     y = z(xs)  # sticky, as the reference's policy
     assert z.fallback_reason == "force_zero"
@@ -104,7 +104,7 @@ def test_runtime_policy_on_device():
     x1 = torch.ones(4, 32, 16, 16, device=DEV)
     d(x1)
     d(x1)
-    assert d._last_avg_active_ratio == 1.0 and d._force_dense
+    assert d._last_avg_active_ratio == 1.0 and d.policy.forced == "dense"
     y = d(xs)
     assert d.fallback_reason == "force_dense"
     assert torch.allclose(y, conv(xs), atol=1e-4, rtol=1e-4)

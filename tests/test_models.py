@@ -59,3 +59,34 @@ def test_optimized_model_same_logits_on_cpu():
         sf.optimize(m, sample_input=x, verbose=False)
         out = m(x)
     assert torch.equal(out, ref)
+
+
+def test_fused_pairs_follow_dispatch_swaps_and_dense_decisions():
+    # fuse_conv_lif_ builds SparseConv1x1LIF pairs; a later dispatch pass that
+    # swaps a block's conv by name makes its pair stale (the block then runs
+    # the unfused modules), and a dense decision on the pair's conv turns the
+    # fused kernel off.
+    from types import SimpleNamespace
+
+    from sparseflow_amd.Models import fuse_conv_lif_
+    from sparseflow_amd.Models.spiking_resnet import SpikingBottleneck
+    from sparseflow_amd.Ops.static_zero_conv2d import StaticZeroConv2d
+
+    m = fold_bn_(_model(seed=5))
+    x = torch.randn(1, 3, 64, 64, generator=torch.Generator().manual_seed(6))
+    with torch.no_grad():
+        sf.optimize(m, sample_input=x, verbose=False)
+        assert fuse_conv_lif_(m) >= 8
+        blk = next(b for b in m.modules() if isinstance(b, SpikingBottleneck) and b.conv1_lif is not None)
+        pair = blk.conv1_lif
+        calls = []
+        pair.register_forward_hook(lambda *a: calls.append(1))
+        blk.conv1 = StaticZeroConv2d.from_conv(blk.conv1)
+        from sparseflow_amd.neuron import reset_net
+        reset_net(m)
+        m(x)
+        assert calls == []          # stale pair not used
+    cuda_like = SimpleNamespace(dim=lambda: 5, is_cuda=True, dtype=torch.float32)
+    assert pair.runs_fused(cuda_like)
+    pair.conv.backend_mode = "dense"
+    assert not pair.runs_fused(cuda_like)

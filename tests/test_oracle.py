@@ -207,6 +207,88 @@ def test_lif_hard_and_soft_reset_and_no_decay():
     np.testing.assert_allclose(H[:, 0], [0.5, 0.75])
 
 
+# Hand-derived trajectories in which the post-reset membrane decides the next
+# step (tau = 2, V_0 = 0 unless given).  Each row: (kwargs, I sequence,
+# expected spikes, expected H, expected V_T).
+#   hard, v_reset=-0.2: H1 = (3 - (0 + 0.2)) / 2 = 1.4 -> spike, V1 = -0.2;
+#                       H2 = -0.2 + (0 - 0) / 2 = -0.2, V_T = -0.2
+#   soft:               H1 = 3 / 2 = 1.5 -> spike, V1 = 0.5;
+#                       H2 = 0.5 + (0 - 0.5) / 2 = 0.25, V_T = 0.25
+#   hard, no decay_input, v_reset=0.1:
+#                       H1 = 0 - (0 - 0.1) / 2 + 1.2 = 1.25 -> spike, V1 = 0.1;
+#                       H2 = 0.1 - 0 + 0.3 = 0.4, V_T = 0.4
+#   soft, no decay_input: H1 = 1.5 -> spike, V1 = 0.5;
+#                       H2 = 0.5 - 0.25 + 0.2 = 0.45, V_T = 0.45
+#   hard, v_reset=0, V_0 = 0.6: H1 = 0.6 + (1.6 - 0.6) / 2 = 1.1 -> spike,
+#                       V1 = 0; H2 = 0 + (1.0 - 0) / 2 = 0.5, V_T = 0.5
+#   hard, v_reset=0.5, two spikes: H1 = (4 - (0 - 0.5)) / 2 = 2.25, V1 = 0.5;
+#                       H2 = 0.5 + (2 - 0) / 2 = 1.5, V2 = 0.5;
+#                       H3 = 0.5 + (0 - 0) / 2 = 0.5, V_T = 0.5
+LIF_RESET_CASES = [
+    (dict(v_reset=-0.2), [3.0, 0.0], [True, False], [1.4, -0.2], -0.2, None),
+    (dict(v_reset=None), [3.0, 0.0], [True, False], [1.5, 0.25], 0.25, None),
+    (dict(v_reset=0.1, decay_input=False), [1.2, 0.3], [True, False], [1.25, 0.4], 0.4, None),
+    (dict(v_reset=None, decay_input=False), [1.5, 0.2], [True, False], [1.5, 0.45], 0.45, None),
+    (dict(v_reset=0.0), [1.6, 1.0], [True, False], [1.1, 0.5], 0.5, 0.6),
+    (dict(v_reset=0.5), [4.0, 2.0, 0.0], [True, True, False], [2.25, 1.5, 0.5], 0.5, None),
+]
+
+
+def _lif_case_failures(step_fn):
+    """Run every reset case through a multistep loop over `step_fn` (the
+    oracle's lif_step or a planted mistake); return the failing cases."""
+    failures = []
+    for kw, I, s_exp, h_exp, v_exp, v0 in LIF_RESET_CASES:
+        V = np.full((1,), 0.0 if v0 is None else v0, np.float64)
+        S_all, H_all = [], []
+        for i in I:
+            S, V, H = step_fn(np.array([i]), V, 2.0, 1.0, kw["v_reset"], kw.get("decay_input", True), np.float64)
+            S_all.append(bool(S[0]))
+            H_all.append(float(H[0]))
+        if S_all != s_exp or not np.allclose(H_all, h_exp, rtol=0, atol=1e-12) or abs(V[0] - v_exp) > 1e-12:
+            failures.append((kw, I))
+    return failures
+
+
+def test_lif_reset_trajectories_closed_form():
+    assert _lif_case_failures(olif.lif_step) == []
+    for kw, I, s_exp, h_exp, v_exp, v0 in LIF_RESET_CASES:
+        v0a = None if v0 is None else np.array([v0])
+        spk, V, H = olif.lif_multistep(np.array(I)[:, None], tau=2.0, v_th=1.0, v_reset=kw["v_reset"],
+                                       decay_input=kw.get("decay_input", True), v0=v0a, dtype=np.float64)
+        assert spk[:, 0].tolist() == s_exp
+        np.testing.assert_allclose(H[:, 0], h_exp, rtol=0, atol=1e-12)
+        assert abs(float(V[0]) - v_exp) <= 1e-12
+
+
+def _mutant(kind):
+    """lif_step with one planted reset mistake (CPU only)."""
+    def step(I, V, tau, v_th, v_reset, decay_input=True, dtype=np.float64):
+        I = np.asarray(I, dtype=dtype)
+        V = np.asarray(V, dtype=dtype)
+        vr = 0.0 if v_reset is None else v_reset
+        H = V + (I - (V - vr)) / tau if decay_input else (V - (V - vr) / tau) + I
+        S = H >= v_th
+        if kind == "hard_reset_to_zero":
+            Vn = H - S * v_th if v_reset is None else np.where(S, 0.0, H)
+        elif kind == "no_hard_reset":
+            Vn = H - S * v_th if v_reset is None else H
+        elif kind == "always_soft_reset":
+            Vn = H - S * v_th
+        elif kind == "soft_reset_to_zero":
+            Vn = np.where(S, 0.0, H)
+        else:
+            raise ValueError(kind)
+        return S, Vn.astype(dtype), H
+    return step
+
+
+@pytest.mark.parametrize("kind", ["hard_reset_to_zero", "no_hard_reset", "always_soft_reset",
+                                  "soft_reset_to_zero"])
+def test_lif_reset_cases_catch_planted_mistakes(kind):
+    assert _lif_case_failures(_mutant(kind)), f"mutation {kind} passes the closed-form reset cases"
+
+
 def test_compare_spikes_tie_rule():
     ref = np.array([[True], [False]])
     H = np.array([[1.0 + 1e-7], [0.2]])
