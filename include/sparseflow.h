@@ -151,6 +151,25 @@ int sf_conv2d_forward(const sf_conv_desc* desc, const void* x, const float* wt,
                       const float* bias, float threshold, void* workspace,
                       size_t workspace_bytes, void* y, void* stream);
 
+/* Bytes of the library-owned scratch area behind sf_conv2d_forward_noalloc
+ * (one per GPU, held from the library's load on that GPU to process exit). */
+#define SF_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* sf_conv2d_forward without a workspace argument: the bitmap and flags live
+ * in the library's scratch area, so the call allocates nothing (no hipMalloc,
+ * no allocating library routine).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  Limit:
+ * sf_conv2d_workspace_size(desc) <= SF_NOALLOC_SCRATCH_BYTES, else
+ * SF_ERR_WORKSPACE before any launch (e.g. 512 frames of 64 x 56 x 56 need
+ * 12.9 MB).  Every call on one GPU uses that GPU's single scratch area:
+ * calls that overlap on one GPU (several streams or host threads) race;
+ * calls ordered on one stream do not.  Results equal sf_conv2d_forward's bit
+ * for bit (same kernels). */
+int sf_conv2d_forward_noalloc(const sf_conv_desc* desc, const void* x,
+                              const float* wt, const float* bias,
+                              float threshold, void* y, void* stream);
+
 /* Fused sparse conv + multi-step LIF.  x is [T, N, c_in, h, w] (desc->n = N),
  * spikes [T, N, c_out, h_out, w_out] in desc->out_dtype, v_out [N, c_out,
  * h_out, w_out] f32 = membrane after step T.  v_init (f32, same shape as

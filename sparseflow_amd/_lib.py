@@ -49,6 +49,7 @@ EXPORTS = {
     ),
     "sf_conv2d_sparse": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_conv2d_forward": (c_int, [_P, _P, _P, _P, c_float, _P, c_size_t, _P, _P]),
+    "sf_conv2d_forward_noalloc": (c_int, [_P, _P, _P, _P, c_float, _P, _P]),
     "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
     "sf_conv1x1_lif_sparse": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_conv1x1_lif_sparse_binres": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
@@ -270,6 +271,19 @@ def conv2d_forward(desc: ConvDesc, x: torch.Tensor, wt: torch.Tensor, bias: Opti
                                  _ptr(workspace), workspace.numel() * workspace.element_size(),
                                  _ptr(y), _stream(x.device))
     _check(rc, "sf_conv2d_forward")
+    return y
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20  # SF_NOALLOC_SCRATCH_BYTES
+
+
+def conv2d_forward_noalloc(desc: ConvDesc, x: torch.Tensor, wt: torch.Tensor, bias: Optional[torch.Tensor],
+                           threshold: float, y: torch.Tensor) -> torch.Tensor:
+    """sf_conv2d_forward with the bitmap in the library's per-GPU scratch
+    area: nothing is allocated (calls overlapping on one GPU race)."""
+    rc = lib().sf_conv2d_forward_noalloc(ctypes.byref(desc), _ptr(x), _ptr(wt), _ptr(bias), float(threshold),
+                                         _ptr(y), _stream(x.device))
+    _check(rc, "sf_conv2d_forward_noalloc")
     return y
 
 

@@ -614,6 +614,65 @@ int sf_conv2d_forward(const sf_conv_desc* d, const void* x, const float* wt, con
   return sf_conv2d_sparse(d, ws.bits, ws.flags, x, wt, bias, y, stream);
 }
 
+}  // extern "C"
+
+// ---- no-allocation variant of sf_conv2d_forward -------------------------------
+// The bitmap and flags of sf_conv2d_forward_noalloc live in `scratch`, a fixed
+// array of the library's device image: each GPU the library runs on holds its
+// own copy (allocated when the code object is loaded there) until the process
+// ends.  In host code the symbol is only a stand-in: its device address is
+// looked up once per GPU with hipGetSymbolAddress (with that GPU current) and
+// only that address reaches a kernel.  k_pack writes every bitmap word and
+// every flag of the frames it covers, so the previous call's contents need no
+// clearing.
+static __device__ __align__(256) uint32_t scratch[SF_NOALLOC_SCRATCH_BYTES / 4];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail((int)e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(SF_ERR_UNSUPPORTED, "device index out of range for the scratch table");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail((int)e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(SF_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sf_conv2d_forward_noalloc(const sf_conv_desc* d, const void* x, const float* wt, const float* bias,
+                              float threshold, void* y, void* stream) {
+  int rc = check_desc(d);
+  if (rc != SF_OK) return rc;
+  if (d->n == 0) return SF_OK;
+  if (x == nullptr || wt == nullptr || y == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  const size_t need = sf_conv2d_workspace_size(d);
+  if (need > (size_t)SF_NOALLOC_SCRATCH_BYTES)
+    return fail(SF_ERR_WORKSPACE, "sf_conv2d_forward_noalloc: the bitmap of these frames needs " +
+                                      std::to_string(need) + " bytes; the library scratch holds " +
+                                      std::to_string((size_t)SF_NOALLOC_SCRATCH_BYTES) +
+                                      " per GPU (split the frames over several calls, or pass a workspace to "
+                                      "sf_conv2d_forward)");
+  void* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc != SF_OK) return rc;
+  return sf_conv2d_forward(d, x, wt, bias, threshold, ws, need, y, stream);
+}
+
 int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const float* wt, const float* bias,
                         const sf_lif_params* lif, float threshold, const float* v_init, void* spikes, float* v_out,
                         void* workspace, size_t workspace_bytes, void* stream) {

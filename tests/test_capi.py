@@ -177,3 +177,18 @@ def test_fused_conv1x1_lif_validation_without_touching_the_device():
     assert _status(L.sf_conv1x1_lif_sparse_binres, ctypes.byref(ok), 2, *args, None, ctypes.byref(lif), None, d, d,
                    None, None, None) == _lib.SF_ERR_INVALID
     assert b"res_bits" in L.sf_last_error()
+
+
+def test_noalloc_entry_point_refuses_oversized_bitmaps_on_the_host():
+    # Returns SF_ERR_WORKSPACE from the size check, before any device call.
+    L = _lib.lib()
+    d = _lib.conv_desc(4096, 256, 56, 56, 64, 56, 56, 3, 1, 1, 0, 0)
+    assert _lib.conv2d_workspace_size(d) > _lib.NOALLOC_SCRATCH_BYTES
+    dummy = ctypes.c_void_p(16)
+    rc = L.sf_conv2d_forward_noalloc(ctypes.byref(d), dummy, dummy, None, ctypes.c_float(1e-6), dummy, None)
+    assert rc == _lib.SF_ERR_WORKSPACE
+    assert b"scratch" in L.sf_last_error()
+    # Bad descriptors are refused before the size check, as sf_conv2d_forward does.
+    bad = _lib.conv_desc(1, 8, 8, 8, 8, 8, 8, 5, 1, 2, 0, 0)
+    assert L.sf_conv2d_forward_noalloc(ctypes.byref(bad), dummy, dummy, None, ctypes.c_float(1e-6), dummy,
+                                       None) == _lib.SF_ERR_UNSUPPORTED
