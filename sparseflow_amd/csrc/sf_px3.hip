@@ -109,26 +109,38 @@ __device__ __forceinline__ uint32_t px3_select(const uint32_t (&w)[9], int t) {
   return b3 ? v8 : d0;
 }
 
-// Bitmap word c of each of the lane's nine input taps (0 outside the frame).
-// Branch-free with 32-bit offsets from the frame's bitmap base: taps outside
-// the frame read pixel 0 and are zeroed, so all nine loads are in flight
-// together.
+// Bitmap word c of each of the lane's nine input taps (0 outside the frame),
+// bf = the frame's bitmap.  Raw buffer loads over the frame's words: a tap
+// outside the frame gets an offset past num_records, which the hardware
+// returns as 0, so no instruction has to touch the loaded values until they
+// are used (the next chunk's words are requested a whole chunk walk ahead).
 __device__ __forceinline__ void px3_load_words(uint32_t (&w)[9], const uint32_t* __restrict__ bf,
                                                const ConvArgs& a, int ih0, int iw0, int c) {
-  uint32_t v[9];
+  const uint32_t frame_bytes = (uint32_t)a.hw_in * (uint32_t)a.cwp * 4u;
+  const auto rs = buf_rsrc(bf, frame_bytes);
 #pragma unroll
   for (int tp = 0; tp < 9; ++tp) {
     const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
     const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
-    const uint32_t off = (uint32_t)(in ? ih * a.w_in + iw : 0) * (uint32_t)a.cwp + (uint32_t)c;
-    v[tp] = bf[off];
+    const uint32_t off = in ? ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.cwp + (uint32_t)c) * 4u : 0x80000000u;
+    w[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
   }
-#pragma unroll
-  for (int tp = 0; tp < 9; ++tp) {
-    const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
-    const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
-    w[tp] = in ? v[tp] : 0u;
-  }
+}
+
+// Tile t of a wavefront (64 output pixels of one sample): whether this lane
+// has an output pixel there, and its sample and the top-left corner of its
+// input window.
+__device__ __forceinline__ bool px3_tile(const ConvArgs& a, int t, int lane, int total, int tpf, int& sample,
+                                         int& ih0, int& iw0) {
+  if (t >= total) return false;
+  sample = t / tpf;
+  const int p0 = (t - sample * tpf) * 64;
+  if (lane >= min(64, a.hw_out - p0)) return false;
+  const int q = p0 + lane;
+  const int oh = q / a.w_out, ow = q - oh * a.w_out;
+  ih0 = oh * a.s - 1;
+  iw0 = ow * a.s - 1;
+  return true;
 }
 
 template <int CO, typename TOut>
@@ -198,6 +210,16 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
+  // First-chunk bitmap words of the next tile (or the next step) are always
+  // requested before the current tile's (step's) stores: the vector memory
+  // counter retires in issue order, so words requested after the 64 stores
+  // of a tile would make their first use wait for all of those stores.
+  uint32_t wn[9];
+  if constexpr (!LIF) {
+    int ih0, iw0, sample;
+    if (px3_tile(a, (int)(blockIdx.x / groups) * kRowsWaves + wave, lane0, total, tpf, sample, ih0, iw0))
+      px3_load_words(wn, bits + (int64_t)sample * a.hw_in * a.cwp, a, ih0, iw0, 0);
+  }
   // Passes of kRowsWaves tiles.  With streamed chunks every wavefront takes
   // part in every barrier, including those of a pass past the end.
   for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
@@ -236,10 +258,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
 #pragma unroll
       for (int co = 0; co < CO; ++co) acc[co] = s_seed[co];
     }
-    // First-chunk bitmap words of the next step are loaded before this step's
-    // spike stores (the vector memory counter retires in issue order).
-    uint32_t wn[9];
-    if (mine) px3_load_words(wn, bits + (LIF ? sample : sample) * a.hw_in * a.cwp, a, ih0, iw0, 0);
+    // The fused LIF kernel requests a tile's first words here; it prefetches
+    // per step instead (the T steps of a tile are its long stretch of work).
+    if constexpr (LIF)
+      if (mine) px3_load_words(wn, bits + (int64_t)sample * a.hw_in * a.cwp, a, ih0, iw0, 0);
     for (int st = 0; st < steps; ++st) {
       const int64_t frame = LIF ? (int64_t)st * a.n + sample : sample;
       if constexpr (LIF) lif_seed_lds<CO>(acc, L, s_seed);
@@ -353,6 +375,12 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
         }
       }
     }
+    if constexpr (!LIF) {
+      int nih0, niw0, nsample;
+      if (px3_tile(a, (pass + nblk) * kRowsWaves + wave, lane, total, tpf, nsample, nih0, niw0))
+        px3_load_words(wn, bits + (int64_t)nsample * a.hw_in * a.cwp, a, nih0, niw0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (mine) {
       if constexpr (LIF) {
         const int64_t vb = ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
@@ -437,8 +465,11 @@ bool px3_resident(const ConvArgs& a) {
 }
 
 bool px3_applicable(const ConvArgs& a) {
+  // (A frame's bitmap must stay below 2 GB: px3_load_words addresses it
+  // through a buffer resource and marks taps outside the frame with offset
+  // 2^31.)
   return a.k == 3 && a.p == 1 && (a.s == 1 || a.s == 2) && a.c_out % 4 == 0 && a.cwp <= 64 &&
-         a.n * (int64_t)((a.hw_out + 63) / 64) < (1ll << 30);
+         a.n * (int64_t)((a.hw_out + 63) / 64) < (1ll << 30) && (int64_t)a.hw_in * a.cwp * 4 < (1ll << 31);
 }
 
 int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
