@@ -233,16 +233,23 @@ def cpu_baseline(name, target_seconds=12.0):
 
 
 E2E_WORKLOAD = "resnet50_e2e"  # T=16, batch 32, 3x224x224, images/s
+# The same network with every neuron layer's threshold calibrated to ~1% spike
+# density (random init at v_th = 1 is silent past the first neuron layer).
+E2E_LIVE_WORKLOAD = "resnet50_e2e_live"
+E2E_LIVE_DENSITY = 0.01
 ATTN_WORKLOAD = "config5_spikformer_block"  # T=4, N=64, 196 tokens, dim 384, 12 heads, Bernoulli(0.1)
 
 
-def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
+def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32, live=False):
     """Spiking-ResNet50 forward (random init, BN folded, multi-step LIF
-    tau=2 v_th=1 hard reset) through optimize(): images/s = batch / t."""
+    tau=2 v_th=1 hard reset) through optimize(): images/s = batch / t.
+    live=True first calibrates every neuron layer's threshold on the timed
+    input to E2E_LIVE_DENSITY spikes (Models.calibrate_lif_thresholds_); the
+    dense baseline then has the same thresholds."""
     import copy
 
     import sparseflow_amd as sf
-    from sparseflow_amd.Models import fold_bn_, fuse_conv_lif_, spiking_resnet50
+    from sparseflow_amd.Models import calibrate_lif_thresholds_, fold_bn_, fuse_conv_lif_, spiking_resnet50
     from sparseflow_amd.neuron import LIFNode, reset_net
 
     t0 = time.time()
@@ -252,9 +259,13 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
     torch.backends.cudnn.benchmark = False
     torch.manual_seed(0)
     model = fold_bn_(spiking_resnet50(T=T)).to(dev)
-    dense = copy.deepcopy(model) if with_dense else None
     g = torch.Generator(device=dev).manual_seed(0)
     img = torch.randn(batch, 3, 224, 224, generator=g, device=dev)
+    calib = None
+    if live:
+        calib = calibrate_lif_thresholds_(model, img, target_density=E2E_LIVE_DENSITY)
+        log(f"[bench] e2e live: thresholds calibrated to {E2E_LIVE_DENSITY} in {time.time() - t0:.1f} s")
+    dense = copy.deepcopy(model) if with_dense else None
     sf.optimize(model, sample_input=img, verbose=False)
     n_sparse = sum(type(m).__name__ == "SparseConv2d" for m in model.modules())
     torch.cuda.synchronize()
@@ -282,13 +293,21 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
         ms = time_gpu(lambda: run(model), steps, warmup)
         log(f"[bench] e2e: fused ({n_fused} conv-LIF pairs) {ms:.2f} ms per forward ({time.time() - t0:.1f} s)")
         res = {
-            "workload": E2E_WORKLOAD, "T": T, "batch": batch, "ms_per_forward": ms,
+            "workload": E2E_LIVE_WORKLOAD if live else E2E_WORKLOAD, "T": T, "batch": batch, "ms_per_forward": ms,
             "images_per_s": batch / (ms * 1e-3), "sparse_convs": n_sparse,
             "fused_conv_lif_pairs": n_fused, "unfused_ms_per_forward": ums,
             "max_abs_logit_diff_fused_vs_unfused": float((fout - out).abs().max()),
             "mean_spike_density": sum(densities.values()) / max(1, len(densities)),
             "spike_density_by_layer": {k: round(v, 5) for k, v in densities.items()},
         }
+        if calib is not None:
+            res["threshold_calibration"] = {
+                "target_density": E2E_LIVE_DENSITY,
+                "method": "per neuron layer, in network order: bisection of v_threshold on the layer's input "
+                          "currents over 2^20 sampled neurons (Models.calibrate_lif_thresholds_)",
+                "v_threshold_min": round(min(v for v, _ in calib.values()), 4),
+                "v_threshold_max": round(max(v for v, _ in calib.values()), 4),
+            }
         if dense is not None:
             ref = run(dense)
             torch.cuda.synchronize()
@@ -298,6 +317,7 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32):
             res["dense_images_per_s"] = batch / (dms * 1e-3)
             res["speedup_vs_dense"] = dms / ms
             res["max_abs_logit_diff_vs_dense"] = float((out - ref).abs().max())
+            res["max_abs_logit_vs_dense"] = float(ref.abs().max())
     return res
 
 
@@ -416,7 +436,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="resnet50_layer1_conv3x3", choices=sorted(WORKLOADS))
     ap.add_argument("--extra", default="all", help="'all', 'none' or comma-separated workload names (+ "
-                                                   f"{LIF_WORKLOAD}, {ATTN_WORKLOAD}, {E2E_WORKLOAD})")
+                                                   f"{LIF_WORKLOAD}, {ATTN_WORKLOAD}, {E2E_WORKLOAD}, "
+                                                   f"{E2E_LIVE_WORKLOAD})")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-miopen", action="store_true", help="skip the MIOpen baselines")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -453,7 +474,8 @@ def main():
     extra = {}
     names = []
     if args.extra == "all":
-        names = [n for n in WORKLOADS if n != args.workload] + [LIF_WORKLOAD, ATTN_WORKLOAD, E2E_WORKLOAD]
+        names = [n for n in WORKLOADS if n != args.workload] + [LIF_WORKLOAD, ATTN_WORKLOAD, E2E_WORKLOAD,
+                                                                E2E_LIVE_WORKLOAD]
     elif args.extra != "none":
         names = [n.strip() for n in args.extra.split(",") if n.strip()]
     for name in names:
@@ -463,8 +485,8 @@ def main():
             r = bench_lif(steps, 3, dev, with_miopen=not args.no_miopen)
         elif name == ATTN_WORKLOAD:
             r = bench_attn(steps, 3, dev, with_dense=not args.no_miopen)
-        elif name == E2E_WORKLOAD:
-            r = bench_e2e(max(3, steps // 5), 2, dev, with_dense=not args.no_miopen)
+        elif name in (E2E_WORKLOAD, E2E_LIVE_WORKLOAD):
+            r = bench_e2e(max(3, steps // 5), 2, dev, with_dense=not args.no_miopen, live=name == E2E_LIVE_WORKLOAD)
         else:
             r = bench_conv(name, steps, 3, dev, with_miopen=not args.no_miopen)
         extra[name] = r

@@ -179,3 +179,69 @@ def fuse_conv_lif_(model: nn.Module) -> int:
             mod.conv3_lif = SparseConv1x1LIF(mod.conv3, mod.sn3)
             n += 1
     return n
+
+
+def _lif_density(I: torch.Tensor, node: LIFNode, v_th: float) -> float:
+    """Spike density of `node`'s LIF dynamics on currents I [T, K] with
+    threshold v_th (the membrane starts at v_reset, 0 for soft reset)."""
+    vr = 0.0 if node.v_reset is None else float(node.v_reset)
+    v = torch.full_like(I[0], vr)
+    fired = torch.zeros((), dtype=torch.float64, device=I.device)
+    for t in range(I.shape[0]):
+        h = v + (I[t] - (v - vr)) / node.tau if node.decay_input else v - (v - vr) / node.tau + I[t]
+        s = h >= v_th
+        fired += s.sum()
+        v = torch.where(s, torch.full_like(h, vr), h) if node.v_reset is not None else h - s.float() * v_th
+    return float(fired) / I.numel()
+
+
+def calibrate_lif_thresholds_(model: nn.Module, img: torch.Tensor, target_density: float = 0.01,
+                              sample: int = 1 << 20, iters: int = 28, seed: int = 0) -> dict:
+    """Set every LIFNode's v_threshold so that its spike density on `img` is
+    `target_density`, in place; returns {layer name: (v_threshold, density)}.
+
+    Random-initialised spiking networks are nearly silent past the first
+    neuron layer at v_threshold = 1 (the density dies out layer by layer), so
+    the sparse kernels would only ever see all-zero input.  The reference's
+    own harness varies the thresholds to vary sparsity
+    (Benchmark/run-resnet50.sh:16-64, v_threshold in {1.0, 0.75, 0.5, 0.25});
+    this calibrates each layer instead: one forward in network order, a
+    pre-hook on each neuron layer bisects the threshold on its input currents
+    (x, plus the residual where one is added) over a fixed random sample of
+    `sample` neurons, so every layer is calibrated on the spikes of the
+    already calibrated layers before it.  The LIF dynamics are elementwise,
+    so a neuron sample gives the layer's density to ~1/sqrt(sample)."""
+    names = {m: n for n, m in model.named_modules() if isinstance(m, LIFNode)}
+    gen = torch.Generator(device=img.device).manual_seed(seed)
+    result = {}
+
+    def pre(mod, args):
+        cur = args[0].float()
+        if len(args) > 1 and args[1] is not None:
+            cur = cur + args[1].float()
+        flat = cur.reshape(cur.shape[0], -1)
+        if flat.shape[1] > sample:
+            idx = torch.randint(0, flat.shape[1], (sample,), generator=gen, device=flat.device)
+            flat = flat[:, idx]
+        lo, hi = 0.0, float(flat.abs().max()) + 1.0
+        for _ in range(iters):
+            mid = 0.5 * (lo + hi)
+            if _lif_density(flat, mod, mid) > target_density:
+                lo = mid
+            else:
+                hi = mid
+        mod.v_threshold = hi
+        result[names[mod]] = (hi, _lif_density(flat, mod, hi))
+
+    hooks = [m.register_forward_pre_hook(pre) for m in names]
+    try:
+        with torch.no_grad():
+            from ..neuron import reset_net
+            reset_net(model)
+            model(img)
+            reset_net(model)
+    finally:
+        for h in hooks:
+            h.remove()
+    return result
+

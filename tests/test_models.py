@@ -90,3 +90,28 @@ def test_fused_pairs_follow_dispatch_swaps_and_dense_decisions():
     assert pair.runs_fused(cuda_like)
     pair.conv.backend_mode = "dense"
     assert not pair.runs_fused(cuda_like)
+
+
+def test_calibrated_thresholds_give_the_target_density_per_layer():
+    # Every neuron layer is calibrated in network order on its own input
+    # currents: on the calibration input each layer then fires at ~1%.
+    from sparseflow_amd.Models import calibrate_lif_thresholds_
+    from sparseflow_amd.neuron import LIFNode, reset_net
+
+    m = fold_bn_(_model(T=4, seed=7))
+    x = torch.randn(1, 3, 64, 64, generator=torch.Generator().manual_seed(8))
+    rec = calibrate_lif_thresholds_(m, x, target_density=0.01, sample=1 << 15)
+    names = [n for n, mod in m.named_modules() if isinstance(mod, LIFNode)]
+    assert list(rec) == names and len(names) == 49
+    ths = [mod.v_threshold for mod in m.modules() if isinstance(mod, LIFNode)]
+    assert len(set(ths)) > 40 and all(t > 0 for t in ths)
+    dens = {}
+    hooks = [mod.register_forward_hook(lambda _m, _i, o, n=n: dens.__setitem__(n, float(o.float().mean())))
+             for n, mod in m.named_modules() if isinstance(mod, LIFNode)]
+    with torch.no_grad():
+        reset_net(m)
+        m(x)
+    for h in hooks:
+        h.remove()
+    for n, d in dens.items():
+        assert 0.005 < d < 0.02, f"{n}: density {d}"
