@@ -393,13 +393,20 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
         sp = SparseConv2d.from_dense(conv).to(dev)
         sp.set_inference_mode(True)
         ms = time_gpu(lambda: sp(img), steps, warmup)
+        kt = kernel_times(lambda: sp(img), max(5, min(steps, 20)))
         torch.backends.cudnn.benchmark = True
         wd = conv.weight.float()
         dms = time_gpu(lambda: torch.nn.functional.conv2d(img, wd, None, 1, 1), max(5, steps // 2), 3) \
             if with_dense else None
         torch.backends.cudnn.benchmark = False
+        stem_y = bt * dim * 32 * 32 * 4
         ops["stem_conv3x3_3to384"] = {"us": ms * 1e3, "dense_us": None if dms is None else dms * 1e3,
-                                      "speedup_vs_dense": None if dms is None else dms / ms}
+                                      "speedup_vs_dense": None if dms is None else dms / ms,
+                                      "kernels_us": {k: v[1] * 1e3 for k, v in kt.items()},
+                                      "alg_bytes": img.numel() * 4 + dim * 27 * 4 + stem_y,
+                                      "hbm_gbs": (img.numel() * 4 + dim * 27 * 4 + stem_y) / (ms * 1e-3) / 1e9}
+        log(f"[bench] attn stem_conv3x3_3to384: {ms * 1e3:.1f} us (dense {'-' if dms is None else f'{dms * 1e3:.1f}'}"
+            f" us) kernels {ops['stem_conv3x3_3to384']['kernels_us']}")
     # One Spikformer block's matmul work: q, k, v, proj projections, the
     # attention core (fused; the dense reference runs qk then av) and the MLP.
     mlp = ops["mlp_fc1_384x1536"]["us"] + ops["mlp_fc2_1536x384"]["us"]

@@ -195,7 +195,7 @@ int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                                      "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse",
-                                     "spike_attention", "linear_mfma", "bmm_mfma", "conv_lif_flat"};
+                                     "spike_attention", "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma"};
 
 }  // namespace
 
@@ -351,6 +351,13 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
   if (bits == nullptr || flags == nullptr || x == nullptr || wt == nullptr || y == nullptr)
     return fail(SF_ERR_INVALID, "NULL pointer");
   const sf::ConvArgs a = conv_args(d, d->n, bits, flags, x, wt, bias, y, false);
+  // 3x3 with a reduction of at most 32 (an image stem): one dense tile on the
+  // matrix cores, whatever the density.
+  if (d->in_dtype == SF_F32 && sf::mfma_conv_applicable(a)) {
+    rc = sf::launch_conv_mfma(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
+    if (rc != hipSuccess) return hip_fail(rc, "conv_mfma launch");
+    return SF_OK;
+  }
   if (sf::rows_applicable(a)) {
     rc = sf::launch_conv_rows(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
     if (rc != hipSuccess) return hip_fail(rc, "conv_rows launch");

@@ -104,6 +104,10 @@ bool px3_applicable(const ConvArgs& a);
 // The weights stay resident in LDS for the whole launch (C_in <= 128).
 bool px3_resident(const ConvArgs& a);
 int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+// Matrix-core Stage 2 for 3x3 layers with a reduction of at most 32
+// (C_in * 9 <= 32, f32 input): the whole K is one dense tile.
+bool mfma_conv_applicable(const ConvArgs& a);
+int launch_conv_mfma(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 // Fused conv + multi-step LIF on the pixel-tile formulation (3x3 s1; same
 // applicability as px3_applicable with stride 1).
 int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
@@ -199,7 +203,7 @@ void conv_geometry(ConvArgs& a, bool lif);
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_LIF_FLAT = 16, K_COUNT = 17 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_LIF_FLAT = 16, K_MFMA_CONV = 17, K_COUNT = 18 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

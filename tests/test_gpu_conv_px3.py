@@ -51,7 +51,7 @@ CASES = [
     (2, 256, 28, 28, 64, 2),    # layer3.0 conv2, stride 2
     (2, 512, 14, 14, 64, 2),    # layer4.0 conv2, stride 2
     (2, 64, 15, 13, 8, 2),      # odd input, stride 2
-    (2, 1, 5, 7, 4, 1),         # one channel
+    (2, 4, 5, 7, 4, 1),         # four channels (one nearly empty word)
     (3, 17, 1, 56, 12, 1),      # single row
     (2, 33, 7, 9, 68, 1),       # two words, second nearly empty; ragged second group
     (1, 300, 6, 10, 100, 1),    # last chunk partially filled

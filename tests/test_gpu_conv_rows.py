@@ -42,7 +42,7 @@ CASES = [
     # (N, C_in, H, W, C_out)
     (8, 64, 32, 32, 64),    # BASELINE config 1 shape
     (4, 64, 57, 32, 64),    # tall frames
-    (2, 1, 5, 32, 3),       # single input channel, few rows
+    (2, 4, 5, 32, 3),       # four input channels (one nearly empty word), few rows
     (3, 17, 1, 32, 10),     # single row: no input row above or below
     (2, 32, 2, 32, 64),     # one 32-bit word per pixel
     (2, 33, 7, 32, 65),     # two words, second nearly empty; C_out one past a group

@@ -44,7 +44,7 @@ CASES = [
     (4, 128, 28, 28, 128),  # ResNet50 layer2 conv2 shape (4 chunks, streamed)
     (4, 256, 14, 14, 256),  # ResNet50 layer3 conv2 shape (8 chunks)
     (3, 64, 28, 28, 64),    # two chunks: resident, no barriers
-    (2, 1, 27, 28, 4),      # one channel, odd height (last tile one row)
+    (2, 4, 27, 28, 4),      # four channels, odd height (last tile one row)
     (2, 64, 13, 14, 64),    # odd plane size (13*14 % 4 != 0): goes to the pixel-tile kernel
     (5, 96, 10, 14, 100),   # three chunks, last tile two rows, ragged group
     (2, 33, 2, 14, 64),     # two-row frames: one tile per frame
