@@ -2,7 +2,8 @@
 
 A LIF layer that runs on the GPU can write, next to its spikes, their
 bitmap in the exact layout the prescan (`sf_prescan_pack`) would produce
-from them.  The map is remembered here, keyed by the spike tensor's memory;
+from them.  The map is remembered here, keyed by the spike tensor's memory
+(device index and address);
 `sparse_conv2d_forward` asks for it and, when the input is still that very
 tensor (alive, not modified in place since: same version counter), skips its
 prescan pass over x.  This is the bit-packed inter-layer spike format: the
@@ -23,7 +24,11 @@ from typing import Optional, Tuple
 import torch
 
 _MAX_ENTRIES = 8
-_entries: "collections.OrderedDict[int, _Entry]" = collections.OrderedDict()
+_entries: "collections.OrderedDict[Tuple[int, int], _Entry]" = collections.OrderedDict()
+
+
+def _key(t: torch.Tensor) -> Tuple[int, int]:
+    return (t.get_device(), t.data_ptr())
 
 
 class _Entry:
@@ -40,7 +45,7 @@ class _Entry:
 def attach(spikes: torch.Tensor, frames: int, c: int, h: int, w: int, bits: torch.Tensor, flags: torch.Tensor) -> None:
     """Remember (bits, flags) as the prescan output of `spikes` viewed as
     [frames, c, h, w]."""
-    key = spikes.data_ptr()
+    key = _key(spikes)
     _entries.pop(key, None)
     _entries[key] = _Entry(spikes, (frames, c, h, w), bits, flags)
     while len(_entries) > _MAX_ENTRIES:
@@ -52,14 +57,21 @@ def lookup(x: torch.Tensor, threshold: float) -> Optional[Tuple[torch.Tensor, to
     exactly this memory and it is unchanged since; else None."""
     if not (0.0 <= threshold < 0.5) or not x.is_cuda or not x.is_contiguous():
         return None
-    e = _entries.get(x.data_ptr())
+    key = _key(x)
+    e = _entries.get(key)
     if e is None:
         return None
     src = e.ref()
     if src is None or src._version != e.version or x._version != e.version or tuple(x.shape) != e.shape:
-        _entries.pop(x.data_ptr(), None)
+        _entries.pop(key, None)
         return None
     return e.bits, e.flags
+
+
+def recorded(x: torch.Tensor) -> bool:
+    """Whether a map is recorded for x's memory (valid or not): a cheap
+    pre-check before `lookup`."""
+    return bool(_entries) and _key(x) in _entries
 
 
 def clear() -> None:

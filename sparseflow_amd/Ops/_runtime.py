@@ -162,8 +162,13 @@ class DispatchAudit:
         self.mismatch = 0
 
     def record(self, module, path: str) -> None:
-        expected = str(getattr(module, "sf_dispatch_decision", getattr(module, "sf_backend_mode", "")))
-        expected = expected.strip().lower()
+        # The decision stamps are plain attributes: read them from the
+        # instance dict (a missed nn.Module attribute lookup is slow).
+        d = vars(module)
+        expected = d.get("sf_dispatch_decision", d.get("sf_backend_mode", ""))
+        if not expected:
+            return
+        expected = str(expected).strip().lower()
         if not expected:
             return
         self.seen += 1

@@ -132,7 +132,8 @@ def _load() -> ctypes.CDLL:
 
 def lib() -> ctypes.CDLL:
     """The loaded library; raises SparseFlowLibError when it is not built."""
-    return _load()
+    loaded = _lib
+    return loaded if loaded is not None else _load()
 
 
 def available() -> bool:
@@ -156,8 +157,20 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else c_void_p(t.data_ptr())
 
 
+_current_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def raw_stream(index: int) -> int:
+    """Handle (hipStream_t as an int) of torch's current stream on device
+    `index`, without building a torch Stream object."""
+    if _current_raw_stream is not None:
+        return int(_current_raw_stream(index))
+    return int(torch.cuda.current_stream(index).cuda_stream)
+
+
 def _stream(device: torch.device):
-    return c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    index = device.index
+    return c_void_p(raw_stream(torch.cuda.current_device() if index is None else index))
 
 
 def dtype_code(dtype: torch.dtype) -> int:
@@ -470,7 +483,7 @@ def spike_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 
 KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                 "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
-                "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma")
+                "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma", "conv_rows_fused")
 
 
 def timing_enable(on: bool) -> None:

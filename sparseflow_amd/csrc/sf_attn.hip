@@ -134,13 +134,9 @@ int launch_attn_t(const AttnArgs& a, hipStream_t stream) {
   const int64_t cap = (int64_t)num_cus() * 16;
   const int grid = (int)(items < cap ? items : cap);
   if (grid == 0) return (int)hipSuccess;
-  auto kern = k_spike_attn<T, TOut, D>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kMaxLdsBytes);
-    attr_done = true;
-  }
+  constexpr auto kern = k_spike_attn<T, TOut, D>;
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
+  if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kAttnThreads), lds, stream, a);
   return (int)hipGetLastError();
 }

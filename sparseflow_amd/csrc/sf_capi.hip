@@ -195,7 +195,8 @@ int64_t g_count[sf::K_COUNT] = {};
 const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                                      "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse",
-                                     "spike_attention", "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma"};
+                                     "spike_attention", "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma",
+                                     "conv_rows_fused"};
 
 }  // namespace
 
@@ -615,6 +616,18 @@ int sf_conv2d_forward(const sf_conv_desc* d, const void* x, const float* wt, con
   if (x == nullptr || wt == nullptr || y == nullptr || workspace == nullptr)
     return fail(SF_ERR_INVALID, "NULL pointer");
   if (workspace_bytes < sf_conv2d_workspace_size(d)) return fail(SF_ERR_WORKSPACE, "workspace too small");
+  // Small 3x3 layers on 32-wide frames: the prescan runs inside the conv
+  // kernel, one launch and no bitmap in HBM.  (The matrix-core stem path
+  // reads the bitmap, so it keeps the two stages.)
+  {
+    const sf::ConvArgs fa = conv_args(d, d->n, nullptr, nullptr, x, wt, bias, y, false);
+    if (!(d->in_dtype == SF_F32 && sf::mfma_conv_applicable(fa)) && sf::rows_fused_applicable(fa)) {
+      rc = sf::launch_conv_rows_fused(fa, d->in_dtype, d->out_dtype, sf_activity_cutoff(threshold),
+                                      static_cast<hipStream_t>(stream));
+      if (rc != hipSuccess) return hip_fail(rc, "conv_rows_fused launch");
+      return SF_OK;
+    }
+  }
   const Workspace ws = carve(workspace, d->n, d->c_in, d->h_in, d->w_in);
   rc = sf_prescan_pack(x, d->in_dtype, d->n, d->c_in, d->h_in, d->w_in, threshold, ws.bits, ws.flags, stream);
   if (rc != SF_OK) return rc;

@@ -383,14 +383,6 @@ __global__ __launch_bounds__(256) void k_conv_lif(ConvArgs a) {
   }
 }
 
-// Raise the dynamic-LDS ceiling of a kernel to the full 160 KB of a gfx950
-// CU (the default limit is 64 KB).  Called once per instantiation.
-template <typename K_t>
-void allow_full_lds(K_t kernel) {
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kMaxLdsBytes);
-}
-
 template <typename TIn, typename TOut>
 int launch_conv_t(const ConvArgs& a, hipStream_t stream) {
   const int64_t blocks = (a.total_groups + a.waves_per_block - 1) / a.waves_per_block;
@@ -398,12 +390,12 @@ int launch_conv_t(const ConvArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.waves_per_block * a.wave_lds;
   const dim3 grid((unsigned)blocks), block(64 * a.waves_per_block);
   const bool wide = a.c_out >= 128;
-#define SF_LAUNCH_CONV(KK, CC)                                  \
-  do {                                                          \
-    auto kern = k_conv_gather<TIn, TOut, KK, CC>;               \
-    static bool attr_done = false;                              \
-    if (!attr_done) { allow_full_lds(kern); attr_done = true; } \
-    hipLaunchKernelGGL(kern, grid, block, lds, stream, a);      \
+#define SF_LAUNCH_CONV(KK, CC)                                   \
+  do {                                                           \
+    constexpr auto kern = k_conv_gather<TIn, TOut, KK, CC>;      \
+    const int e = set_lds_limit_once<kern>(kMaxLdsBytes);        \
+    if (e != (int)hipSuccess) return e;                          \
+    hipLaunchKernelGGL(kern, grid, block, lds, stream, a);       \
   } while (0)
   if (a.k == 3) {
     if (wide) SF_LAUNCH_CONV(3, 2); else SF_LAUNCH_CONV(3, 1);
@@ -423,14 +415,14 @@ int launch_lif_t(const ConvArgs& a, hipStream_t stream) {
   const size_t lds = (size_t)a.waves_per_block * a.wave_lds;
   const dim3 grid((unsigned)blocks), block(64 * a.waves_per_block);
   if (a.k == 3) {
-    auto kern = k_conv_lif<TIn, TOut, 3>;
-    static bool attr_done = false;
-    if (!attr_done) { allow_full_lds(kern); attr_done = true; }
+    constexpr auto kern = k_conv_lif<TIn, TOut, 3>;
+    const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
+    if (e != (int)hipSuccess) return e;
     hipLaunchKernelGGL(kern, grid, block, lds, stream, a);
   } else {
-    auto kern = k_conv_lif<TIn, TOut, 1>;
-    static bool attr_done = false;
-    if (!attr_done) { allow_full_lds(kern); attr_done = true; }
+    constexpr auto kern = k_conv_lif<TIn, TOut, 1>;
+    const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
+    if (e != (int)hipSuccess) return e;
     hipLaunchKernelGGL(kern, grid, block, lds, stream, a);
   }
   return (int)hipGetLastError();

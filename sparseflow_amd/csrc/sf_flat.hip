@@ -517,15 +517,10 @@ int launch_flat_lif_t(const ConvArgs& a, const void* x2, const FlatLifOut& o, hi
   const int64_t cap = (int64_t)num_cus() * (NWV == 4 ? 3 : 1);  // resident workgroups
   const int per_group = (int)(need < cap ? need : cap);
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_flat_lif<CW, TIn, TOut, VEC, XV, NWV>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    // The kernel also holds 256 B of static LDS (the per-channel seed).
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes - 1024);
-    if (e != hipSuccess) return (int)e;
-    attr_done = true;
-  }
+  constexpr auto kern = k_conv_flat_lif<CW, TIn, TOut, VEC, XV, NWV>;
+  // The kernel also holds 256 B of static LDS (the per-channel seed).
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
+  if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NWV), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<const TIn*>(x2),
                      static_cast<TOut*>(a.y), o, groups, nchunks);
@@ -571,15 +566,10 @@ int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_flat<CW, TIn, ROWS>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    // 1 KB of the LDS is left to the kernel's static arrays.
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes - 1024);
-    if (e != hipSuccess) return (int)e;
-    attr_done = true;
-  }
+  constexpr auto kern = k_conv_flat<CW, TIn, ROWS>;
+  // 1 KB of the LDS is left to the kernel's static arrays.
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
+  if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype);
   return (int)hipGetLastError();

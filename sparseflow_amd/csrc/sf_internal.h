@@ -7,6 +7,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "sparseflow.h"
 
 namespace sf {
@@ -90,6 +92,11 @@ int launch_conv_lif(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
 // Row-tile scatter Stage 2 (3x3 s1, C_in <= 64, frame width 32 or 56).
 bool rows_applicable(const ConvArgs& a);
 int launch_conv_rows(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+
+// Stage 1 fused into the row-tile Stage 2 (3x3 s1, C_in <= 64, frame width
+// 32): reads x directly (a.bits / a.flags unused); bit = |x| >= cutoff.
+bool rows_fused_applicable(const ConvArgs& a);
+int launch_conv_rows_fused(const ConvArgs& a, int in_dtype, int out_dtype, float cutoff, hipStream_t stream);
 
 // K-chunked row-tile Stage 2 (3x3 s1, any C_in, frame width 28 or 14).
 bool rows_kc_applicable(const ConvArgs& a);
@@ -197,13 +204,30 @@ struct AttnArgs {
 size_t attn_lds_bytes(int s, int d);
 int launch_spike_attn(const AttnArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
+// Raise kernel K's dynamic-LDS ceiling to `bytes` (the default limit is
+// 64 KB) once per device and process.  Thread-safe: two first calls racing
+// set the same attribute twice, which is harmless; a failure is returned and
+// the next call tries again.
+template <auto K>
+int set_lds_limit_once(int bytes) {
+  static std::atomic<uint64_t> done{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (done.load(std::memory_order_acquire) & bit) return (int)hipSuccess;
+  const hipError_t e =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(K), hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+  return (int)e;
+}
+
 // Conv launch geometry shared by the ABI (workspace checks) and launchers.
 void conv_geometry(ConvArgs& a, bool lif);
 
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_LIF_FLAT = 16, K_MFMA_CONV = 17, K_COUNT = 18 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_LIF_FLAT = 16, K_MFMA_CONV = 17, K_ROWS_FUSED = 18, K_COUNT = 19 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

@@ -224,13 +224,10 @@ int launch_conv_mfma(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t
   const int64_t blocks = a.n * (int64_t)bpf * groups;
   const int win = (int)mc_window_floats(a);
   const size_t lds = kMcFixedLds + (size_t)win * sizeof(float);
-  static bool attr_done = false;  // the attribute is per function, set once per process
-  if (!attr_done) {
-    const hipError_t e =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(k_conv_mfma), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)(kMcFixedLds + kMcMaxInFloats * sizeof(float)));
-    if (e != hipSuccess) return (int)e;
-    attr_done = true;
+  const int e = set_lds_limit_once<k_conv_mfma>((int)(kMcFixedLds + kMcMaxInFloats * sizeof(float)));
+  if (e != (int)hipSuccess) {
+    timing_end(K_MFMA_CONV, stream);
+    return e;
   }
   hipLaunchKernelGGL(k_conv_mfma, dim3((unsigned)blocks), dim3(64 * kMcWaves), lds, stream, a, a.bits,
                      static_cast<const float*>(a.x), a.wt, a.bias, static_cast<float*>(a.y), groups, bpf, win);

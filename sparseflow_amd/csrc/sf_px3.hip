@@ -406,14 +406,9 @@ int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_px3<TIn, TOut, CO, LIF>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes - 1024);
-    if (e != hipSuccess) return (int)e;
-    attr_done = true;
-  }
+  constexpr auto kern = k_conv_px3<TIn, TOut, CO, LIF>;
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
+  if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype);
   return (int)hipGetLastError();

@@ -7,11 +7,11 @@
 // (lane = output channel, one accumulator register per output pixel).  The
 // weights of the workgroup's 64-channel group stay in LDS for the whole
 // (persistent) launch.  The wavefront walks the spike bitmap of the three
-// input rows on the scalar unit: every active (ci, ih, iw) contributes weight
-// rows (ci, kh = ih - oh + 1, kw) to output columns iw + 1 - kw, and because
-// the input position is a compile-time loop index, every target accumulator
-// is a fixed register.  Each weight row is read from LDS at an immediate
-// offset.  The finished row is transposed in registers (DPP row shifts and
+// input rows on the scalar unit (walk_window): every active (ci, ih, iw)
+// contributes weight rows (ci, kh = ih - oh + 1, kw) to output columns
+// iw + 1 - kw, and because the input position is a compile-time loop index,
+// every target accumulator is a fixed register.  Each weight row is read
+// from LDS at an immediate offset.  The finished row is transposed in registers (DPP row shifts and
 // quad permutes) so that each store instruction writes whole frame rows of
 // 64/QP channels as float4 runs.
 //
@@ -40,41 +40,25 @@ __device__ __forceinline__ M rl_word(M v0, M v1, int p) {
   }
 }
 
-// Accumulate the spikes of input row ih (= oh - 1 + IA) into acc; the
-// words of the three input rows were fetched with vector loads (v0, v1).
-template <int W, int QP, int CWP, int IA, bool VALUE, typename TIn>
-__device__ __forceinline__ void scatter_row(float (&acc)[4 * QP], typename Word<CWP>::type v0,
-                                            typename Word<CWP>::type v1, const char* wlb,
-                                            const TIn* __restrict__ xrow, int hw_in) {
-  typedef typename Word<CWP>::type M;
-  constexpr int CH = 8;  // positions per batch
-#pragma unroll
-  for (int ib0 = 0; ib0 < W; ib0 += CH) {
-    M mw[CH];
-#pragma unroll
-    for (int u = 0; u < CH; ++u) mw[u] = rl_word<M>(v0, v1, IA * W + ib0 + u);
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int ib = ib0 + u;
-      M m = mw[u];
-      while (m) {
-        const int ci = lowest_bit(m);
-        m &= m - 1;
-        const char* base = wlb + (ci * 9 + IA * 3) * 256;
-        float xv = 1.f;
-        if constexpr (VALUE) xv = to_f32<TIn>(xrow[(size_t)ci * hw_in + ib]);
-#pragma unroll
-        for (int kw = 0; kw < 3; ++kw) {
-          const int x = ib + 1 - kw;
-          if (x < 0 || x >= W) continue;
-          const float wv = *reinterpret_cast<const float*>(base + kw * 256);
-          if constexpr (VALUE) acc[x] = fmaf(xv, wv, acc[x]);
-          else acc[x] += wv;
-        }
-      }
-    }
+// Channel word of window position (input row oh - 1 + ia, column ib): lane
+// p & 63 of v0 (p < 64) or v1, p = ia * W + ib, read on the scalar unit.
+template <int W, typename M>
+struct RowWords {
+  M v0, v1;
+  __device__ __forceinline__ M operator()(int ia, int ib) const { return rl_word<M>(v0, v1, ia * W + ib); }
+};
+
+// x(ci, input row oh - 1 + ia, column ib) of the value path; xr = element
+// offset of row oh - 1 within a channel plane.
+template <int W, typename TIn>
+struct RowValues {
+  const TIn* __restrict__ xf;
+  int64_t xr;
+  int hw;
+  __device__ __forceinline__ float operator()(int ci, int ia, int ib) const {
+    return to_f32<TIn>(xf[(int64_t)ci * hw + xr + ia * W + ib]);
   }
-}
+};
 
 template <int W, int QP, int CWP, bool VALUE, typename TIn>
 __device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArgs& a,
@@ -83,9 +67,9 @@ __device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArg
   typedef typename Word<CWP>::type M;
   const M* __restrict__ fb = bits + frame * (int64_t)a.hw_in;
   const TIn* __restrict__ xf = x + frame * (int64_t)a.c_in * a.hw_in;
-  // Words of the 3 x W halo positions (rows oh-1 .. oh+1), position p in lane
-  // p & 63 of v0 / v1: two vector loads instead of batches of dependent
-  // scalar loads; rows outside the frame are never walked.
+  // Words of the 3 x W window positions (rows oh-1 .. oh+1), position p in
+  // lane p & 63 of v0 / v1: two vector loads instead of batches of dependent
+  // scalar loads; rows outside the frame read as zero words.
   const int lane = lane_id();
   M v0 = 0, v1 = 0;
   {
@@ -94,11 +78,9 @@ __device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArg
     if (p0 < 3 * W && ih0 >= 0 && ih0 < a.h_in) v0 = fb[(int64_t)(oh - 1) * W + p0];
     if (p1 < 3 * W && ih1 >= 0 && ih1 < a.h_in) v1 = fb[(int64_t)(oh - 1) * W + p1];
   }
-  if (oh >= 1)
-    scatter_row<W, QP, CWP, 0, VALUE, TIn>(acc, v0, v1, wlb, xf + (oh - 1) * W, a.hw_in);
-  scatter_row<W, QP, CWP, 1, VALUE, TIn>(acc, v0, v1, wlb, xf + oh * W, a.hw_in);
-  if (oh + 1 < a.h_in)
-    scatter_row<W, QP, CWP, 2, VALUE, TIn>(acc, v0, v1, wlb, xf + (oh + 1) * W, a.hw_in);
+  walk_window<0, W, 1, 4 * QP, VALUE, M>(acc, RowWords<W, M>{v0, v1}, wlb,
+                                          RowValues<W, TIn>{xf, (int64_t)(oh - 1) * W, a.hw_in}, oh >= 1,
+                                          oh + 1 < a.h_in);
 }
 
 // OR of the non-binary chunk flags covering input rows oh-1 .. oh+1.
@@ -425,13 +407,9 @@ int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stre
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_rows_kc<TH, W>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kMaxLdsBytes);
-    attr_done = true;
-  }
+  constexpr auto kern = k_conv_rows_kc<TH, W>;
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
+  if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags, a.x, a.wt, a.bias,
                      a.y, groups, nchunks, in_dtype, out_dtype);
   return (int)hipGetLastError();
@@ -446,13 +424,9 @@ int launch_rows_t(const ConvArgs& a, hipStream_t stream) {
   const int64_t need = (rows_total + NWR - 1) / NWR;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  auto kern = k_conv_rows<TIn, TOut, W, CWP, NWR>;
-  static bool attr_done = false;
-  if (!attr_done) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              kMaxLdsBytes);
-    attr_done = true;
-  }
+  constexpr auto kern = k_conv_rows<TIn, TOut, W, CWP, NWR>;
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
+  if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NWR), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, krows);
   return (int)hipGetLastError();

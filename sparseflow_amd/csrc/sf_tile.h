@@ -74,6 +74,85 @@ __device__ __forceinline__ int lowest_bit(M m) {
   else return __builtin_ctz(m);
 }
 
+template <typename M>
+__device__ __forceinline__ int pop_count(M m) {
+  if constexpr (sizeof(M) == 8) return __builtin_popcountll(m);
+  else return __builtin_popcount(m);
+}
+
+// ---------------------------------------------------------------------------
+// Spike walk of a three-row window (3x3 stride-1 row kernels, lane = output
+// channel, weight row (ci, kh, kw) of 64 channels at LDS byte offset
+// (ci * 9 + kh * 3 + kw) * 256 from the lane's slot wlb).
+//
+// Positions are walked row by row (ia = 0, 1, 2), column by column (IB, a
+// compile-time index), channels in ascending order.  Spike (ci, ia) at IB
+// adds weight row (ci, kh = ia, kw) to acc[IB + D - kw] for each kw with
+// 0 <= IB + D - kw < NACC (value tiles multiply it by xval(ci, ia, IB)), so
+// every accumulator is a fixed register and receives its taps in the order
+// (input row, input column, ci): deterministic, and the same in every kernel
+// that walks this way.
+//
+// The walk runs on the scalar unit, whose issue rate (one instruction per
+// SIMD every fourth cycle, shared by the SIMD's wavefronts) bounds it: per
+// spike one find-first-set, a shift and xor that clear the bit and set the
+// loop condition, and one multiply for the channel's row block; the row and
+// tap offsets (kh * 768 + kw * 256) ride in the LDS instructions' immediate
+// offsets.
+// ---------------------------------------------------------------------------
+template <int IA, int IB, int D, int NACC, bool VALUE, typename M, typename XV>
+__device__ __forceinline__ void walk_position(float (&acc)[NACC], M m, const char* wlb, const XV& xval) {
+  while (m) {
+    const int ci = lowest_bit(m);
+    m ^= (M)1 << ci;
+    const char* base = wlb + ci * (9 * 256);
+    float xv = 1.f;
+    if constexpr (VALUE) xv = xval(ci, IA, IB);
+#pragma unroll
+    for (int kw = 0; kw < 3; ++kw) {
+      const int o = IB + D - kw;
+      if (o < 0 || o >= NACC) continue;
+      const float wv = *reinterpret_cast<const float*>(base + (IA * 3 + kw) * 256);
+      if constexpr (VALUE) acc[o] = fmaf(xv, wv, acc[o]);
+      else acc[o] += wv;
+    }
+  }
+}
+
+template <int IA, int IB0, int U, int NB, int D, int NACC, bool VALUE, typename M, typename XV>
+__device__ __forceinline__ void walk_batch(float (&acc)[NACC], const M (&mw)[NB], const char* wlb, const XV& xval) {
+  if constexpr (U < NB) {
+    walk_position<IA, IB0 + U, D, NACC, VALUE>(acc, mw[U], wlb, xval);
+    walk_batch<IA, IB0, U + 1, NB, D, NACC, VALUE, M>(acc, mw, wlb, xval);
+  }
+}
+
+// Positions (IA, IB .. NCOL - 1), words read eight at a time from
+// word(ia, ib) (the channel word of window position (input row ia, column
+// ib)) so that their scalar reads overlap.
+template <int IA, int IB, int NCOL, int D, int NACC, bool VALUE, typename M, typename WF, typename XV>
+__device__ __forceinline__ void walk_row(float (&acc)[NACC], const WF& word, const char* wlb, const XV& xval) {
+  if constexpr (IB < NCOL) {
+    constexpr int NB = (NCOL - IB) < 8 ? (NCOL - IB) : 8;
+    M mw[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) mw[u] = word(IA, IB + u);
+    walk_batch<IA, IB, 0, NB, D, NACC, VALUE, M>(acc, mw, wlb, xval);
+    walk_row<IA, IB + NB, NCOL, D, NACC, VALUE, M>(acc, word, wlb, xval);
+  }
+}
+
+// Rows IA .. 2 of the window; row 0 is skipped unless row0, row 2 unless
+// row2 (rows outside the frame).
+template <int IA, int NCOL, int D, int NACC, bool VALUE, typename M, typename WF, typename XV>
+__device__ __forceinline__ void walk_window(float (&acc)[NACC], const WF& word, const char* wlb, const XV& xval,
+                                            bool row0, bool row2) {
+  if constexpr (IA < 3) {
+    if ((IA != 0 || row0) && (IA != 2 || row2)) walk_row<IA, 0, NCOL, D, NACC, VALUE, M>(acc, word, wlb, xval);
+    walk_window<IA + 1, NCOL, D, NACC, VALUE, M>(acc, word, wlb, xval, row0, row2);
+  }
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
