@@ -359,8 +359,8 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
     if (rc != hipSuccess) return hip_fail(rc, "conv_mfma launch");
     return SF_OK;
   }
-  if (sf::rows_applicable(a)) {
-    rc = sf::launch_conv_rows(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
+  if (sf::band_applicable(a)) {
+    rc = sf::launch_conv_band(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
     if (rc != hipSuccess) return hip_fail(rc, "conv_rows launch");
     return SF_OK;
   }

@@ -89,12 +89,13 @@ int launch_tiles(const TilesArgs& a, hipStream_t stream);
 int launch_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 int launch_conv_lif(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
-// Row-tile scatter Stage 2 (3x3 s1, C_in <= 64, frame width 32 or 56).
-bool rows_applicable(const ConvArgs& a);
-int launch_conv_rows(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+// Row-band Stage 2 from the bitmap (3x3 s1, C_in <= 64, frame width 32),
+// lane = output channel.
+bool band_applicable(const ConvArgs& a);
+int launch_conv_band(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
 
-// Stage 1 fused into the row-tile Stage 2 (3x3 s1, C_in <= 64, frame width
-// 32): reads x directly (a.bits / a.flags unused); bit = |x| >= cutoff.
+// The same walk with Stage 1 fused in (3x3 s1, C_in <= 64, frame width 32):
+// reads x directly (a.bits / a.flags unused); bit = |x| >= cutoff.
 bool rows_fused_applicable(const ConvArgs& a);
 int launch_conv_rows_fused(const ConvArgs& a, int in_dtype, int out_dtype, float cutoff, hipStream_t stream);
 

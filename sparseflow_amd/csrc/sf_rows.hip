@@ -1,187 +1,12 @@
-// Stage 2, row-tile scatter formulation: 3x3 stride-1 convolutions whose
-// weights for 64 output channels fit in LDS (C_in <= 64) on frames of width
-// 32 (the small-frame case, where one 64-pixel pixel tile per wavefront would
-// leave most of the chip idle).
-//
-// One wavefront owns one output row of one frame for 64 output channels
-// (lane = output channel, one accumulator register per output pixel).  The
-// weights of the workgroup's 64-channel group stay in LDS for the whole
-// (persistent) launch.  The wavefront walks the spike bitmap of the three
-// input rows on the scalar unit (walk_window): every active (ci, ih, iw)
-// contributes weight rows (ci, kh = ih - oh + 1, kw) to output columns
-// iw + 1 - kw, and because the input position is a compile-time loop index,
-// every target accumulator is a fixed register.  Each weight row is read
-// from LDS at an immediate offset.  The finished row is transposed in registers (DPP row shifts and
-// quad permutes) so that each store instruction writes whole frame rows of
-// 64/QP channels as float4 runs.
-//
-// Output element (co, oh, ow) = bias[co] + its taps summed by one lane in the
-// order (input row, input column, ci): deterministic from run to run.
-// Replaces the reference's sparse_conv3x3s1_nhwc_kernel_8x8/8x16
-// (Kernels/conv2d.py:564-724) for these shapes.
+// Stage 2, K-chunked row-band formulation for 3x3 stride-1 convolutions on
+// 28- and 14-wide frames whose weights do not fit LDS (C_in > 64): lane =
+// output channel, weights streamed through LDS in chunks of 32 input
+// channels (k_conv_rows_kc below).
 #include "sf_tile.h"
 
 namespace sf {
 
 namespace {
-
-
-// Word of halo position p (lane p & 63 of v0 for p < 64, else of v1) on the
-// scalar unit; p is a compile-time constant once the walks are unrolled.
-template <typename M>
-__device__ __forceinline__ M rl_word(M v0, M v1, int p) {
-  const M v = p < 64 ? v0 : v1;
-  if constexpr (sizeof(M) == 8) {
-    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, p & 63);
-    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), p & 63);
-    return ((M)hi << 32) | lo;
-  } else {
-    return __builtin_amdgcn_readlane(v, p & 63);
-  }
-}
-
-// Channel word of window position (input row oh - 1 + ia, column ib): lane
-// p & 63 of v0 (p < 64) or v1, p = ia * W + ib, read on the scalar unit.
-template <int W, typename M>
-struct RowWords {
-  M v0, v1;
-  __device__ __forceinline__ M operator()(int ia, int ib) const { return rl_word<M>(v0, v1, ia * W + ib); }
-};
-
-// x(ci, input row oh - 1 + ia, column ib) of the value path; xr = element
-// offset of row oh - 1 within a channel plane.
-template <int W, typename TIn>
-struct RowValues {
-  const TIn* __restrict__ xf;
-  int64_t xr;
-  int hw;
-  __device__ __forceinline__ float operator()(int ci, int ia, int ib) const {
-    return to_f32<TIn>(xf[(int64_t)ci * hw + xr + ia * W + ib]);
-  }
-};
-
-template <int W, int QP, int CWP, bool VALUE, typename TIn>
-__device__ __forceinline__ void scatter_tile(float (&acc)[4 * QP], const ConvArgs& a,
-                                             const typename Word<CWP>::type* __restrict__ bits,
-                                             const TIn* __restrict__ x, int64_t frame, int oh, const char* wlb) {
-  typedef typename Word<CWP>::type M;
-  const M* __restrict__ fb = bits + frame * (int64_t)a.hw_in;
-  const TIn* __restrict__ xf = x + frame * (int64_t)a.c_in * a.hw_in;
-  // Words of the 3 x W window positions (rows oh-1 .. oh+1), position p in
-  // lane p & 63 of v0 / v1: two vector loads instead of batches of dependent
-  // scalar loads; rows outside the frame read as zero words.
-  const int lane = lane_id();
-  M v0 = 0, v1 = 0;
-  {
-    const int p0 = lane, p1 = 64 + lane;
-    const int ih0 = oh - 1 + p0 / W, ih1 = oh - 1 + p1 / W;
-    if (p0 < 3 * W && ih0 >= 0 && ih0 < a.h_in) v0 = fb[(int64_t)(oh - 1) * W + p0];
-    if (p1 < 3 * W && ih1 >= 0 && ih1 < a.h_in) v1 = fb[(int64_t)(oh - 1) * W + p1];
-  }
-  walk_window<0, W, 1, 4 * QP, VALUE, M>(acc, RowWords<W, M>{v0, v1}, wlb,
-                                          RowValues<W, TIn>{xf, (int64_t)(oh - 1) * W, a.hw_in}, oh >= 1,
-                                          oh + 1 < a.h_in);
-}
-
-// OR of the non-binary chunk flags covering input rows oh-1 .. oh+1.
-__device__ __forceinline__ bool rows_value_path(const ConvArgs& a, const uint32_t* __restrict__ flags, int64_t frame,
-                                                int oh) {
-  const int ih_a = max(0, oh - 1), ih_b = min(a.h_in - 1, oh + 1);
-  const int64_t c_a = ((int64_t)ih_a * a.w_in) / a.chunk;
-  const int64_t c_b = ((int64_t)ih_b * a.w_in + a.w_in - 1) / a.chunk;
-  const uint32_t* __restrict__ fl = flags + frame * a.chunks_per_frame;
-  uint32_t f = 0u;
-  for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
-  return f != 0u;
-}
-
-// The bitmap, flags, x and weights are passed as separate restrict-qualified
-// arguments so that their uniform loads compile to scalar (SMEM) loads.
-// NWR wavefronts per workgroup: 16, or 4 when 16-wave workgroups would leave
-// CUs idle (few rows: the weights are then loaded by more workgroups).
-template <typename TIn, typename TOut, int W, int CWP, int NWR>
-__global__ __launch_bounds__(64 * NWR) void k_conv_rows(ConvArgs a, const uint32_t* __restrict__ bits,
-                                                               const uint32_t* __restrict__ flags,
-                                                               const TIn* __restrict__ x, const float* __restrict__ wt,
-                                                               const float* __restrict__ bias_p, TOut* __restrict__ y,
-                                                               int groups, int krows) {
-  typedef typename Word<CWP>::type M;
-  constexpr int QP = W <= 32 ? 8 : 16;  // quad slots per row (power of two >= W/4)
-  extern __shared__ __align__(16) char smem[];
-  float* wl = reinterpret_cast<float*>(smem);
-  const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = blockIdx.x % groups;
-  const int co0 = grp * 64;
-  // Weights straight from global memory into LDS (direct loads, 1 KB = four
-  // 64-channel rows per wavefront instruction, all in flight; 16-byte pieces
-  // of a row need C_out % 4 == 0); columns past C_out are then zeroed.
-  // Otherwise eight loads in flight per thread through registers.
-  if (a.c_out % 4 != 0) {
-    const int nw = krows * 64;
-    const int c = threadIdx.x & 63;  // the stride is a multiple of 64
-    const bool cok = co0 + c < a.c_out;
-    const int cc = cok ? co0 + c : 0;
-    for (int i0 = threadIdx.x; i0 < nw; i0 += 64 * NWR * 8) {
-      float v[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = i0 + 64 * NWR * u;
-        const int r = (i < nw ? i : 0) >> 6;
-        v[u] = wt[(int64_t)r * a.c_out + cc];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = i0 + 64 * NWR * u;
-        if (i < nw) wl[i] = cok ? v[u] : 0.f;
-      }
-    }
-  } else {
-    const int units = (krows + 3) / 4;
-    for (int u = wave; u < units; u += NWR) {
-      const int r = u * 4 + (lane >> 4);
-      const int col = co0 + 4 * (lane & 15);
-      const float* src = (r < krows && col < a.c_out) ? wt + (int64_t)r * a.c_out + col : wt;
-      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(smem + u * 1024), 16, 0, 0);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    if (co0 + 64 > a.c_out) {
-      __syncthreads();
-      for (int i = threadIdx.x; i < krows * 64; i += 64 * NWR)
-        if (co0 + (i & 63) >= a.c_out) wl[i] = 0.f;
-    }
-  }
-  __syncthreads();
-  const char* wlb = smem + lane * 4;
-  const float bias = (bias_p != nullptr && co0 + lane < a.c_out) ? bias_p[co0 + lane] : 0.f;
-  const int rows_total = (int)(a.n * a.h_out);
-  const int wpg = (int)(gridDim.x / groups) * NWR;
-  const int q = lane & (QP - 1);
-  const int cbase = lane & ~(QP - 1);
-  for (int t = (int)(blockIdx.x / groups) * NWR + wave; t < rows_total; t += wpg) {
-    const int frame = t / a.h_out;
-    const int oh = t - frame * a.h_out;
-    float acc[4 * QP];
-#pragma unroll
-    for (int i = 0; i < 4 * QP; ++i) acc[i] = i < W ? bias : 0.f;
-    const M* mbits = reinterpret_cast<const M*>(bits);
-    if (rows_value_path(a, flags, frame, oh)) scatter_tile<W, QP, CWP, true, TIn>(acc, a, mbits, x, frame, oh, wlb);
-    else scatter_tile<W, QP, CWP, false, TIn>(acc, a, mbits, x, frame, oh, wlb);
-    butterfly<1, QP>(acc, lane);
-    butterfly<2, QP>(acc, lane);
-    butterfly<4, QP>(acc, lane);
-    if constexpr (QP == 16) butterfly<8, QP>(acc, lane);
-    // Slot k of lane L now holds output channel (L & ~(QP-1)) | k, columns 4*(L & (QP-1)) .. +3.
-    if (4 * q < W) {
-      TOut* yr = y + ((int64_t)frame * a.c_out + co0 + cbase) * a.hw_out + oh * W + 4 * q;
-#pragma unroll
-      for (int k = 0; k < QP; ++k) {
-        if (co0 + cbase + k < a.c_out)
-          store4<TOut>(yr + (int64_t)k * a.hw_out, acc[4 * k], acc[4 * k + 1], acc[4 * k + 2], acc[4 * k + 3]);
-      }
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // K-chunked variant for layers whose weights do not fit LDS (C_in > 64).
@@ -415,32 +240,6 @@ int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stre
   return (int)hipGetLastError();
 }
 
-template <typename TIn, typename TOut, int W, int CWP, int NWR>
-int launch_rows_t(const ConvArgs& a, hipStream_t stream) {
-  const int groups = (a.c_out + 63) / 64;
-  const int krows = a.c_in * 9;
-  const size_t lds = (size_t)((krows + 3) / 4) * 1024;  // whole 1 KB load units
-  const int64_t rows_total = a.n * (int64_t)a.h_out;
-  const int64_t need = (rows_total + NWR - 1) / NWR;
-  const int per_group = (int)(need < num_cus() ? need : num_cus());
-  const int grid = groups * (per_group > 0 ? per_group : 1);
-  constexpr auto kern = k_conv_rows<TIn, TOut, W, CWP, NWR>;
-  const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
-  if (e != (int)hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NWR), lds, stream, a, a.bits, a.flags,
-                     static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, krows);
-  return (int)hipGetLastError();
-}
-
-template <typename TIn, typename TOut>
-int launch_rows_d(const ConvArgs& a, hipStream_t stream) {
-  const int groups = (a.c_out + 63) / 64;
-  const bool few = a.n * (int64_t)a.h_out * groups < (int64_t)kRowsWaves * num_cus();
-  if (few) return a.cwp == 1 ? launch_rows_t<TIn, TOut, 32, 1, 4>(a, stream) : launch_rows_t<TIn, TOut, 32, 2, 4>(a, stream);
-  return a.cwp == 1 ? launch_rows_t<TIn, TOut, 32, 1, kRowsWaves>(a, stream)
-                    : launch_rows_t<TIn, TOut, 32, 2, kRowsWaves>(a, stream);
-}
-
 }  // namespace
 
 namespace {
@@ -458,12 +257,6 @@ int num_cus() {
   return g_num_cus[dev];
 }
 
-bool rows_applicable(const ConvArgs& a) {
-  return a.k == 3 && a.s == 1 && a.p == 1 && a.c_in <= 64 && a.cwp <= 2 && a.h_out == a.h_in &&
-         a.w_out == a.w_in && a.w_out == 32 && a.n * (int64_t)a.h_out < (1ll << 30) &&
-         (int64_t)a.c_in * 9 * 64 * 4 <= kMaxLdsBytes;
-}
-
 bool rows_kc_applicable(const ConvArgs& a) {
   return a.k == 3 && a.s == 1 && a.p == 1 && a.h_out == a.h_in && a.w_out == a.w_in &&
          (a.w_out == 28 || a.w_out == 14) && a.c_out % 4 == 0 && a.hw_out % 4 == 0 &&
@@ -475,18 +268,6 @@ int launch_conv_rows_kc(const ConvArgs& a, int in_dtype, int out_dtype, hipStrea
   const int rc = a.w_out == 28 ? launch_kc_t<2, 28>(a, in_dtype, out_dtype, stream)
                                : launch_kc_t<4, 14>(a, in_dtype, out_dtype, stream);
   timing_end(K_ROWS_KC, stream);
-  return rc;
-}
-
-int launch_conv_rows(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
-  timing_begin(K_ROWS, stream);
-  int rc;
-  if (in_dtype == SF_F32) rc = launch_rows_d<float, float>(a, stream);
-  else if (in_dtype == SF_F16) rc = out_dtype == SF_F32 ? launch_rows_d<__half, float>(a, stream)
-                                                        : launch_rows_d<__half, __half>(a, stream);
-  else rc = out_dtype == SF_F32 ? launch_rows_d<__hip_bfloat16, float>(a, stream)
-                                : launch_rows_d<__hip_bfloat16, __hip_bfloat16>(a, stream);
-  timing_end(K_ROWS, stream);
   return rc;
 }
 

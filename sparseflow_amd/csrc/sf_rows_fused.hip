@@ -24,7 +24,8 @@
 //     registers for compile-time ia, ib.  Non-binary blocks multiply by x.
 //  3. Each lane stores its 8 output columns as two 16-byte runs.
 // Every output is bias + its taps summed in the order (input row, input
-// column, ci), the order of k_conv_rows: the two kernels agree bit for bit.
+// column, ci), the order of k_conv_band (the same walk from the bitmap):
+// the two kernels agree bit for bit.
 // Replaces the reference's prescan + sparse_conv3x3s1_nhwc_kernel_8x8 pair
 // (Kernels/conv2d.py:564-643, 986) for these shapes.
 #include "sf_tile.h"

@@ -1,7 +1,7 @@
-"""Row-tile scatter Stage 2 (3x3 stride 1, C_in <= 64, frame width 32), in
-its two forms: the two-stage path (k_pack, then k_conv_rows on the bitmap;
-the path of a handed spike map) and the fused kernel k_conv_rows_fused
-(prescan inside the conv, the path of sf_conv2d_forward).
+"""Row-band Stage 2 (3x3 stride 1, C_in <= 64, frame width 32), in its two
+input forms: from the bitmap (k_pack, then k_conv_band -- the path of a
+handed spike map) and from x (k_conv_rows_fused, the prescan fused in --
+the path of sf_conv2d_forward).
 
 Same bar as the gather kernel: fp32 within 1e-4 abs + 1e-4 rel of float64
 F.conv2d on the spike-masked input, fp16/bf16 within 1e-2, bit-identical
@@ -82,7 +82,7 @@ CASES = [
     (2, 48, 9, 32, 200),    # several output-channel groups, ragged last group
     (1, 64, 32, 32, 128),   # two full groups
     (3, 20, 6, 32, 30),     # C_out % 4 != 0: weights staged through registers
-    (70, 64, 30, 32, 64),   # more row blocks than CUs (the fused kernel loops), last block half full
+    (70, 64, 30, 32, 64),   # more row blocks than CUs (the kernel loops), last block half full
 ]
 
 
@@ -100,27 +100,29 @@ def test_rows_fp32_matches_dense(case, density):
     assert native_loaded()
 
 
-def test_rows_all_ones_input():
+@pytest.mark.parametrize("width", [32])
+def test_rows_all_ones_input(width):
     # Every tap active: the scalar walk visits all 64 channel bits of every
     # input position.
-    x = torch.ones(2, 64, 6, 32)
+    x = torch.ones(2, 64, 6, width)
     w = _weights(64, 64, seed=9)
-    announce("rows all-ones")
+    announce(f"rows all-ones w{width}")
     y = _both(x.to(DEV), w.to(DEV), None)
     ok, err, _ = close(y, oconv.conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
     assert ok, f"max abs err {err}"
 
 
-def test_rows_value_path_only_where_flagged():
+@pytest.mark.parametrize("width", [32])
+def test_rows_value_path_only_where_flagged(width):
     # Non-binary values in a few rows of one frame: those tiles take the
     # multiply path, the rest stay on the add path.
     g = torch.Generator().manual_seed(4)
-    x = spikes((3, 64, 32, 32), 0.05, seed=6)
-    x[1, :, 10:12] = x[1, :, 10:12] * torch.randn(64, 2, 32, generator=g)
-    x[2, 5, 31, 31] = -2.5
+    x = spikes((3, 64, 20, width), 0.05, seed=6)
+    x[1, :, 10:12] = x[1, :, 10:12] * torch.randn(64, 2, width, generator=g)
+    x[2, 5, 19, width - 1] = -2.5
     x[0, 0, 0, 0] = 3e-7       # below the activity threshold: dropped
     w = _weights(64, 64, seed=10)
-    announce("rows value path")
+    announce(f"rows value path w{width}")
     y = _both(x.to(DEV), w.to(DEV), None)
     ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
     assert ok, f"max abs err {err}"

@@ -65,7 +65,7 @@ def test_rows_kc_fp32_matches_dense(case, density):
     b = torch.randn(Co, generator=torch.Generator().manual_seed(3)) * 0.1
     y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV))
     # The pixel-tile kernel takes odd planes and C_in <= 128 (its weights then
-    # stay resident in LDS); the row-band kernel the rest.
+    # stay resident in LDS); the K-chunked row kernel the rest.
     expect = "conv_px3" if (H * W) % 4 or C <= 128 else "conv_rows_kc"
     assert expect in kernels and len(kernels) == 2, kernels  # prescan_pack + one conv kernel
     ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
