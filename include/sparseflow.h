@@ -131,10 +131,12 @@ int sf_prescan_tiles(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in,
 
 /* Sparse conv over a bitmap produced by sf_prescan_pack for the same x.
  * Binary chunks add weight rows; chunks flagged non-binary read x and FMA.
- * bias may be NULL.  Kernel choice, by shape: 3x3 stride 1 with c_in <= 64
- * on frames of width 32 runs the row-tile scatter kernel ("conv_rows"); 3x3
- * stride 1 on frames of width 28 or 14 with c_out and h*w multiples of 4 runs
- * the K-chunked row-tile kernel ("conv_rows_kc"); other 3x3 (stride 1 or 2)
+ * bias may be NULL.  Kernel choice, by shape: 3x3 with c_in * 9 <= 32 and
+ * fp32 input (an image stem) runs the matrix-core kernel ("conv_mfma"); 3x3
+ * stride 1 with c_in <= 64 on frames of width 32 runs the row-band kernel
+ * ("conv_rows"); 3x3 stride 1 on frames of width 28 or 14 with c_out and h*w
+ * multiples of 4 runs the K-chunked row kernel ("conv_rows_kc") unless the
+ * pixel-tile kernel keeps its weights resident; other 3x3 (stride 1 or 2)
  * with c_out a multiple of 4 runs the pixel-tile kernel ("conv_px3"); 1x1
  * stride 1 with c_out a multiple of 4 runs the flat-tile kernel
  * ("conv_flat"); every other supported shape runs the gather kernel
@@ -145,7 +147,10 @@ int sf_conv2d_sparse(const sf_conv_desc* desc, const uint32_t* bits,
                      const uint32_t* flags, const void* x, const float* wt,
                      const float* bias, void* y, void* stream);
 
-/* Stage 1a + Stage 2 in one call; the bitmap lives in `workspace`.
+/* Stage 1a + Stage 2 in one call; the bitmap lives in `workspace`.  3x3
+ * stride-1 layers with c_in <= 64 on 32-wide frames (other than an image
+ * stem) run as one launch with the prescan fused into the conv
+ * ("conv_rows_fused"; the workspace is then unused).
  * Replaces sparse_conv2d_forward's device work (Kernels/conv2d.py:893-1178). */
 int sf_conv2d_forward(const sf_conv_desc* desc, const void* x, const float* wt,
                       const float* bias, float threshold, void* workspace,
@@ -342,7 +347,7 @@ int sf_spike_attention(const void* q, const void* k, const void* v,
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
  * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep",
  * "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
- * "linear_mfma", "bmm_mfma", "conv_lif_flat").
+ * "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma", "conv_rows_fused").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

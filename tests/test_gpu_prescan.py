@@ -187,3 +187,49 @@ def test_golden_prescan_fixture():
         np.testing.assert_array_equal(tc.cpu().numpy(), g[f"tc{i}"])
         bits, _ = _lib.prescan_pack(x.to(DEV), 1e-6)
         np.testing.assert_array_equal(bits_numpy(bits, n, h * w, _lib.words_per_pixel(c)), g[f"bits{i}"])
+
+
+def test_nan_masks_only_its_own_element():
+    # Documented divergence from the reference: its metadata cascade takes a
+    # max-pool over each channel group's window, which propagates a NaN and
+    # reads the whole group as inactive (Kernels/_prescan_common.py:32-45,
+    # 167-188).  Here the bit of each element is |x| >= cutoff, false for a
+    # NaN, so the NaN element alone is inactive: the other channels of its
+    # pixel and of its group, and its channel at other pixels, keep their
+    # bits; the NaN marks its pixel chunk non-binary; the tile metadata keeps
+    # the group live; and the convolution gives the output of the input with
+    # that element zeroed.
+    from oracle import conv as oconv
+
+    n, c, h, w = 2, 64, 8, 8
+    x = torch.zeros(n, c, h, w)
+    x[1, 0:16, 3, 4] = 1.0          # the NaN's whole 16-channel group, same pixel
+    x[1, 5, 3, 5] = 1.0             # the NaN's channel at the next pixel
+    x[1, 5, 3, 4] = float("nan")
+    announce("pack NaN element")
+    xd = x.to(DEV)
+    bits, flags = _lib.prescan_pack(xd, 1e-6)
+    torch.cuda.synchronize()
+    got = bits_numpy(bits, n, h * w, 2)
+    p = 3 * w + 4
+    assert got[1, p, 0] == 0xFFFF & ~(1 << 5)      # channels 0-15 but 5
+    assert got[1, p + 1, 0] == 1 << 5
+    np.testing.assert_array_equal(got, op.bitmap(x.numpy(), 1e-6))
+    chunk = _lib.chunk_pixels(n, c, h, w)
+    cpf = -(-(h * w) // chunk)
+    f = flags[: n * cpf].cpu().numpy().reshape(n, cpf)
+    assert f[1, p // chunk] != 0 and not f[0].any()
+
+    # Tile metadata: the group of channels 0-15 stays live in the NaN's tile.
+    tc, ag = pc.build_rf_prescan_metadata(xd.permute(0, 2, 3, 1), (h, w), 3, 1, 1, (8, 8), 16, 4, 1e-6)
+    assert ag.cpu().tolist() == [0, 1] and tc.cpu().tolist() == [0, 1]
+
+    # The convolution: the NaN element contributes nothing.
+    from sparseflow_amd.Kernels.conv2d import sparse_conv2d_forward
+
+    g = torch.Generator().manual_seed(31)
+    wgt = torch.randn(16, c, 3, 3, generator=g) * 0.05
+    y = sparse_conv2d_forward(xd, wgt.to(DEV), None, kernel_size=3, stride=1, padding=1)[0]
+    ref = oconv.conv2d_ref(torch.nan_to_num(x, nan=0.0), wgt, None, 1, 1)
+    assert torch.isfinite(y).all()
+    assert torch.allclose(y.cpu().double(), ref, atol=1e-5, rtol=1e-5)
