@@ -170,7 +170,8 @@ __global__ __launch_bounds__(64 * kBandWaves) void k_conv_band(ConvArgs a, const
   float* wl = reinterpret_cast<float*>(smem);
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = blockIdx.x % groups;
+  const int blk = xcd_local_block((int)blockIdx.x, (int)gridDim.x);
+  const int grp = blk % groups;
   const int co0 = grp * 64;
   const bool direct = a.c_out % 4 == 0;
   const int hw = a.hw_in;
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(64 * kBandWaves) void k_conv_band(ConvArgs a, const
 
   // The weights stream in first; the first block's words follow.
   band_stage_weights(smem, wt, krows, a.c_out, co0, wave, lane, direct);
-  int64_t b = blockIdx.x / groups;
+  int64_t b = blk / groups;
   M nvw = 0;
   bool nvalue = false;
   if (b < nblocks) {

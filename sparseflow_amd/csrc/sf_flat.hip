@@ -133,7 +133,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
   extern __shared__ __align__(16) char smem[];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = blockIdx.x % groups;
+  const int blk = xcd_local_block((int)blockIdx.x, (int)gridDim.x);
+  const int grp = blk % groups;
   const int co0 = grp * 64;
   const int hw = a.hw_in;
   const int tpf = (hw + 63) / 64;
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
   }
   // Passes of kRowsWaves tiles.  With more than two chunks every wavefront
   // takes part in every barrier, including those of a pass past the end.
-  for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
+  for (int pass = (blk / groups); pass * kRowsWaves < total; pass += nblk) {
     const int t = pass * kRowsWaves + wave;
     const bool valid = t < total;
     const int frame = valid ? t / tpf : 0;
@@ -280,7 +281,8 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(XV ? 2
   extern __shared__ __align__(16) char smem[];
   const int lane0 = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = blockIdx.x % groups;
+  const int blk = xcd_local_block((int)blockIdx.x, (int)gridDim.x);
+  const int grp = blk % groups;
   const int co0 = grp * 64;
   const int hw = a.hw_in;
   const int tpf = (hw + 63) / 64;
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(XV ? 2
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  for (int pass = (int)(blockIdx.x / groups); pass * NWV < total; pass += nblk) {
+  for (int pass = (blk / groups); pass * NWV < total; pass += nblk) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
     const int t = pass * NWV + wave;

@@ -183,7 +183,12 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
   extern __shared__ __align__(16) char smem[];
   const int lane0 = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = blockIdx.x % groups;
+  // With 8 or more channel groups the default placement would give each XCD
+  // one group over every frame, re-reading the whole bitmap through an L2
+  // too small for it (layer4.0: 827 MB fetched for 61 MB of y + W); with
+  // fewer groups the default placement measured faster.
+  const int blk = groups >= 8 ? xcd_local_block((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+  const int grp = blk % groups;
   const int co0 = grp * CO;
   const int krows = a.c_in * 9;
   const int hwo = a.hw_out;
@@ -217,12 +222,12 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
   uint32_t wn[9];
   if constexpr (!LIF) {
     int ih0, iw0, sample;
-    if (px3_tile(a, (int)(blockIdx.x / groups) * kRowsWaves + wave, lane0, total, tpf, sample, ih0, iw0))
+    if (px3_tile(a, (blk / groups) * kRowsWaves + wave, lane0, total, tpf, sample, ih0, iw0))
       px3_load_words(wn, bits + (int64_t)sample * a.hw_in * a.cwp, a, ih0, iw0, 0);
   }
   // Passes of kRowsWaves tiles.  With streamed chunks every wavefront takes
   // part in every barrier, including those of a pass past the end.
-  for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
+  for (int pass = blk / groups; pass * kRowsWaves < total; pass += nblk) {
     // Lane-dependent addresses are recomputed in every pass rather than kept
     // live across the loop (the accumulators need the registers).
     int lane = lane0;

@@ -147,7 +147,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
   extern __shared__ __align__(16) char smem[];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = blockIdx.x % groups;
+  const int blk = (int)blockIdx.x;
+  const int grp = blk % groups;
   const int co0 = grp * 64;
   const int krows = a.c_in * 9;
   const float bias = (bias_p != nullptr && co0 + lane < a.c_out) ? bias_p[co0 + lane] : 0.f;
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
   }
   // Passes of kRowsWaves tiles.  With more than two chunks every wavefront
   // takes part in every barrier, including those of a pass past the end.
-  for (int pass = (int)(blockIdx.x / groups); pass * kRowsWaves < total; pass += nblk) {
+  for (int pass = (blk / groups); pass * kRowsWaves < total; pass += nblk) {
     const int t = pass * kRowsWaves + wave;
     const bool valid = t < total;
     const int frame = valid ? t / tpf : 0;

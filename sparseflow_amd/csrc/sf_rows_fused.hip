@@ -92,7 +92,8 @@ __global__ __launch_bounds__(64 * kFNW) void k_conv_rows_fused(ConvArgs a, const
   float* wl = reinterpret_cast<float*>(smem);
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = blockIdx.x % groups;
+  const int blk = xcd_local_block((int)blockIdx.x, (int)gridDim.x);
+  const int grp = blk % groups;
   const int co0 = grp * 64;
   const bool direct = a.c_out % 4 == 0;
 
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(64 * kFNW) void k_conv_rows_fused(ConvArgs a, const
   const int hw = a.hw_in;
   const char* wlb = smem + lane * 4;
   bool first = true;
-  for (int64_t b = blockIdx.x / groups; b < nblocks; b += bstride) {
+  for (int64_t b = blk / groups; b < nblocks; b += bstride) {
     const int64_t frame = b / bpf;
     const int oh0 = (int)(b - frame * bpf) * kFRB;
     const TIn* __restrict__ xf = x + frame * (int64_t)a.c_in * hw;

@@ -153,6 +153,19 @@ __device__ __forceinline__ void walk_window(float (&acc)[NACC], const WF& word, 
   }
 }
 
+// Workgroup index as the tile loops see it.  The chip deals workgroups to
+// its 8 XCDs round-robin (workgroup i runs on XCD i % 8), and each XCD has
+// its own L2.  Remapping i -> (i % 8) * (n / 8) + i / 8 gives each XCD one
+// contiguous range of the launch's (channel group, pass) work, so the
+// bitmap words and weight chunks its workgroups share stay in its L2
+// instead of every XCD touching every frame.  A bijection on [0, n) when
+// n % 8 == 0 (the identity otherwise): placement changes speed, never
+// results.
+__device__ __forceinline__ int xcd_local_block(int i, int n) {
+  constexpr int kXcds = 8;
+  return (n % kXcds == 0) ? (i % kXcds) * (n / kXcds) + i / kXcds : i;
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
