@@ -400,6 +400,181 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide-chunk variant of the plain conv for C_in <= 64 and 64 output channels
+// per workgroup: the weight rows of all 64 input channels (576 rows of 272
+// bytes, 156.7 KB) are resident, and each lane walks its nine taps'
+// 64-channel words in one pass instead of two 32-channel chunks.  A tile's
+// round count is its busiest pixel's spike count; over 64 channels at once
+// it is ~19% below the sum over two 32-channel chunks (the maximum over a
+// tile's lanes grows more slowly than the mean).  Output element (co, oh,
+// ow) = bias[co] + its active taps summed by one lane in (tap, ci) order.
+// ---------------------------------------------------------------------------
+constexpr int kPx3wRows = 64 * 9;
+constexpr int kPx3wUnits = (kPx3wRows * 17 + 63) / 64;  // 1 KB load units
+constexpr int kPx3wBytes = kPx3wUnits * 1024;           // 156,672
+
+// Direct-to-LDS loads of the 576 rows (padded to 17 pieces of 16 bytes):
+// pads, rows past C_in and channels past C_out read a valid but unrelated
+// address whose values are never used.
+__device__ __forceinline__ void load_rows_px3w(char* buf, const float* __restrict__ wt, int krows, int c_out, int co0,
+                                               int wave, int lane) {
+  for (int u = wave; u < kPx3wUnits; u += kRowsWaves) {
+    const int pos = u * 64 + lane;
+    const int r = pos / 17, q = pos - r * 17;
+    const int col = co0 + 4 * q;
+    const float* src = (q < 16 && r < krows && col < c_out) ? wt + (int64_t)r * c_out + col : wt;
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+  }
+}
+
+// Channel words 0 and 1 (channels 0-31, 32-63) of the lane's nine taps (0
+// outside the frame; word 1 is 0 with one word per pixel), bf = the frame's
+// bitmap, through one buffer resource as in px3_load_words.
+__device__ __forceinline__ void px3w_load_words(uint32_t (&lo)[9], uint32_t (&hi)[9], const uint32_t* __restrict__ bf,
+                                                const ConvArgs& a, int ih0, int iw0) {
+  const uint32_t frame_bytes = (uint32_t)a.hw_in * (uint32_t)a.cwp * 4u;
+  const auto rs = buf_rsrc(bf, frame_bytes);
+#pragma unroll
+  for (int tp = 0; tp < 9; ++tp) {
+    const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
+    const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
+    const uint32_t off = in ? (uint32_t)(ih * a.w_in + iw) * (uint32_t)a.cwp * 4u : 0x80000000u;
+    lo[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
+    hi[tp] = a.cwp == 2 ? __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(off + 4u), 0, 0) : 0u;
+  }
+}
+
+template <typename TIn>
+__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const uint32_t* __restrict__ bits,
+                                                               const uint32_t* __restrict__ flags,
+                                                               const TIn* __restrict__ x, const float* __restrict__ wt,
+                                                               const float* __restrict__ bias_p, void* __restrict__ y,
+                                                               int groups, int out_dtype) {
+  extern __shared__ __align__(16) char smem[];
+  __shared__ float s_seed[64];
+  const int lane0 = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = groups >= 8 ? xcd_local_block((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+  const int grp = blk % groups;
+  const int co0 = grp * 64;
+  const int hwo = a.hw_out;
+  const int tpf = (hwo + 63) / 64;
+  const int total = (int)a.n * tpf;
+  const int nblk = (int)(gridDim.x / groups);
+  if (threadIdx.x < 64) {
+    const int co = co0 + (int)threadIdx.x;
+    s_seed[threadIdx.x] = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
+  }
+  load_rows_px3w(smem, wt, a.c_in * 9, a.c_out, co0, wave, lane0);
+  // The first tile's words; later tiles' are requested before the previous
+  // tile's stores (the vector memory counter retires in issue order).
+  uint32_t nlo[9], nhi[9];
+  {
+    const int t = (blk / groups) * kRowsWaves + wave;
+    if (t < total) {
+      const int sample = t / tpf, p0 = (t - sample * tpf) * 64;
+      const int q = p0 + min(lane0, hwo - p0 - 1);
+      const int oh = q / a.w_out, ow = q - oh * a.w_out;
+      px3w_load_words(nlo, nhi, bits + (int64_t)sample * a.hw_in * a.cwp, a, oh * a.s - 1, ow * a.s - 1);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wavefront's direct weight loads have landed
+  __syncthreads();
+  for (int pass = blk / groups; pass * kRowsWaves < total; pass += nblk) {
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int t = pass * kRowsWaves + wave;
+    const bool valid = t < total;
+    const int sample = valid ? t / tpf : 0;
+    const int p0 = valid ? (t - sample * tpf) * 64 : 0;
+    const int npx = min(64, hwo - p0);
+    const bool mine = valid && lane < npx;
+    const int q = p0 + min(lane, npx - 1);
+    const int oh = q / a.w_out, ow = q - (q / a.w_out) * a.w_out;
+    const int ih0 = oh * a.s - 1, iw0 = ow * a.s - 1;
+    int hwo_t = hwo, c_out_t = a.c_out;
+    asm volatile("" : "+s"(hwo_t), "+s"(c_out_t));
+    const int nco = min(64, c_out_t - co0);
+    float acc[64];
+#pragma unroll
+    for (int co = 0; co < 64; ++co) acc[co] = s_seed[co];
+    bool value = false;
+    if (valid) {
+      const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
+      value = rows_value_path(a, flags, sample, oh_a * a.s - 1, oh_b * a.s + 1);
+    }
+    if (mine) {
+      uint32_t wl[9], wh[9];
+#pragma unroll
+      for (int tp = 0; tp < 9; ++tp) {
+        wl[tp] = nlo[tp];
+        wh[tp] = nhi[tp];
+      }
+      // Opaque to the optimiser: a select between array elements would
+      // otherwise be folded into an indexed load from scratch memory.
+      asm volatile("" : "+v"(wl[0]), "+v"(wl[1]), "+v"(wl[2]), "+v"(wl[3]), "+v"(wl[4]), "+v"(wl[5]), "+v"(wl[6]),
+                   "+v"(wl[7]), "+v"(wl[8]));
+      asm volatile("" : "+v"(wh[0]), "+v"(wh[1]), "+v"(wh[2]), "+v"(wh[3]), "+v"(wh[4]), "+v"(wh[5]), "+v"(wh[6]),
+                   "+v"(wh[7]), "+v"(wh[8]));
+      uint32_t nz = 0u;
+#pragma unroll
+      for (int tp = 0; tp < 9; ++tp) nz |= ((wl[tp] | wh[tp]) != 0u ? 1u : 0u) << tp;
+      const TIn* __restrict__ xf = x + (int64_t)sample * a.c_in * a.hw_in;
+      uint64_t m = 0ull;
+      int tap = 0;
+      // Per-lane cursor over (tap, ci): the wavefront loops while any lane
+      // has spikes left.
+      while ((m != 0ull) || (nz != 0u)) {
+        if (m == 0ull) {
+          tap = __builtin_ctz(nz);
+          nz &= nz - 1u;
+          m = ((uint64_t)px3_select(wh, tap) << 32) | px3_select(wl, tap);
+        }
+        const int bit = __builtin_ctzll(m);
+        m &= m - 1ull;
+        float xv = 1.f;
+        if (value) {
+          const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+          xv = to_f32<TIn>(xf[(int64_t)bit * a.hw_in + ih * a.w_in + iw]);
+        }
+        px3_add_row<64>(acc, smem, bit * 9 + tap, xv);
+      }
+    }
+    {
+      const int tn = (pass + nblk) * kRowsWaves + wave;
+      if (tn < total) {
+        const int ns = tn / tpf, np0 = (tn - ns * tpf) * 64;
+        const int nq = np0 + min(lane, hwo - np0 - 1);
+        const int noh = nq / a.w_out, now = nq - noh * a.w_out;
+        px3w_load_words(nlo, nhi, bits + (int64_t)ns * a.hw_in * a.cwp, a, noh * a.s - 1, now * a.s - 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (mine) {
+      const int64_t yb = ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
+      if (out_dtype == SF_F16) px3_store<64>(acc, static_cast<__half*>(y) + yb, hwo_t, nco);
+      else if (out_dtype == SF_BF16) px3_store<64>(acc, static_cast<__hip_bfloat16*>(y) + yb, hwo_t, nco);
+      else px3_store<64>(acc, static_cast<float*>(y) + yb, hwo_t, nco);
+    }
+  }
+}
+
+template <typename TIn>
+int launch_px3w_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+  const int groups = (a.c_out + 63) / 64;
+  const int64_t tiles = a.n * (int64_t)((a.hw_out + 63) / 64);
+  const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
+  const int per_group = (int)(need < num_cus() ? need : num_cus());
+  const int grid = groups * (per_group > 0 ? per_group : 1);
+  constexpr auto kern = k_conv_px3w<TIn>;
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
+  if (e != (int)hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), (size_t)kPx3wBytes, stream, a, a.bits, a.flags,
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, out_dtype);
+  return (int)hipGetLastError();
+}
+
 template <typename TIn, typename TOut, int CO, bool LIF>
 int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   typedef Px3Layout<CO> LY;
@@ -432,6 +607,12 @@ int launch_px3_co(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t st
 // per slice.  (A 16-channel slice, resident up to C_in = 256, walks too
 // often: slower than streaming.)
 int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  // C_in <= 64: one 64-channel chunk, every weight row resident.
+  if (a.c_in <= 64 && a.cwp <= 2) {
+    if (in_dtype == SF_F16) return launch_px3w_t<__half>(a, out_dtype, stream);
+    if (in_dtype == SF_BF16) return launch_px3w_t<__hip_bfloat16>(a, out_dtype, stream);
+    return launch_px3w_t<float>(a, out_dtype, stream);
+  }
   const int nch = (a.c_in + kPx3Ch - 1) / kPx3Ch;
   if (nch > Px3Layout<64>::resident_chunks && nch <= Px3Layout<32>::resident_chunks)
     return launch_px3_co<32>(a, in_dtype, out_dtype, stream);
