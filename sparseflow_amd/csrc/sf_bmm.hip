@@ -147,12 +147,23 @@ int launch_bmm(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream
 // ---------------------------------------------------------------------------
 // Batched matmul on the matrix cores, for the attention shapes (A's rows
 // dense enough that every 32-wide K slice of a 16-row tile is live: q at
-// p ~ 0.1 with head_dim 32, the seq x seq scores).  One workgroup per batch:
-// B (k <= 256, n <= 256) is converted to bf16 hi + lo parts into LDS,
-// [n][kp] with k contiguous and an XOR piece swizzle; each wavefront takes
-// 16-row tiles of A, loads the tile's whole K range from HBM once, splits it
-// into bf16 hi + lo in registers, and computes every 16-column tile of C
-// with 16x16x32 MFMAs (ah.bh + ah.bl + al.bh: ~16 bits of both operands).
+// p ~ 0.1 with head_dim 32, the seq x seq scores).  Persistent workgroups of
+// four wavefronts, as many as fit on the chip, each taking batches in turn:
+//  * B (k <= 256, n <= 256) is staged in LDS as bf16 hi + lo parts,
+//    [n][kp] with k contiguous and an XOR piece swizzle.  A thread converts
+//    one 16-byte piece (8 consecutive k of one column) at a time and writes
+//    it with one ds_write_b128; pieces are handed out so that the global
+//    reads are coalesced along whichever axis of B is contiguous, and
+//    sixteen consecutive pieces land on distinct banks either way.
+//  * Each wavefront takes 16-row tiles of A (row-major, k contiguous).  The
+//    tile's whole K range is loaded into registers, split into bf16 hi + lo,
+//    and the NEXT tile of the wavefront's sequence (possibly in its next
+//    batch) is requested before the current one's MFMAs and stores, so that
+//    HBM reads stay in flight throughout.
+//  * Every 16-column tile of C takes 16x16x32 MFMAs: ah.bh + ah.bl + al.bh
+//    (~16 significant bits of both operands), the ah.bl term dropped when
+//    all of the batch's B is exact in bf16 and al.bh when all of the tile's
+//    A is (binary spikes, small counts): both are then exact zeros.
 // A elements below the activity cutoff count as zero.
 // ---------------------------------------------------------------------------
 
@@ -164,12 +175,37 @@ typedef __bf16 bmm_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float bmm_f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kBmKsMax = 8;  // kp <= 256
+constexpr int kBmWaves = 4;
 
-__device__ __forceinline__ uint16_t bm_bf16_bits(float f) {
-  const __hip_bfloat16 h = __float2bfloat16(f);
-  uint16_t u;
-  __builtin_memcpy(&u, &h, 2);
-  return u;
+typedef __bf16 bmm_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float bmm_f32x2 __attribute__((ext_vector_type(2)));
+
+// bf16 hi parts (round to nearest even) of two floats and the bf16 of their
+// remainders, one packed convert each.
+__device__ __forceinline__ void bm_split2(float x0, float x1, bmm_bf16x2& h, bmm_bf16x2& l) {
+  const bmm_f32x2 x = {x0, x1};
+  h = __builtin_convertvector(x, bmm_bf16x2);
+  const bmm_f32x2 hf = __builtin_convertvector(h, bmm_f32x2);
+  l = __builtin_convertvector(x - hf, bmm_bf16x2);
+}
+
+// Eight floats to bf16x8 hi and lo operands.
+__device__ __forceinline__ void bm_split8(const float (&v)[8], bmm_bf16x8& h, bmm_bf16x8& l) {
+  bmm_bf16x2 h0, h1, h2, h3, l0, l1, l2, l3;
+  bm_split2(v[0], v[1], h0, l0);
+  bm_split2(v[2], v[3], h1, l1);
+  bm_split2(v[4], v[5], h2, l2);
+  bm_split2(v[6], v[7], h3, l3);
+  h = __builtin_shufflevector(__builtin_shufflevector(h0, h1, 0, 1, 2, 3), __builtin_shufflevector(h2, h3, 0, 1, 2, 3),
+                              0, 1, 2, 3, 4, 5, 6, 7);
+  l = __builtin_shufflevector(__builtin_shufflevector(l0, l1, 0, 1, 2, 3), __builtin_shufflevector(l2, l3, 0, 1, 2, 3),
+                              0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ bool bm_nonzero(const bmm_bf16x8& v) {
+  uint4 u;
+  __builtin_memcpy(&u, &v, 16);
+  return (u.x | u.y | u.z | u.w) != 0;
 }
 
 // Position (bf16 elements) of element k of row r in a [rows][kp] tile whose
@@ -180,124 +216,274 @@ __device__ __forceinline__ int bm_pos(int r, int k, int kp) {
   return r * kp + sw * 8 + (k & 7);
 }
 
-template <typename T, typename TOut, int KS>
-__global__ __launch_bounds__(256) void k_bmm_mfma(BmmArgs a) {
-  extern __shared__ __align__(16) uint16_t s_b[];  // hi [npad][kp], then lo
-  const int kp = KS * 32;
-  const int npad = (a.n + 15) & ~15;
-  uint16_t* s_bh = s_b;
-  uint16_t* s_bl = s_b + npad * kp;
-  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-  const int g = lane >> 4, li = lane & 15;
-  const T* __restrict__ A = static_cast<const T*>(a.a);
-  const T* __restrict__ B = static_cast<const T*>(a.b);
-  TOut* __restrict__ C = static_cast<TOut*>(a.c);
-  const int M = a.m, K = a.k, N = a.n;
-  const int mtiles = (M + 15) / 16, ntiles = npad / 16;
-  // f32 rows of A 16-byte aligned: rows start at multiples of K floats.
-  const bool vec = sizeof(T) == 4 && (K & 3) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0;
-  for (int64_t bt = blockIdx.x; bt < a.batches; bt += gridDim.x) {
-    __syncthreads();  // the previous batch is done with s_b
-    const T* __restrict__ Bb = B + bt * a.b_stride_batch;
-    // Stage B: consecutive threads walk B's contiguous axis, sixteen loads in
-    // flight per thread (one at a time, the staging was a chain of up to a
-    // few hundred dependent global loads).
-    const bool kfast = a.b_stride_k == 1 && a.b_stride_n != 1;
-    const int nb = npad * kp;
-    constexpr int U = 16;
-    for (int i0 = tid; i0 < nb; i0 += 256 * U) {
-      float v[U];
+// Stage batch bt's B into s_bh / s_bl.  Returns nonzero in some thread when
+// any lo part is nonzero (the caller reduces it over the workgroup).
+template <typename T, int KS>
+__device__ __forceinline__ uint32_t bm_stage_b(const BmmArgs& a, int64_t bt, int npad, uint16_t* s_bh,
+                                               uint16_t* s_bl) {
+  constexpr int kPc = KS * 4;  // 8-element pieces per column
+  constexpr int kUnroll = 4;
+  const T* __restrict__ Bb = static_cast<const T*>(a.b) + bt * a.b_stride_batch;
+  const int K = a.k, N = a.n;
+  const int npieces = npad * kPc;
+  // k contiguous (a transposed view): consecutive threads take consecutive
+  // pieces of one column; else consecutive columns of one piece row.
+  const bool kfast = a.b_stride_k == 1 && a.b_stride_n != 1;
+  const bool vec4 = kfast && sizeof(T) == 4 && (a.b_stride_n & 3) == 0 && (a.b_stride_batch & 3) == 0 &&
+                    (reinterpret_cast<uintptr_t>(a.b) & 15) == 0;
+  uint32_t lo_any = 0;
+  const int tid = threadIdx.x;
+  for (int p0 = tid; p0 < npieces; p0 += 64 * kBmWaves * kUnroll) {
+    float v[kUnroll][8];
+    int col[kUnroll], pc[kUnroll];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int i = i0 + 256 * u;
-        int kk, nn;
-        if (kfast) { nn = i / kp; kk = i - nn * kp; } else { kk = i / npad; nn = i - kk * npad; }
-        v[u] = (i < nb && kk < K && nn < N) ? to_f32<T>(Bb[(int64_t)kk * a.b_stride_k + (int64_t)nn * a.b_stride_n])
-                                            : 0.f;
+    for (int u = 0; u < kUnroll; ++u) {
+      const int p = p0 + 64 * kBmWaves * u;
+      int nn, c;
+      if (kfast) {
+        nn = p / kPc;
+        c = p - nn * kPc;
+      } else {
+        c = p / npad;
+        nn = p - c * npad;
       }
+      col[u] = p < npieces ? nn : -1;
+      pc[u] = c;
+      const int k0 = c * 8;
+      const bool colok = p < npieces && nn < N;
+      if (vec4 && colok && k0 + 8 <= K) {
+        const float4* src = reinterpret_cast<const float4*>(Bb + (int64_t)nn * a.b_stride_n + k0);
+        const float4 t0 = src[0], t1 = src[1];
+        v[u][0] = t0.x; v[u][1] = t0.y; v[u][2] = t0.z; v[u][3] = t0.w;
+        v[u][4] = t1.x; v[u][5] = t1.y; v[u][6] = t1.z; v[u][7] = t1.w;
+      } else {
+        // Clamped in-bounds reads, masked after: no per-element branches.
+        const int nc = nn < N ? nn : N - 1;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int i = i0 + 256 * u;
-        if (i < nb) {
-          int kk, nn;
-          if (kfast) { nn = i / kp; kk = i - nn * kp; } else { kk = i / npad; nn = i - kk * npad; }
-          const uint16_t h = bm_bf16_bits(v[u]);
-          const uint16_t l = bm_bf16_bits(v[u] - __uint_as_float((uint32_t)h << 16));
-          const int pos = bm_pos(nn, kk, kp);
-          s_bh[pos] = h;
-          s_bl[pos] = l;
+        for (int j = 0; j < 8; ++j) {
+          const int kc = k0 + j < K ? k0 + j : K - 1;
+          const float x = to_f32<T>(Bb[(int64_t)kc * a.b_stride_k + (int64_t)nc * a.b_stride_n]);
+          v[u][j] = (colok && k0 + j < K) ? x : 0.f;
         }
       }
     }
-    __syncthreads();
-    const T* __restrict__ Ab = A + bt * (int64_t)M * K;
-    TOut* __restrict__ Cb = C + bt * (int64_t)M * N;
-    for (int mt = wave; mt < mtiles; mt += 4) {
-      const int row = mt * 16 + li;
-      const bool row_ok = row < M;
-      const T* __restrict__ ar = Ab + (int64_t)(row_ok ? row : 0) * K;
-      // The tile's whole K range: lane (li, g) holds k = 32 ks + 8 g .. +7.
-      float av[KS][8];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (col[u] < 0) continue;
+      bmm_bf16x8 h, l;
+      bm_split8(v[u], h, l);
+      lo_any |= bm_nonzero(l) ? 1u : 0u;
+      const int pos = bm_pos(col[u], pc[u] * 8, KS * 32);
+      *reinterpret_cast<bmm_bf16x8*>(&s_bh[pos]) = h;
+      *reinterpret_cast<bmm_bf16x8*>(&s_bl[pos]) = l;
+    }
+  }
+  return lo_any;
+}
+
+// Raw A values of one 16-row tile: lane (li, g) holds row 16 mt + li,
+// k = 32 ks + 8 g .. +7.  Rows past m are not read.
+template <typename T, int KS>
+__device__ __forceinline__ void bm_load_a(float (&av)[KS][8], const BmmArgs& a, int64_t bt, int mt, bool vec) {
+  const int li = lane_id() & 15, g = lane_id() >> 4;
+  const int row = mt * 16 + li;
+  const int K = a.k;
+  if (row >= a.m) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) av[ks][j] = 0.f;
+    return;
+  }
+  const T* __restrict__ ar = static_cast<const T*>(a.a) + (bt * a.m + row) * (int64_t)K;
+  if (vec) {  // K % 4 == 0: whole float4 groups are in or out
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int k0 = ks * 32 + 8 * g + 4 * h;
+        float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+        // KS = ceil(K / 32): only the last slice can reach past K.
+        if (ks < KS - 1 || k0 < K) t = *reinterpret_cast<const float4*>(ar + k0);
+        av[ks][4 * h] = t.x; av[ks][4 * h + 1] = t.y; av[ks][4 * h + 2] = t.z; av[ks][4 * h + 3] = t.w;
+      }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int k = ks * 32 + 8 * g + j;
+        const bool in = ks < KS - 1 || k < K;
+        const float x = to_f32<T>(ar[in ? k : K - 1]);
+        av[ks][j] = in ? x : 0.f;
+      }
+  }
+}
+
+// Four consecutive outputs of one row, one vector store when `vec`.
+template <typename TOut>
+__device__ __forceinline__ void bm_store4(TOut* p, const bmm_f32x4& v, float alpha, int nvalid, bool vec) {
+  if (vec && nvalid >= 4) {
+    if constexpr (sizeof(TOut) == 4) {
+      *reinterpret_cast<float4*>(p) = make_float4(v[0] * alpha, v[1] * alpha, v[2] * alpha, v[3] * alpha);
+    } else {
+      TOut h[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) h[i] = from_f32<TOut>(v[i] * alpha);
+      uint2 u;
+      __builtin_memcpy(&u, h, 8);
+      *reinterpret_cast<uint2*>(p) = u;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (i < nvalid) p[i] = from_f32<TOut>(v[i] * alpha);
+  }
+}
+
+// C tile (mt, every column tile) from the split A tile and the staged B.
+// The MFMAs compute the transposed tile, D[n][m] = sum_k B[k][n] A[m][k]
+// (B's staged [n][k] pieces are the first operand, A's registers the
+// second), so that lane (li, g) ends with row 16 mt + li, columns
+// 16 nt + 4 g .. +3 of C.  With s_c (n % 4 == 0) the wavefront collects
+// the tile's rows in LDS exactly as they lie in C, one contiguous block of
+// rows x n values, and copies it out in 16-byte pieces: whole cache lines
+// per store instead of 64-byte pieces of sixteen rows.  Else each lane
+// stores its four outputs directly.
+// blo / alo (wave-uniform): B / the A tile has nonzero lo parts.
+template <typename TOut, int KS>
+__device__ __forceinline__ void bm_tile(const bmm_bf16x8 (&ah)[KS], const bmm_bf16x8 (&al)[KS],
+                                        const uint16_t* s_bh, const uint16_t* s_bl, float* s_c, const BmmArgs& a,
+                                        int64_t bt, int mt, int ntiles, bool blo, bool alo, bool vec_out) {
+  const int lane = lane_id(), li = lane & 15, g = lane >> 4;
+  const int row = mt * 16 + li;
+  TOut* __restrict__ cr = static_cast<TOut*>(a.c) + (bt * a.m + (row < a.m ? row : 0)) * (int64_t)a.n + 4 * g;
+  // bm_pos(col, 32 ks + 8 g): the lane's piece within each 64-byte group is
+  // g ^ ((col >> 2) & 3), the same for every ks and every column tile
+  // (col advances by 16), so one base per array and immediate offsets.
+  const int lbase = li * (KS * 32) + 8 * (g ^ ((li >> 2) & 3));
+  const bmm_bf16x8* __restrict__ ph = reinterpret_cast<const bmm_bf16x8*>(s_bh + lbase);
+  const bmm_bf16x8* __restrict__ pl = reinterpret_cast<const bmm_bf16x8*>(s_bl + lbase);
+#pragma clang loop unroll(disable)
+  for (int nt = 0; nt < ntiles; ++nt) {
+    bmm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const bmm_bf16x8 bh = ph[ks * 4];  // 32 bf16 per ks
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, ah[ks], acc, 0, 0, 0);
+      if (blo) {
+        const bmm_bf16x8 bl = pl[ks * 4];
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bl, ah[ks], acc, 0, 0, 0);
+      }
+      if (alo) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, al[ks], acc, 0, 0, 0);
+    }
+    ph += 16 * KS * 4;  // 16 columns of kp bf16
+    pl += 16 * KS * 4;
+    const int c0 = nt * 16 + 4 * g;
+    if (s_c != nullptr) {
+      if (c0 < a.n) *reinterpret_cast<bmm_f32x4*>(s_c + li * a.n + c0) = acc;
+    } else if (row < a.m) {
+      bm_store4<TOut>(cr + nt * 16, acc, a.alpha, a.n - c0, vec_out);
+    }
+  }
+  if (s_c != nullptr) {
+    const int rows = a.m - mt * 16 < 16 ? a.m - mt * 16 : 16;
+    const int total = rows * a.n;  // a multiple of 4
+    TOut* __restrict__ cb = static_cast<TOut*>(a.c) + (bt * a.m + mt * 16) * (int64_t)a.n;
+    for (int e = lane * 4; e < total; e += 256)
+      bm_store4<TOut>(cb + e, *reinterpret_cast<const bmm_f32x4*>(s_c + e), a.alpha, 4, true);
+  }
+}
+
+// stage_c: each wavefront also has a 16 x n f32 C tile in LDS after B
+// (n % 4 == 0, C rows 16-byte aligned).
+template <typename T, typename TOut, int KS>
+__global__ __launch_bounds__(64 * kBmWaves) __attribute__((amdgpu_waves_per_eu(KS <= 7 ? 3 : 2)))
+void k_bmm_mfma(BmmArgs a, int stage_c) {
+  extern __shared__ __align__(16) uint16_t s_b[];  // hi [npad][kp], lo, then C tiles
+  const int npad = (a.n + 15) & ~15;
+  uint16_t* s_bh = s_b;
+  uint16_t* s_bl = s_b + npad * (KS * 32);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int mtiles = (a.m + 15) / 16, ntiles = npad / 16;
+  // f32 rows of A 16-byte aligned: rows start at multiples of K floats.
+  const bool vec = sizeof(T) == 4 && (a.k & 3) == 0 && (reinterpret_cast<uintptr_t>(a.a) & 15) == 0;
+  const bool has_tiles = wave < mtiles;
+  float* s_c = stage_c ? reinterpret_cast<float*>(s_b + 2 * npad * (KS * 32)) + wave * 16 * a.n : nullptr;
+  // Rows of C start 4-element aligned: four outputs leave as one store.
+  const bool vec_out = (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.c) & (4 * sizeof(TOut) - 1)) == 0;
+  // This wavefront's items, in order: tiles wave, wave + 4, ... of batch
+  // blockIdx.x, then of batch blockIdx.x + gridDim.x, ...  av holds the raw
+  // A of the next item to compute.
+  float av[KS][8];
+  int64_t nb = blockIdx.x;
+  int nm = wave;
+  if (has_tiles && nb < a.batches) bm_load_a<T, KS>(av, a, nb, nm, vec);
+  for (int64_t bt = blockIdx.x; bt < a.batches; bt += gridDim.x) {
+    __syncthreads();  // the previous batch is done with s_b
+    const uint32_t blo = __syncthreads_or((int)bm_stage_b<T, KS>(a, bt, npad, s_bh, s_bl));
+    if (!has_tiles) continue;
+    for (int mt = wave; mt < mtiles; mt += kBmWaves) {
+      bmm_bf16x8 ah[KS], al[KS];
+      bool alo = false;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
-        const int kk0 = ks * 32 + 8 * g;
-        if (vec && kk0 + 8 <= K) {  // two 16-byte loads
-          const float4 t0 = *reinterpret_cast<const float4*>(ar + kk0);
-          const float4 t1 = *reinterpret_cast<const float4*>(ar + kk0 + 4);
-          av[ks][0] = t0.x; av[ks][1] = t0.y; av[ks][2] = t0.z; av[ks][3] = t0.w;
-          av[ks][4] = t1.x; av[ks][5] = t1.y; av[ks][6] = t1.z; av[ks][7] = t1.w;
-        } else {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) av[ks][j] = to_f32<T>(ar[kk0 + j < K ? kk0 + j : 0]);
-        }
+        for (int j = 0; j < 8; ++j) av[ks][j] = fabsf(av[ks][j]) >= a.cutoff ? av[ks][j] : 0.f;
+        bm_split8(av[ks], ah[ks], al[ks]);
+        alo |= bm_nonzero(al[ks]);
       }
-      bmm_bf16x8 ah[KS], al[KS];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int kk = ks * 32 + 8 * g + j;
-          const float v = (row_ok && kk < K && fabsf(av[ks][j]) >= a.cutoff) ? av[ks][j] : 0.f;
-          const uint16_t h = bm_bf16_bits(v);
-          const uint16_t l = bm_bf16_bits(v - __uint_as_float((uint32_t)h << 16));
-          __bf16 hb, lb;
-          __builtin_memcpy(&hb, &h, 2);
-          __builtin_memcpy(&lb, &l, 2);
-          ah[ks][j] = hb;
-          al[ks][j] = lb;
-        }
-      for (int nt = 0; nt < ntiles; ++nt) {
-        bmm_f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const int col = nt * 16 + li;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int pos = bm_pos(col, ks * 32 + 8 * g, kp);
-          const bmm_bf16x8 bh = *reinterpret_cast<const bmm_bf16x8*>(&s_bh[pos]);
-          const bmm_bf16x8 bl = *reinterpret_cast<const bmm_bf16x8*>(&s_bl[pos]);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[ks], bh, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[ks], bl, acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[ks], bh, acc, 0, 0, 0);
-        }
-        // acc element i: row 16 mt + 4 g + i, column nt * 16 + li.
-        if (col < N) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = mt * 16 + 4 * g + i;
-            if (r < M) Cb[(int64_t)r * N + col] = from_f32<TOut>(acc[i] * a.alpha);
-          }
-        }
+      // Request the next item's A before this tile's MFMAs and stores.
+      nm += kBmWaves;
+      if (nm >= mtiles) {
+        nm = wave;
+        nb += gridDim.x;
       }
+      if (nb < a.batches) bm_load_a<T, KS>(av, a, nb, nm, vec);
+      const bool any_alo = __builtin_amdgcn_ballot_w64(alo) != 0;
+      bm_tile<TOut, KS>(ah, al, s_bh, s_bl, s_c, a, bt, mt, ntiles, blo != 0, any_alo, vec_out);
     }
   }
 }
 
+// Workgroups of k_bmm_mfma<...> that fit on one CU with `lds` bytes of
+// dynamic LDS each (cached per kernel, device and size).
+template <auto K>
+int bm_blocks_per_cu(size_t lds) {
+  static std::atomic<uint64_t> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  std::atomic<uint64_t>& slot = cache[dev & 63];
+  const uint64_t c = slot.load(std::memory_order_relaxed);
+  if (c != 0 && (c >> 8) == lds) return (int)(c & 0xff);
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, reinterpret_cast<const void*>(K), 64 * kBmWaves, lds) !=
+          hipSuccess ||
+      blocks <= 0)
+    blocks = 1;
+  if (blocks > 255) blocks = 255;
+  slot.store(((uint64_t)lds << 8) | (uint64_t)blocks, std::memory_order_relaxed);
+  return blocks;
+}
+
 template <typename T, typename TOut, int KS>
 int launch_bmm_mfma_t(const BmmArgs& a, hipStream_t stream) {
-  const size_t lds = (size_t)2 * ((a.n + 15) & ~15) * (KS * 32) * sizeof(uint16_t);
-  const int64_t cap = (int64_t)num_cus() * 8;
+  const size_t lds_b = (size_t)2 * ((a.n + 15) & ~15) * (KS * 32) * sizeof(uint16_t);
+  const size_t lds_c = (size_t)kBmWaves * 16 * a.n * sizeof(float);
+  // Stage C tiles when rows are whole 16-byte pieces and two workgroups
+  // still fit on a CU.
+  const bool vec_out = (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.c) & (4 * sizeof(TOut) - 1)) == 0;
+  const int stage_c = vec_out && lds_b + lds_c <= (size_t)80 * 1024 ? 1 : 0;
+  const size_t lds = lds_b + (stage_c ? lds_c : 0);
+  constexpr auto kern = k_bmm_mfma<T, TOut, KS>;
+  if (lds > 64 * 1024) {
+    const int e = set_lds_limit_once<kern>(80 * 1024);
+    if (e != (int)hipSuccess) return e;
+  }
+  const int64_t cap = (int64_t)num_cus() * bm_blocks_per_cu<kern>(lds);
   const int grid = (int)(a.batches < cap ? a.batches : cap);
   if (grid == 0) return (int)hipSuccess;
-  hipLaunchKernelGGL((k_bmm_mfma<T, TOut, KS>), dim3(grid), dim3(256), lds, stream, a);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kBmWaves), lds, stream, a, stage_c);
   return (int)hipGetLastError();
 }
 

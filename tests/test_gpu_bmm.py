@@ -36,6 +36,10 @@ def _run(a, b, **kw):
 CASES = [  # (batches, m, k, n)
     (1, 1, 1, 1), (3, 5, 7, 9), (48, 196, 32, 196), (48, 196, 196, 32), (4, 64, 252, 64), (2, 300, 64, 300),
     (5, 17, 130, 70), (2, 8, 40, 513),
+    # More batches than resident workgroups: each workgroup takes several in
+    # turn, and a wavefront's next tile is often in its next batch (m = 80:
+    # five row tiles over four wavefronts; m = 20: two wavefronts idle).
+    (2000, 80, 40, 24), (1500, 20, 32, 16),
 ]
 
 
@@ -68,6 +72,20 @@ def test_bmm_strided_b_equals_contiguous(kernel):
     c2, _ = _run(a, k.transpose(1, 2).contiguous(), kernel=kernel)
     assert torch.equal(c1, c2)
     ok, err, _ = close(c1, olin.bmm_ref(a.cpu(), k.cpu().transpose(1, 2)), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_bmm_general_strides_b(kernel):
+    # B with neither axis contiguous (every other column of a wider tensor).
+    a = spikes((6, 50, 70), 0.2, seed=8).to(DEV)
+    wide = torch.randn(6, 70, 66, generator=torch.Generator().manual_seed(9)).to(DEV)
+    b = wide[:, :, ::2]
+    announce(f"bmm strided B {kernel}")
+    c1, _ = _run(a, b, kernel=kernel)
+    c2, _ = _run(a, b.contiguous(), kernel=kernel)
+    assert torch.equal(c1, c2)
+    ok, err, _ = close(c1, olin.bmm_ref(a.cpu(), b.cpu()), **FP32_TOL)
     assert ok, f"max abs err {err}"
 
 
