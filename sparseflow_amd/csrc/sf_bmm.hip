@@ -150,7 +150,8 @@ int launch_bmm(const BmmArgs& a, int in_dtype, int out_dtype, hipStream_t stream
 // p ~ 0.1 with head_dim 32, the seq x seq scores).  Persistent workgroups of
 // four wavefronts, as many as fit on the chip, each taking batches in turn:
 //  * B (k <= 256, n <= 256) is staged in LDS as bf16 hi + lo parts,
-//    [n][kp] with k contiguous and an XOR piece swizzle.  A thread converts
+//    [n][kp] with k contiguous (rows padded, pieces XOR-swizzled: see
+//    bm_row / bm_pos for the bank-conflict measurement).  A thread converts
 //    one 16-byte piece (8 consecutive k of one column) at a time and writes
 //    it with one ds_write_b128; pieces are handed out so that the global
 //    reads are coalesced along whichever axis of B is contiguous, and
@@ -208,13 +209,27 @@ __device__ __forceinline__ bool bm_nonzero(const bmm_bf16x8& v) {
   return (u.x | u.y | u.z | u.w) != 0;
 }
 
-// Position (bf16 elements) of element k of row r in a [rows][kp] tile whose
-// 16-byte pieces are XOR-swizzled within each 64-byte group by (r >> 2) & 3.
-__device__ __forceinline__ int bm_pos(int r, int k, int kp) {
+// Staged B rows: kp = 32 KS bf16, padded by one 64-byte group when KS is
+// even.  Measured on gfx950 (rocprofv3 SQ_LDS_BANK_CONFLICT over
+// ds_read_b128 / ds_write_b128 patterns), 16-lane fragments over rows whose
+// stride is an odd number of 64-byte groups, with the 16-byte pieces of
+// each group XOR-swizzled by (r >> 1) & 3, read and write without bank
+// conflicts; even strides, or the swizzle by (r >> 2) & 3, do not.
+template <int KS>
+constexpr int bm_row() { return KS * 32 + (KS % 2 == 0 ? 32 : 0); }
+
+// Position (bf16 elements) of element k of row r.
+template <int KS>
+__device__ __forceinline__ int bm_pos(int r, int k) {
   const int piece = k >> 3;
-  const int sw = (piece & ~3) | ((piece & 3) ^ ((r >> 2) & 3));
-  return r * kp + sw * 8 + (k & 7);
+  const int sw = (piece & ~3) | ((piece & 3) ^ ((r >> 1) & 3));
+  return r * bm_row<KS>() + sw * 8 + (k & 7);
 }
+
+// C tile rows in LDS: n floats padded to an odd number of 16-byte pieces
+// (n % 4 == 0), which the same measurement shows conflict-free for the
+// tile's 16-byte writes.
+__host__ __device__ constexpr int bm_c_row(int n) { return ((n >> 2) & 1) ? n : n + 4; }
 
 // Stage batch bt's B into s_bh / s_bl.  Returns nonzero in some thread when
 // any lo part is nonzero (the caller reduces it over the workgroup).
@@ -273,7 +288,7 @@ __device__ __forceinline__ uint32_t bm_stage_b(const BmmArgs& a, int64_t bt, int
       bmm_bf16x8 h, l;
       bm_split8(v[u], h, l);
       lo_any |= bm_nonzero(l) ? 1u : 0u;
-      const int pos = bm_pos(col[u], pc[u] * 8, KS * 32);
+      const int pos = bm_pos<KS>(col[u], pc[u] * 8);
       *reinterpret_cast<bmm_bf16x8*>(&s_bh[pos]) = h;
       *reinterpret_cast<bmm_bf16x8*>(&s_bl[pos]) = l;
     }
@@ -346,10 +361,10 @@ __device__ __forceinline__ void bm_store4(TOut* p, const bmm_f32x4& v, float alp
 // (B's staged [n][k] pieces are the first operand, A's registers the
 // second), so that lane (li, g) ends with row 16 mt + li, columns
 // 16 nt + 4 g .. +3 of C.  With s_c (n % 4 == 0) the wavefront collects
-// the tile's rows in LDS exactly as they lie in C, one contiguous block of
-// rows x n values, and copies it out in 16-byte pieces: whole cache lines
-// per store instead of 64-byte pieces of sixteen rows.  Else each lane
-// stores its four outputs directly.
+// the tile's rows in LDS (rows of bm_c_row(n) floats) and copies them out
+// as the one contiguous block of rows x n values they form in C, in 16-byte
+// pieces: whole cache lines per store instead of 64-byte pieces of sixteen
+// rows.  Else each lane stores its four outputs directly.
 // blo / alo (wave-uniform): B / the A tile has nonzero lo parts.
 template <typename TOut, int KS>
 __device__ __forceinline__ void bm_tile(const bmm_bf16x8 (&ah)[KS], const bmm_bf16x8 (&al)[KS],
@@ -359,9 +374,9 @@ __device__ __forceinline__ void bm_tile(const bmm_bf16x8 (&ah)[KS], const bmm_bf
   const int row = mt * 16 + li;
   TOut* __restrict__ cr = static_cast<TOut*>(a.c) + (bt * a.m + (row < a.m ? row : 0)) * (int64_t)a.n + 4 * g;
   // bm_pos(col, 32 ks + 8 g): the lane's piece within each 64-byte group is
-  // g ^ ((col >> 2) & 3), the same for every ks and every column tile
+  // g ^ ((col >> 1) & 3), the same for every ks and every column tile
   // (col advances by 16), so one base per array and immediate offsets.
-  const int lbase = li * (KS * 32) + 8 * (g ^ ((li >> 2) & 3));
+  const int lbase = li * bm_row<KS>() + 8 * (g ^ ((li >> 1) & 3));
   const bmm_bf16x8* __restrict__ ph = reinterpret_cast<const bmm_bf16x8*>(s_bh + lbase);
   const bmm_bf16x8* __restrict__ pl = reinterpret_cast<const bmm_bf16x8*>(s_bl + lbase);
 #pragma clang loop unroll(disable)
@@ -377,11 +392,11 @@ __device__ __forceinline__ void bm_tile(const bmm_bf16x8 (&ah)[KS], const bmm_bf
       }
       if (alo) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh, al[ks], acc, 0, 0, 0);
     }
-    ph += 16 * KS * 4;  // 16 columns of kp bf16
-    pl += 16 * KS * 4;
+    ph += 16 * bm_row<KS>() / 8;  // 16 rows of staged B
+    pl += 16 * bm_row<KS>() / 8;
     const int c0 = nt * 16 + 4 * g;
     if (s_c != nullptr) {
-      if (c0 < a.n) *reinterpret_cast<bmm_f32x4*>(s_c + li * a.n + c0) = acc;
+      if (c0 < a.n) *reinterpret_cast<bmm_f32x4*>(s_c + li * bm_c_row(a.n) + c0) = acc;
     } else if (row < a.m) {
       bm_store4<TOut>(cr + nt * 16, acc, a.alpha, a.n - c0, vec_out);
     }
@@ -390,8 +405,14 @@ __device__ __forceinline__ void bm_tile(const bmm_bf16x8 (&ah)[KS], const bmm_bf
     const int rows = a.m - mt * 16 < 16 ? a.m - mt * 16 : 16;
     const int total = rows * a.n;  // a multiple of 4
     TOut* __restrict__ cb = static_cast<TOut*>(a.c) + (bt * a.m + mt * 16) * (int64_t)a.n;
-    for (int e = lane * 4; e < total; e += 256)
-      bm_store4<TOut>(cb + e, *reinterpret_cast<const bmm_f32x4*>(s_c + e), a.alpha, 4, true);
+    const int crow = bm_c_row(a.n);
+    // r = e / n: e < 4096 and n <= 256 keep (e + 0.5) / n at least 1 / 512
+    // away from an integer, far beyond the rounding of the product.
+    const float inv_n = 1.f / (float)a.n;
+    for (int e = lane * 4; e < total; e += 256) {
+      const int r = (int)(((float)e + 0.5f) * inv_n), c = e - r * a.n;
+      bm_store4<TOut>(cb + e, *reinterpret_cast<const bmm_f32x4*>(s_c + r * crow + c), a.alpha, 4, true);
+    }
   }
 }
 
@@ -400,16 +421,16 @@ __device__ __forceinline__ void bm_tile(const bmm_bf16x8 (&ah)[KS], const bmm_bf
 template <typename T, typename TOut, int KS>
 __global__ __launch_bounds__(64 * kBmWaves) __attribute__((amdgpu_waves_per_eu(KS <= 7 ? 3 : 2)))
 void k_bmm_mfma(BmmArgs a, int stage_c) {
-  extern __shared__ __align__(16) uint16_t s_b[];  // hi [npad][kp], lo, then C tiles
+  extern __shared__ __align__(16) uint16_t s_b[];  // hi [npad][bm_row], lo, then C tiles
   const int npad = (a.n + 15) & ~15;
   uint16_t* s_bh = s_b;
-  uint16_t* s_bl = s_b + npad * (KS * 32);
+  uint16_t* s_bl = s_b + npad * bm_row<KS>();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int mtiles = (a.m + 15) / 16, ntiles = npad / 16;
   // f32 rows of A 16-byte aligned: rows start at multiples of K floats.
   const bool vec = sizeof(T) == 4 && (a.k & 3) == 0 && (reinterpret_cast<uintptr_t>(a.a) & 15) == 0;
   const bool has_tiles = wave < mtiles;
-  float* s_c = stage_c ? reinterpret_cast<float*>(s_b + 2 * npad * (KS * 32)) + wave * 16 * a.n : nullptr;
+  float* s_c = stage_c ? reinterpret_cast<float*>(s_b + 2 * npad * bm_row<KS>()) + wave * 16 * bm_c_row(a.n) : nullptr;
   // Rows of C start 4-element aligned: four outputs leave as one store.
   const bool vec_out = (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.c) & (4 * sizeof(TOut) - 1)) == 0;
   // This wavefront's items, in order: tiles wave, wave + 4, ... of batch
@@ -468,16 +489,18 @@ int bm_blocks_per_cu(size_t lds) {
 
 template <typename T, typename TOut, int KS>
 int launch_bmm_mfma_t(const BmmArgs& a, hipStream_t stream) {
-  const size_t lds_b = (size_t)2 * ((a.n + 15) & ~15) * (KS * 32) * sizeof(uint16_t);
-  const size_t lds_c = (size_t)kBmWaves * 16 * a.n * sizeof(float);
+  const size_t lds_b = (size_t)2 * ((a.n + 15) & ~15) * bm_row<KS>() * sizeof(uint16_t);
+  const size_t lds_c = (size_t)kBmWaves * 16 * bm_c_row(a.n) * sizeof(float);
   // Stage C tiles when rows are whole 16-byte pieces and two workgroups
   // still fit on a CU.
   const bool vec_out = (a.n & 3) == 0 && (reinterpret_cast<uintptr_t>(a.c) & (4 * sizeof(TOut) - 1)) == 0;
   const int stage_c = vec_out && lds_b + lds_c <= (size_t)80 * 1024 ? 1 : 0;
   const size_t lds = lds_b + (stage_c ? lds_c : 0);
   constexpr auto kern = k_bmm_mfma<T, TOut, KS>;
+  // Beyond the default 64 KB: padded B rows of the widest shapes (at most
+  // 1.5 x 64 KB, KS = 2) or B plus C tiles (at most 80 KB).
   if (lds > 64 * 1024) {
-    const int e = set_lds_limit_once<kern>(80 * 1024);
+    const int e = set_lds_limit_once<kern>(96 * 1024);
     if (e != (int)hipSuccess) return e;
   }
   const int64_t cap = (int64_t)num_cus() * bm_blocks_per_cu<kern>(lds);

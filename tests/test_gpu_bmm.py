@@ -40,6 +40,8 @@ CASES = [  # (batches, m, k, n)
     # turn, and a wavefront's next tile is often in its next batch (m = 80:
     # five row tiles over four wavefronts; m = 20: two wavefronts idle).
     (2000, 80, 40, 24), (1500, 20, 32, 16),
+    # Widest padded B rows in LDS (k 33..64 with n = 256: 96 KB).
+    (3, 40, 64, 256),
 ]
 
 
