@@ -356,15 +356,22 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
         TOut* __restrict__ spk = static_cast<TOut*>(y) + (frame * c_out_t + co0) * hwo_t;
         if (nco == 32 && CO == 32 && (hwo_t & 3) == 0) {
           // Lane l stores pixels p0 + 4*(l & 15) .. +3 of channel 4*i + (l >> 4):
-          // eight vector stores instead of 32 (npx is a multiple of 4).
-          const int src = 4 * (lane & 15);
+          // eight vector stores instead of 32 (npx is a multiple of 4).  The
+          // lane-dependent offsets are formed here from a fresh opaque copy
+          // of the lane index: hoisted out of the step loop they were
+          // spilled, and the reload's wait for it (the vector memory counter
+          // retires in order) also waited for the next step's prefetched
+          // bitmap words.
+          int ls = lane;
+          asm volatile("" : "+v"(ls));
+          const int src = 4 * (ls & 15);
           uint32_t gw[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) gw[j] = __shfl(sw, src + j);
           if (valid && src < npx) {
             constexpr int B = (int)sizeof(TOut);
             const auto sr = buf_rsrc(spk, (uint32_t)c_out_t * (uint32_t)hwo_t * B);
-            const int cq = lane >> 4;
+            const int cq = ls >> 4;
             const int vo = ((cq) * hwo_t + p0 + src) * B;
 #pragma unroll
             for (int i = 0; i < CO / 4; ++i) {
