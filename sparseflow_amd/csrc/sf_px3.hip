@@ -24,6 +24,8 @@
 // in (chunk, tap, ci) order: deterministic from run to run.
 // Replaces the reference's sparse_conv3x3s1_nhwc_kernel_8x8/8x16 and
 // sparse_conv3x3s2 kernels (Kernels/conv2d.py:564-886) for these shapes.
+#include <type_traits>
+
 #include "sf_tile.h"
 
 namespace sf {
@@ -452,12 +454,20 @@ __device__ __forceinline__ void px3w_load_words(uint32_t (&lo)[9], uint32_t (&hi
   }
 }
 
-template <typename TIn>
+// Stores and waits: a tile's 64 channel stores are issued unconditionally
+// (buffer stores; pixels past the tile and channels past C_out fall outside
+// the buffer's range and are dropped), and the bitmap walk has no memory
+// loads of its own, so the compiler can count exactly how many stores
+// follow the next tile's word loads: the walk then waits for those loads
+// only, not for the previous tile's stores.  (With conditional stores the
+// count differed between paths and the merged wait drained nearly all of
+// them before every walk.)
+template <typename TIn, typename TOut>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                const uint32_t* __restrict__ flags,
                                                                const TIn* __restrict__ x, const float* __restrict__ wt,
-                                                               const float* __restrict__ bias_p, void* __restrict__ y,
-                                                               int groups, int out_dtype) {
+                                                               const float* __restrict__ bias_p, TOut* __restrict__ y,
+                                                               int groups) {
   extern __shared__ __align__(16) char smem[];
   __shared__ float s_seed[64];
   const int lane0 = lane_id();
@@ -528,10 +538,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
 #pragma unroll
       for (int tp = 0; tp < 9; ++tp) nz |= ((wl[tp] | wh[tp]) != 0u ? 1u : 0u) << tp;
       const TIn* __restrict__ xf = x + (int64_t)sample * a.c_in * a.hw_in;
+      // Per-lane cursor over (tap, ci): the wavefront loops while any lane
+      // has spikes left.  Two copies: only the value path loads x.
       uint64_t m = 0ull;
       int tap = 0;
-      // Per-lane cursor over (tap, ci): the wavefront loops while any lane
-      // has spikes left.
       while ((m != 0ull) || (nz != 0u)) {
         if (m == 0ull) {
           tap = __builtin_ctz(nz);
@@ -544,6 +554,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
         if (value) {
           const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
           xv = to_f32<TIn>(xf[(int64_t)bit * a.hw_in + ih * a.w_in + iw]);
+          // Waited for here, in the value path: otherwise the products
+          // below wait for every memory operation in flight (the previous
+          // tile's stores included) on every spike of the bitmap path too.
+          __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
         }
         px3_add_row<64>(acc, smem, bit * 9 + tap, xv);
       }
@@ -558,28 +572,47 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (mine) {
-      const int64_t yb = ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
-      if (out_dtype == SF_F16) px3_store<64>(acc, static_cast<__half*>(y) + yb, hwo_t, nco);
-      else if (out_dtype == SF_BF16) px3_store<64>(acc, static_cast<__hip_bfloat16*>(y) + yb, hwo_t, nco);
-      else px3_store<64>(acc, static_cast<float*>(y) + yb, hwo_t, nco);
+    {
+      // The sample's output planes as one buffer: lanes without a pixel get
+      // an offset past its end, channels past C_out land past it too.
+      constexpr uint32_t B = (uint32_t)sizeof(TOut);
+      const auto rs = buf_rsrc(y + (int64_t)sample * c_out_t * hwo_t, (uint32_t)c_out_t * (uint32_t)hwo_t * B);
+      const uint32_t base = mine ? ((uint32_t)co0 * (uint32_t)hwo_t + (uint32_t)(p0 + lane)) * B : 0x80000000u;
+      const uint32_t plane = (uint32_t)hwo_t * B;
+      // One offset register stepped by a plane per store (opaque, so the 64
+      // offsets are not precomputed into registers); soffset stays 0.
+      uint32_t off = base;
+#pragma unroll
+      for (int co = 0; co < 64; ++co) {
+        BufIO<TOut>::store(from_f32<TOut>(acc[co]), rs, (int)off, 0);
+        off += plane;
+        asm volatile("" : "+v"(off));
+      }
+      (void)nco;
     }
   }
 }
 
-template <typename TIn>
-int launch_px3w_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+template <typename TIn, typename TOut>
+int launch_px3w_to(const ConvArgs& a, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
   const int64_t tiles = a.n * (int64_t)((a.hw_out + 63) / 64);
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  constexpr auto kern = k_conv_px3w<TIn>;
+  constexpr auto kern = k_conv_px3w<TIn, TOut>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), (size_t)kPx3wBytes, stream, a, a.bits, a.flags,
-                     static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, out_dtype);
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups);
   return (int)hipGetLastError();
+}
+
+template <typename TIn>
+int launch_px3w_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+  if (out_dtype == SF_F16) return launch_px3w_to<TIn, __half>(a, stream);
+  if (out_dtype == SF_BF16) return launch_px3w_to<TIn, __hip_bfloat16>(a, stream);
+  return launch_px3w_to<TIn, float>(a, stream);
 }
 
 template <typename TIn, typename TOut, int CO, bool LIF>
@@ -614,8 +647,10 @@ int launch_px3_co(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t st
 // per slice.  (A 16-channel slice, resident up to C_in = 256, walks too
 // often: slower than streaming.)
 int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
-  // C_in <= 64: one 64-channel chunk, every weight row resident.
-  if (a.c_in <= 64 && a.cwp <= 2) {
+  // C_in <= 64: one 64-channel chunk, every weight row resident (and one
+  // sample's output planes addressable by one buffer resource).
+  const int out_bytes = out_dtype == SF_F32 ? 4 : 2;
+  if (a.c_in <= 64 && a.cwp <= 2 && (int64_t)a.c_out * a.hw_out * out_bytes < 0x7fffffffLL) {
     if (in_dtype == SF_F16) return launch_px3w_t<__half>(a, out_dtype, stream);
     if (in_dtype == SF_BF16) return launch_px3w_t<__hip_bfloat16>(a, out_dtype, stream);
     return launch_px3w_t<float>(a, out_dtype, stream);
