@@ -422,39 +422,63 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
 constexpr int kPx3wRows = 64 * 9;
 constexpr int kPx3wUnits = (kPx3wRows * 17 + 63) / 64;  // 1 KB load units
 constexpr int kPx3wBytes = kPx3wUnits * 1024;           // 156,672
+// 32 output channels: the rows of up to 128 input channels (1152 rows of
+// 128 bytes, the 32-channel slice layout of Px3Layout<32>).
+constexpr int kPx3w32Rows = 128 * 9;
+constexpr int kPx3w32Units = kPx3w32Rows * 8 / 64;      // 1 KB load units
+constexpr int kPx3w32Bytes = kPx3w32Units * 1024;       // 147,456
 
-// Direct-to-LDS loads of the 576 rows (padded to 17 pieces of 16 bytes):
-// pads, rows past C_in and channels past C_out read a valid but unrelated
-// address whose values are never used.
+template <int CO>
+constexpr int px3w_bytes() { return CO == 64 ? kPx3wBytes : kPx3w32Bytes; }
+
+// Direct-to-LDS loads of the resident rows.  CO = 64: 576 rows padded to 17
+// pieces of 16 bytes; CO = 32: up to 1152 rows of 8 pieces, piece s of row r
+// stored at position s ^ ((r >> 1) & 7) (Px3Layout<32>; the swizzle key of a
+// row is the same whether it is indexed within its 32-channel chunk or across
+// the chunks, 288 rows being a multiple of 16).  Pads, rows past C_in and
+// channels past C_out read a valid but unrelated address whose values are
+// never used.
+template <int CO>
 __device__ __forceinline__ void load_rows_px3w(char* buf, const float* __restrict__ wt, int krows, int c_out, int co0,
                                                int wave, int lane) {
-  for (int u = wave; u < kPx3wUnits; u += kRowsWaves) {
-    const int pos = u * 64 + lane;
-    const int r = pos / 17, q = pos - r * 17;
-    const int col = co0 + 4 * q;
-    const float* src = (q < 16 && r < krows && col < c_out) ? wt + (int64_t)r * c_out + col : wt;
-    __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+  if constexpr (CO == 64) {
+    for (int u = wave; u < kPx3wUnits; u += kRowsWaves) {
+      const int pos = u * 64 + lane;
+      const int r = pos / 17, q = pos - r * 17;
+      const int col = co0 + 4 * q;
+      const float* src = (q < 16 && r < krows && col < c_out) ? wt + (int64_t)r * c_out + col : wt;
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+    }
+  } else {
+    for (int u = wave; u < kPx3w32Units; u += kRowsWaves) {
+      const int pos = u * 64 + lane;
+      const int r = pos >> 3, q = pos & 7;
+      const int col = co0 + 4 * (q ^ ((r >> 1) & 7));
+      const float* src = (r < krows && col < c_out) ? wt + (int64_t)r * c_out + col : wt;
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+    }
   }
 }
 
-// Channel words 0 and 1 (channels 0-31, 32-63) of the lane's nine taps (0
-// outside the frame; word 1 is 0 with one word per pixel), bf = the frame's
-// bitmap, through one buffer resource as in px3_load_words.
+// Channel words c0 and c0 + 1 (a 64-channel super-chunk) of the lane's nine
+// taps (0 outside the frame; the second is 0 past the pixel's last word),
+// bf = the frame's bitmap, through one buffer resource as in px3_load_words.
 __device__ __forceinline__ void px3w_load_words(uint32_t (&lo)[9], uint32_t (&hi)[9], const uint32_t* __restrict__ bf,
-                                                const ConvArgs& a, int ih0, int iw0) {
+                                                const ConvArgs& a, int ih0, int iw0, int c0) {
   const uint32_t frame_bytes = (uint32_t)a.hw_in * (uint32_t)a.cwp * 4u;
   const auto rs = buf_rsrc(bf, frame_bytes);
+  const bool two = c0 + 1 < a.cwp;
 #pragma unroll
   for (int tp = 0; tp < 9; ++tp) {
     const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
     const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
-    const uint32_t off = in ? (uint32_t)(ih * a.w_in + iw) * (uint32_t)a.cwp * 4u : 0x80000000u;
+    const uint32_t off = in ? ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.cwp + (uint32_t)c0) * 4u : 0x80000000u;
     lo[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
-    hi[tp] = a.cwp == 2 ? __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(off + 4u), 0, 0) : 0u;
+    hi[tp] = two ? __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(off + 4u), 0, 0) : 0u;
   }
 }
 
-// Stores and waits: a tile's 64 channel stores are issued unconditionally
+// Stores and waits: a tile's channel stores are issued unconditionally
 // (buffer stores; pixels past the tile and channels past C_out fall outside
 // the buffer's range and are dropped), and the bitmap walk has no memory
 // loads of its own, so the compiler can count exactly how many stores
@@ -462,28 +486,33 @@ __device__ __forceinline__ void px3w_load_words(uint32_t (&lo)[9], uint32_t (&hi
 // only, not for the previous tile's stores.  (With conditional stores the
 // count differed between paths and the merged wait drained nearly all of
 // them before every walk.)
-template <typename TIn, typename TOut>
+//
+// CO = 32 (64 < C_in <= 128): the same walk over up to two 64-channel
+// super-chunks, the second's words requested before the first's walk; rows
+// (64 sc + ci) * 9 + tap of the resident 32-channel slice layout.
+template <typename TIn, typename TOut, int CO>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                const uint32_t* __restrict__ flags,
                                                                const TIn* __restrict__ x, const float* __restrict__ wt,
                                                                const float* __restrict__ bias_p, TOut* __restrict__ y,
                                                                int groups) {
   extern __shared__ __align__(16) char smem[];
-  __shared__ float s_seed[64];
+  __shared__ float s_seed[CO];
   const int lane0 = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int blk = groups >= 8 ? xcd_local_block((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
   const int grp = blk % groups;
-  const int co0 = grp * 64;
+  const int co0 = grp * CO;
   const int hwo = a.hw_out;
   const int tpf = (hwo + 63) / 64;
   const int total = (int)a.n * tpf;
   const int nblk = (int)(gridDim.x / groups);
-  if (threadIdx.x < 64) {
+  const int nsc = CO == 64 ? 1 : (a.cwp + 1) / 2;  // 64-channel super-chunks
+  if (threadIdx.x < CO) {
     const int co = co0 + (int)threadIdx.x;
     s_seed[threadIdx.x] = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
   }
-  load_rows_px3w(smem, wt, a.c_in * 9, a.c_out, co0, wave, lane0);
+  load_rows_px3w<CO>(smem, wt, a.c_in * 9, a.c_out, co0, wave, lane0);
   // The first tile's words; later tiles' are requested before the previous
   // tile's stores (the vector memory counter retires in issue order).
   uint32_t nlo[9], nhi[9];
@@ -493,7 +522,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
       const int sample = t / tpf, p0 = (t - sample * tpf) * 64;
       const int q = p0 + min(lane0, hwo - p0 - 1);
       const int oh = q / a.w_out, ow = q - oh * a.w_out;
-      px3w_load_words(nlo, nhi, bits + (int64_t)sample * a.hw_in * a.cwp, a, oh * a.s - 1, ow * a.s - 1);
+      px3w_load_words(nlo, nhi, bits + (int64_t)sample * a.hw_in * a.cwp, a, oh * a.s - 1, ow * a.s - 1, 0);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wavefront's direct weight loads have landed
@@ -512,16 +541,17 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
     const int ih0 = oh * a.s - 1, iw0 = ow * a.s - 1;
     int hwo_t = hwo, c_out_t = a.c_out;
     asm volatile("" : "+s"(hwo_t), "+s"(c_out_t));
-    const int nco = min(64, c_out_t - co0);
-    float acc[64];
+    float acc[CO];
 #pragma unroll
-    for (int co = 0; co < 64; ++co) acc[co] = s_seed[co];
+    for (int co = 0; co < CO; ++co) acc[co] = s_seed[co];
     bool value = false;
     if (valid) {
       const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
       value = rows_value_path(a, flags, sample, oh_a * a.s - 1, oh_b * a.s + 1);
     }
-    if (mine) {
+    const uint32_t* __restrict__ bf = bits + (int64_t)sample * a.hw_in * a.cwp;
+    const TIn* __restrict__ xf = x + (int64_t)sample * a.c_in * a.hw_in;
+    for (int sc = 0; sc < nsc; ++sc) {
       uint32_t wl[9], wh[9];
 #pragma unroll
       for (int tp = 0; tp < 9; ++tp) {
@@ -534,32 +564,36 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
                    "+v"(wl[7]), "+v"(wl[8]));
       asm volatile("" : "+v"(wh[0]), "+v"(wh[1]), "+v"(wh[2]), "+v"(wh[3]), "+v"(wh[4]), "+v"(wh[5]), "+v"(wh[6]),
                    "+v"(wh[7]), "+v"(wh[8]));
-      uint32_t nz = 0u;
+      // The next super-chunk's words are in flight during this walk.
+      if (CO != 64 && sc + 1 < nsc) px3w_load_words(nlo, nhi, bf, a, ih0, iw0, 2 * (sc + 1));
+      if (mine) {
+        uint32_t nz = 0u;
 #pragma unroll
-      for (int tp = 0; tp < 9; ++tp) nz |= ((wl[tp] | wh[tp]) != 0u ? 1u : 0u) << tp;
-      const TIn* __restrict__ xf = x + (int64_t)sample * a.c_in * a.hw_in;
-      // Per-lane cursor over (tap, ci): the wavefront loops while any lane
-      // has spikes left.  Two copies: only the value path loads x.
-      uint64_t m = 0ull;
-      int tap = 0;
-      while ((m != 0ull) || (nz != 0u)) {
-        if (m == 0ull) {
-          tap = __builtin_ctz(nz);
-          nz &= nz - 1u;
-          m = ((uint64_t)px3_select(wh, tap) << 32) | px3_select(wl, tap);
+        for (int tp = 0; tp < 9; ++tp) nz |= ((wl[tp] | wh[tp]) != 0u ? 1u : 0u) << tp;
+        const int row0 = 64 * sc * 9;
+        // Per-lane cursor over (tap, ci): the wavefront loops while any lane
+        // has spikes left.
+        uint64_t m = 0ull;
+        int tap = 0;
+        while ((m != 0ull) || (nz != 0u)) {
+          if (m == 0ull) {
+            tap = __builtin_ctz(nz);
+            nz &= nz - 1u;
+            m = ((uint64_t)px3_select(wh, tap) << 32) | px3_select(wl, tap);
+          }
+          const int bit = __builtin_ctzll(m);
+          m &= m - 1ull;
+          float xv = 1.f;
+          if (value) {
+            const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+            xv = to_f32<TIn>(xf[(int64_t)(64 * sc + bit) * a.hw_in + ih * a.w_in + iw]);
+            // Waited for here, in the value path: otherwise the products
+            // below wait for every memory operation in flight (the previous
+            // tile's stores included) on every spike of the bitmap path too.
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+          }
+          px3_add_row<CO>(acc, smem, row0 + bit * 9 + tap, xv);
         }
-        const int bit = __builtin_ctzll(m);
-        m &= m - 1ull;
-        float xv = 1.f;
-        if (value) {
-          const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
-          xv = to_f32<TIn>(xf[(int64_t)bit * a.hw_in + ih * a.w_in + iw]);
-          // Waited for here, in the value path: otherwise the products
-          // below wait for every memory operation in flight (the previous
-          // tile's stores included) on every spike of the bitmap path too.
-          __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-        }
-        px3_add_row<64>(acc, smem, bit * 9 + tap, xv);
       }
     }
     {
@@ -568,51 +602,52 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
         const int ns = tn / tpf, np0 = (tn - ns * tpf) * 64;
         const int nq = np0 + min(lane, hwo - np0 - 1);
         const int noh = nq / a.w_out, now = nq - noh * a.w_out;
-        px3w_load_words(nlo, nhi, bits + (int64_t)ns * a.hw_in * a.cwp, a, noh * a.s - 1, now * a.s - 1);
+        px3w_load_words(nlo, nhi, bits + (int64_t)ns * a.hw_in * a.cwp, a, noh * a.s - 1, now * a.s - 1, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     {
-      // The sample's output planes as one buffer: lanes without a pixel get
-      // an offset past its end, channels past C_out land past it too.
+      // The sample's output planes as one buffer: lanes without a pixel
+      // start at its end, channels past C_out land past it too (the host
+      // keeps (C_out + CO) planes below 2^31 bytes, so no offset wraps).
       constexpr uint32_t B = (uint32_t)sizeof(TOut);
-      const auto rs = buf_rsrc(y + (int64_t)sample * c_out_t * hwo_t, (uint32_t)c_out_t * (uint32_t)hwo_t * B);
-      const uint32_t base = mine ? ((uint32_t)co0 * (uint32_t)hwo_t + (uint32_t)(p0 + lane)) * B : 0x80000000u;
+      const uint32_t range = (uint32_t)c_out_t * (uint32_t)hwo_t * B;
+      const auto rs = buf_rsrc(y + (int64_t)sample * c_out_t * hwo_t, range);
+      const uint32_t base = mine ? ((uint32_t)co0 * (uint32_t)hwo_t + (uint32_t)(p0 + lane)) * B : range;
       const uint32_t plane = (uint32_t)hwo_t * B;
-      // One offset register stepped by a plane per store (opaque, so the 64
+      // One offset register stepped by a plane per store (opaque, so the
       // offsets are not precomputed into registers); soffset stays 0.
       uint32_t off = base;
 #pragma unroll
-      for (int co = 0; co < 64; ++co) {
+      for (int co = 0; co < CO; ++co) {
         BufIO<TOut>::store(from_f32<TOut>(acc[co]), rs, (int)off, 0);
         off += plane;
         asm volatile("" : "+v"(off));
       }
-      (void)nco;
     }
   }
 }
 
-template <typename TIn, typename TOut>
+template <typename TIn, typename TOut, int CO>
 int launch_px3w_to(const ConvArgs& a, hipStream_t stream) {
-  const int groups = (a.c_out + 63) / 64;
+  const int groups = (a.c_out + CO - 1) / CO;
   const int64_t tiles = a.n * (int64_t)((a.hw_out + 63) / 64);
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  constexpr auto kern = k_conv_px3w<TIn, TOut>;
+  constexpr auto kern = k_conv_px3w<TIn, TOut, CO>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), (size_t)kPx3wBytes, stream, a, a.bits, a.flags,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), (size_t)px3w_bytes<CO>(), stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups);
   return (int)hipGetLastError();
 }
 
-template <typename TIn>
+template <typename TIn, int CO>
 int launch_px3w_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
-  if (out_dtype == SF_F16) return launch_px3w_to<TIn, __half>(a, stream);
-  if (out_dtype == SF_BF16) return launch_px3w_to<TIn, __hip_bfloat16>(a, stream);
-  return launch_px3w_to<TIn, float>(a, stream);
+  if (out_dtype == SF_F16) return launch_px3w_to<TIn, __half, CO>(a, stream);
+  if (out_dtype == SF_BF16) return launch_px3w_to<TIn, __hip_bfloat16, CO>(a, stream);
+  return launch_px3w_to<TIn, float, CO>(a, stream);
 }
 
 template <typename TIn, typename TOut, int CO, bool LIF>
@@ -647,13 +682,22 @@ int launch_px3_co(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t st
 // per slice.  (A 16-channel slice, resident up to C_in = 256, walks too
 // often: slower than streaming.)
 int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
-  // C_in <= 64: one 64-channel chunk, every weight row resident (and one
-  // sample's output planes addressable by one buffer resource).
+  // C_in <= 64: one 64-channel super-chunk, every weight row resident, 64
+  // output channels; 64 < C_in <= 128: 32-channel slices of all 128 input
+  // channels' rows, two super-chunks.  (One sample's output planes must be
+  // addressable by one buffer resource, with CO planes to spare.)
   const int out_bytes = out_dtype == SF_F32 ? 4 : 2;
-  if (a.c_in <= 64 && a.cwp <= 2 && (int64_t)a.c_out * a.hw_out * out_bytes < 0x7fffffffLL) {
-    if (in_dtype == SF_F16) return launch_px3w_t<__half>(a, out_dtype, stream);
-    if (in_dtype == SF_BF16) return launch_px3w_t<__hip_bfloat16>(a, out_dtype, stream);
-    return launch_px3w_t<float>(a, out_dtype, stream);
+  if ((int64_t)(a.c_out + 64) * a.hw_out * out_bytes < 0x7fffffffLL) {
+    if (a.c_in <= 64 && a.cwp <= 2) {
+      if (in_dtype == SF_F16) return launch_px3w_t<__half, 64>(a, out_dtype, stream);
+      if (in_dtype == SF_BF16) return launch_px3w_t<__hip_bfloat16, 64>(a, out_dtype, stream);
+      return launch_px3w_t<float, 64>(a, out_dtype, stream);
+    }
+    if (a.c_in <= 128 && a.cwp <= 4) {
+      if (in_dtype == SF_F16) return launch_px3w_t<__half, 32>(a, out_dtype, stream);
+      if (in_dtype == SF_BF16) return launch_px3w_t<__hip_bfloat16, 32>(a, out_dtype, stream);
+      return launch_px3w_t<float, 32>(a, out_dtype, stream);
+    }
   }
   const int nch = (a.c_in + kPx3Ch - 1) / kPx3Ch;
   if (nch > Px3Layout<64>::resident_chunks && nch <= Px3Layout<32>::resident_chunks)

@@ -66,6 +66,9 @@ CASES = [
     (1, 300, 6, 10, 100, 1),    # last chunk partially filled
     (17, 96, 8, 8, 64, 1),      # one tile per frame, passes past the end
     (2, 48, 3, 100, 20, 1),     # tiles spanning rows
+    (2, 72, 9, 11, 40, 1),      # 32-channel slices: second super-chunk of one sparse word, ragged group
+    (3, 100, 10, 10, 36, 2),    # 32-channel slices, stride 2, last word partial
+    (2, 65, 17, 5, 96, 1),      # one channel past a super-chunk
 ]
 
 
