@@ -157,17 +157,56 @@ __device__ __forceinline__ void px3_store(const float (&acc)[CO], TOut* __restri
   }
 }
 
-// H, spike and reset of one step: the spike of channel co goes straight to
-// sp[co * hw] (when the lane's pixel exists), the new membrane stays in acc.
-template <int CO, typename TOut>
-__device__ __forceinline__ void lif_step(float (&acc)[CO], const LifCoef& L, TOut* __restrict__ sp, int hw, int nco,
-                                         bool mine) {
+// H, spike and reset of one step with the membrane in acc: returns the
+// spikes as one word (bit co = channel co0 + co fired).
+template <int CO>
+__device__ __forceinline__ uint32_t lif_fire(float (&acc)[CO], const LifCoef& L) {
+  static_assert(CO <= 32, "one spike word per lane");
+  uint32_t sw = 0u;
 #pragma unroll
   for (int co = 0; co < CO; ++co) {
     const float h = L.decay_input ? acc[co] * L.inv_tau : acc[co];
     const bool fire = h >= L.v_th;
-    if (mine && co < nco) sp[(int64_t)co * hw] = from_f32<TOut>(fire ? 1.f : 0.f);
+    sw |= (fire ? 1u : 0u) << co;
     acc[co] = L.hard ? (fire ? L.v_reset : h) : h - (fire ? L.v_th : 0.f);
+  }
+  return sw;
+}
+
+// One step's spikes of a tile (64 pixels from p0, npx of them present) to
+// spk = the frame's plane of channel co0.
+template <typename TOut, int CO>
+__device__ __forceinline__ void px3_store_spikes(uint32_t sw, TOut* __restrict__ spk, int lane, int p0, int npx,
+                                                 bool valid, bool mine, int nco, int hwo_t, int c_out_t) {
+  if (nco == 32 && CO == 32 && (hwo_t & 3) == 0) {
+    // Lane l stores pixels p0 + 4*(l & 15) .. +3 of channel 4*i + (l >> 4):
+    // eight vector stores instead of 32 (npx is a multiple of 4).  The
+    // lane-dependent offsets are formed here from a fresh opaque copy of
+    // the lane index: hoisted out of the step loop they were spilled, and
+    // the reload's wait for it (the vector memory counter retires in order)
+    // also waited for the next step's prefetched bitmap words.
+    int ls = lane;
+    asm volatile("" : "+v"(ls));
+    const int src = 4 * (ls & 15);
+    uint32_t gw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) gw[j] = __shfl(sw, src + j);
+    if (valid && src < npx) {
+      constexpr int B = (int)sizeof(TOut);
+      const auto sr = buf_rsrc(spk, (uint32_t)c_out_t * (uint32_t)hwo_t * B);
+      const int cq = ls >> 4;
+      const int vo = ((cq) * hwo_t + p0 + src) * B;
+#pragma unroll
+      for (int i = 0; i < CO / 4; ++i) {
+        const int sh = 4 * i + cq;
+        const uint32_t q = ((gw[0] >> sh) & 1u) | (((gw[1] >> sh) & 1u) << 1) | (((gw[2] >> sh) & 1u) << 2) |
+                           (((gw[3] >> sh) & 1u) << 3);
+        store_bits4<TOut>(q, sr, vo + 4 * i * hwo_t * B);
+      }
+    }
+  } else if (mine) {
+    for (int co = 0; co < nco; ++co)
+      spk[(int64_t)co * hwo_t + p0 + lane] = from_f32<TOut>(((sw >> co) & 1u) ? 1.f : 0.f);
   }
 }
 
@@ -343,50 +382,12 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
         // H, spike and the reset: the spikes are collected as one word per
         // 32 channels (the membrane stays in acc), the next step's words are
         // requested, then the spikes are stored.
-        static_assert(!LIF || CO <= 32, "one spike word per lane");
-        uint32_t sw = 0u;
-#pragma unroll
-        for (int co = 0; co < CO; ++co) {
-          const float h = L.decay_input ? acc[co] * L.inv_tau : acc[co];
-          const bool fire = h >= L.v_th;
-          sw |= (fire ? 1u : 0u) << co;
-          acc[co] = L.hard ? (fire ? L.v_reset : h) : h - (fire ? L.v_th : 0.f);
-        }
+        const uint32_t sw = lif_fire<CO>(acc, L);
         if (st + 1 < steps && mine)
           px3_load_words(wn, bits + (frame + a.n) * a.hw_in * a.cwp, a, ih0, iw0, 0);
         __builtin_amdgcn_sched_barrier(0);
         TOut* __restrict__ spk = static_cast<TOut*>(y) + (frame * c_out_t + co0) * hwo_t;
-        if (nco == 32 && CO == 32 && (hwo_t & 3) == 0) {
-          // Lane l stores pixels p0 + 4*(l & 15) .. +3 of channel 4*i + (l >> 4):
-          // eight vector stores instead of 32 (npx is a multiple of 4).  The
-          // lane-dependent offsets are formed here from a fresh opaque copy
-          // of the lane index: hoisted out of the step loop they were
-          // spilled, and the reload's wait for it (the vector memory counter
-          // retires in order) also waited for the next step's prefetched
-          // bitmap words.
-          int ls = lane;
-          asm volatile("" : "+v"(ls));
-          const int src = 4 * (ls & 15);
-          uint32_t gw[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) gw[j] = __shfl(sw, src + j);
-          if (valid && src < npx) {
-            constexpr int B = (int)sizeof(TOut);
-            const auto sr = buf_rsrc(spk, (uint32_t)c_out_t * (uint32_t)hwo_t * B);
-            const int cq = ls >> 4;
-            const int vo = ((cq) * hwo_t + p0 + src) * B;
-#pragma unroll
-            for (int i = 0; i < CO / 4; ++i) {
-              const int sh = 4 * i + cq;
-              const uint32_t q = ((gw[0] >> sh) & 1u) | (((gw[1] >> sh) & 1u) << 1) | (((gw[2] >> sh) & 1u) << 2) |
-                                 (((gw[3] >> sh) & 1u) << 3);
-              store_bits4<TOut>(q, sr, vo + 4 * i * hwo_t * B);
-            }
-          }
-        } else if (mine) {
-          for (int co = 0; co < nco; ++co)
-            spk[(int64_t)co * hwo_t + p0 + lane] = from_f32<TOut>(((sw >> co) & 1u) ? 1.f : 0.f);
-        }
+        px3_store_spikes<TOut, CO>(sw, spk, lane, p0, npx, valid, mine, nco, hwo_t, c_out_t);
       }
     }
     if constexpr (!LIF) {
@@ -490,12 +491,18 @@ __device__ __forceinline__ void px3w_load_words(uint32_t (&lo)[9], uint32_t (&hi
 // CO = 32 (64 < C_in <= 128): the same walk over up to two 64-channel
 // super-chunks, the second's words requested before the first's walk; rows
 // (64 sc + ci) * 9 + tap of the resident 32-channel slice layout.
-template <typename TIn, typename TOut, int CO>
+//
+// LIF (CO = 32): the fused conv-LIF of k_conv_px3<LIF> on this walk: the
+// membrane stays in acc over the T steps of a tile, each step's spikes are
+// stored as 4-pixel vectors after the next step's first words are
+// requested, and v_T is stored at the end; y is then the spike tensor.
+template <typename TIn, typename TOut, int CO, bool LIF>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                const uint32_t* __restrict__ flags,
                                                                const TIn* __restrict__ x, const float* __restrict__ wt,
                                                                const float* __restrict__ bias_p, TOut* __restrict__ y,
                                                                int groups) {
+  static_assert(!LIF || CO == 32, "the fused LIF form keeps one spike word per lane");
   extern __shared__ __align__(16) char smem[];
   __shared__ float s_seed[CO];
   const int lane0 = lane_id();
@@ -505,18 +512,23 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   const int co0 = grp * CO;
   const int hwo = a.hw_out;
   const int tpf = (hwo + 63) / 64;
-  const int total = (int)a.n * tpf;
+  const int total = (int)a.n * tpf;  // LIF: a.n = samples, the T steps run inside a tile
   const int nblk = (int)(gridDim.x / groups);
   const int nsc = CO == 64 ? 1 : (a.cwp + 1) / 2;  // 64-channel super-chunks
+  const int steps = LIF ? a.T : 1;
+  const LifCoef L = lif_coef(a);
   if (threadIdx.x < CO) {
     const int co = co0 + (int)threadIdx.x;
-    s_seed[threadIdx.x] = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
+    const float b = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
+    s_seed[threadIdx.x] = LIF ? L.vr_term + b : b;
   }
   load_rows_px3w<CO>(smem, wt, a.c_in * 9, a.c_out, co0, wave, lane0);
   // The first tile's words; later tiles' are requested before the previous
-  // tile's stores (the vector memory counter retires in issue order).
+  // tile's stores (the vector memory counter retires in issue order).  The
+  // fused LIF form requests a tile's first words at the tile and prefetches
+  // per step (the T steps of a tile are its long stretch of work).
   uint32_t nlo[9], nhi[9];
-  {
+  if constexpr (!LIF) {
     const int t = (blk / groups) * kRowsWaves + wave;
     if (t < total) {
       const int sample = t / tpf, p0 = (t - sample * tpf) * 64;
@@ -542,71 +554,107 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
     int hwo_t = hwo, c_out_t = a.c_out;
     asm volatile("" : "+s"(hwo_t), "+s"(c_out_t));
     float acc[CO];
+    if constexpr (LIF) {
+      // Membrane before step 0: v_init or 0.
+      const int nco = min(CO, c_out_t - co0);
+      const float* vi = a.v_init;
 #pragma unroll
-    for (int co = 0; co < CO; ++co) acc[co] = s_seed[co];
-    bool value = false;
-    if (valid) {
-      const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
-      value = rows_value_path(a, flags, sample, oh_a * a.s - 1, oh_b * a.s + 1);
-    }
-    const uint32_t* __restrict__ bf = bits + (int64_t)sample * a.hw_in * a.cwp;
-    const TIn* __restrict__ xf = x + (int64_t)sample * a.c_in * a.hw_in;
-    for (int sc = 0; sc < nsc; ++sc) {
-      uint32_t wl[9], wh[9];
+      for (int co = 0; co < CO; ++co) acc[co] = 0.f;
+      if (vi != nullptr && mine) {
+        const float* vp = vi + ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
 #pragma unroll
-      for (int tp = 0; tp < 9; ++tp) {
-        wl[tp] = nlo[tp];
-        wh[tp] = nhi[tp];
+        for (int co = 0; co < CO; ++co)
+          if (co < nco) acc[co] = vp[(int64_t)co * hwo_t];
       }
-      // Opaque to the optimiser: a select between array elements would
-      // otherwise be folded into an indexed load from scratch memory.
-      asm volatile("" : "+v"(wl[0]), "+v"(wl[1]), "+v"(wl[2]), "+v"(wl[3]), "+v"(wl[4]), "+v"(wl[5]), "+v"(wl[6]),
-                   "+v"(wl[7]), "+v"(wl[8]));
-      asm volatile("" : "+v"(wh[0]), "+v"(wh[1]), "+v"(wh[2]), "+v"(wh[3]), "+v"(wh[4]), "+v"(wh[5]), "+v"(wh[6]),
-                   "+v"(wh[7]), "+v"(wh[8]));
-      // The next super-chunk's words are in flight during this walk.
-      if (CO != 64 && sc + 1 < nsc) px3w_load_words(nlo, nhi, bf, a, ih0, iw0, 2 * (sc + 1));
-      if (mine) {
-        uint32_t nz = 0u;
+      px3w_load_words(nlo, nhi, bits + (int64_t)sample * a.hw_in * a.cwp, a, ih0, iw0, 0);
+    } else {
 #pragma unroll
-        for (int tp = 0; tp < 9; ++tp) nz |= ((wl[tp] | wh[tp]) != 0u ? 1u : 0u) << tp;
-        const int row0 = 64 * sc * 9;
-        // Per-lane cursor over (tap, ci): the wavefront loops while any lane
-        // has spikes left.
-        uint64_t m = 0ull;
-        int tap = 0;
-        while ((m != 0ull) || (nz != 0u)) {
-          if (m == 0ull) {
-            tap = __builtin_ctz(nz);
-            nz &= nz - 1u;
-            m = ((uint64_t)px3_select(wh, tap) << 32) | px3_select(wl, tap);
+      for (int co = 0; co < CO; ++co) acc[co] = s_seed[co];
+    }
+    for (int st = 0; st < steps; ++st) {
+      const int64_t frame = LIF ? (int64_t)st * a.n + sample : sample;
+      if constexpr (LIF) lif_seed_lds<CO>(acc, L, s_seed);
+      bool value = false;
+      if (valid) {
+        const int oh_a = p0 / a.w_out, oh_b = (p0 + npx - 1) / a.w_out;
+        value = rows_value_path(a, flags, frame, oh_a * a.s - 1, oh_b * a.s + 1);
+      }
+      const uint32_t* __restrict__ bf = bits + frame * a.hw_in * a.cwp;
+      const TIn* __restrict__ xf = x + frame * a.c_in * a.hw_in;
+      for (int sc = 0; sc < nsc; ++sc) {
+        uint32_t wl[9], wh[9];
+#pragma unroll
+        for (int tp = 0; tp < 9; ++tp) {
+          wl[tp] = nlo[tp];
+          wh[tp] = nhi[tp];
+        }
+        // Opaque to the optimiser: a select between array elements would
+        // otherwise be folded into an indexed load from scratch memory.
+        asm volatile("" : "+v"(wl[0]), "+v"(wl[1]), "+v"(wl[2]), "+v"(wl[3]), "+v"(wl[4]), "+v"(wl[5]), "+v"(wl[6]),
+                     "+v"(wl[7]), "+v"(wl[8]));
+        asm volatile("" : "+v"(wh[0]), "+v"(wh[1]), "+v"(wh[2]), "+v"(wh[3]), "+v"(wh[4]), "+v"(wh[5]), "+v"(wh[6]),
+                     "+v"(wh[7]), "+v"(wh[8]));
+        // The next super-chunk's words are in flight during this walk.
+        if (CO != 64 && sc + 1 < nsc) px3w_load_words(nlo, nhi, bf, a, ih0, iw0, 2 * (sc + 1));
+        if (mine) {
+          uint32_t nz = 0u;
+#pragma unroll
+          for (int tp = 0; tp < 9; ++tp) nz |= ((wl[tp] | wh[tp]) != 0u ? 1u : 0u) << tp;
+          const int row0 = 64 * sc * 9;
+          // Per-lane cursor over (tap, ci): the wavefront loops while any
+          // lane has spikes left.
+          uint64_t m = 0ull;
+          int tap = 0;
+          while ((m != 0ull) || (nz != 0u)) {
+            if (m == 0ull) {
+              tap = __builtin_ctz(nz);
+              nz &= nz - 1u;
+              m = ((uint64_t)px3_select(wh, tap) << 32) | px3_select(wl, tap);
+            }
+            const int bit = __builtin_ctzll(m);
+            m &= m - 1ull;
+            float xv = 1.f;
+            if (value) {
+              const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+              xv = to_f32<TIn>(xf[(int64_t)(64 * sc + bit) * a.hw_in + ih * a.w_in + iw]);
+              // Waited for here, in the value path: otherwise the products
+              // below wait for every memory operation in flight (the
+              // previous tile's stores included) on every spike of the
+              // bitmap path too.
+              __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            }
+            px3_add_row<CO>(acc, smem, row0 + bit * 9 + tap, xv);
           }
-          const int bit = __builtin_ctzll(m);
-          m &= m - 1ull;
-          float xv = 1.f;
-          if (value) {
-            const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
-            xv = to_f32<TIn>(xf[(int64_t)(64 * sc + bit) * a.hw_in + ih * a.w_in + iw]);
-            // Waited for here, in the value path: otherwise the products
-            // below wait for every memory operation in flight (the previous
-            // tile's stores included) on every spike of the bitmap path too.
-            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-          }
-          px3_add_row<CO>(acc, smem, row0 + bit * 9 + tap, xv);
         }
       }
-    }
-    {
-      const int tn = (pass + nblk) * kRowsWaves + wave;
-      if (tn < total) {
-        const int ns = tn / tpf, np0 = (tn - ns * tpf) * 64;
-        const int nq = np0 + min(lane, hwo - np0 - 1);
-        const int noh = nq / a.w_out, now = nq - noh * a.w_out;
-        px3w_load_words(nlo, nhi, bits + (int64_t)ns * a.hw_in * a.cwp, a, noh * a.s - 1, now * a.s - 1, 0);
+      if constexpr (LIF) {
+        // Spikes and reset; the next step's first words are requested
+        // before the spike stores.
+        const int nco = min(CO, c_out_t - co0);
+        const uint32_t sw = lif_fire<CO>(acc, L);
+        if (st + 1 < steps)
+          px3w_load_words(nlo, nhi, bits + (frame + a.n) * a.hw_in * a.cwp, a, ih0, iw0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        TOut* __restrict__ spk = y + (frame * c_out_t + co0) * hwo_t;
+        px3_store_spikes<TOut, CO>(sw, spk, lane, p0, npx, valid, mine, nco, hwo_t, c_out_t);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    {
+    if constexpr (LIF) {
+      if (mine) {
+        const int64_t vb = ((int64_t)sample * c_out_t + co0) * hwo_t + p0 + lane;
+        px3_store<CO>(acc, a.v_out + vb, hwo_t, min(CO, c_out_t - co0));
+      }
+    } else {
+      {
+        const int tn = (pass + nblk) * kRowsWaves + wave;
+        if (tn < total) {
+          const int ns = tn / tpf, np0 = (tn - ns * tpf) * 64;
+          const int nq = np0 + min(lane, hwo - np0 - 1);
+          const int noh = nq / a.w_out, now = nq - noh * a.w_out;
+          px3w_load_words(nlo, nhi, bits + (int64_t)ns * a.hw_in * a.cwp, a, noh * a.s - 1, now * a.s - 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
       // The sample's output planes as one buffer: lanes without a pixel
       // start at its end, channels past C_out land past it too (the host
       // keeps (C_out + CO) planes below 2^31 bytes, so no offset wraps).
@@ -628,14 +676,14 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   }
 }
 
-template <typename TIn, typename TOut, int CO>
+template <typename TIn, typename TOut, int CO, bool LIF = false>
 int launch_px3w_to(const ConvArgs& a, hipStream_t stream) {
   const int groups = (a.c_out + CO - 1) / CO;
   const int64_t tiles = a.n * (int64_t)((a.hw_out + 63) / 64);
   const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
   const int per_group = (int)(need < num_cus() ? need : num_cus());
   const int grid = groups * (per_group > 0 ? per_group : 1);
-  constexpr auto kern = k_conv_px3w<TIn, TOut, CO>;
+  constexpr auto kern = k_conv_px3w<TIn, TOut, CO, LIF>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), (size_t)px3w_bytes<CO>(), stream, a, a.bits, a.flags,
@@ -711,6 +759,11 @@ int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
 // as many workgroups.
 template <typename TIn, typename TOut>
 int launch_px3_lif_t(const ConvArgs& a, hipStream_t stream) {
+  // Up to 128 input channels: every weight row resident and the spikes
+  // walked as 64-channel super-chunks (fewer rounds than 32-channel chunks:
+  // a round count is the busiest lane's, which grows more slowly than the
+  // mean).
+  if (a.c_in <= 128 && a.cwp <= 4) return launch_px3w_to<TIn, TOut, 32, true>(a, stream);
   return launch_px3_t<TIn, TOut, 32, true>(a, 0, stream);
 }
 

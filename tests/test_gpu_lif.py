@@ -176,6 +176,8 @@ PX_LIF_CASES = [
     (3, 2, 160, 9, 9, 64, 0.1, 0.0, False, 1.0),      # five chunks: streamed through two LDS buffers
     (5, 2, 33, 7, 11, 36, 0.1, None, True, 2.0),      # soft reset, ragged channel group, odd plane
     (2, 1, 1, 5, 5, 4, 0.5, -0.3, True, 6.0),         # one input channel
+    (3, 2, 96, 11, 9, 40, 0.05, 0.0, True, 2.0),      # second 64-channel super-chunk of one word, ragged group
+    (2, 3, 100, 12, 12, 32, 0.08, None, False, 2.0),  # last word partial, soft reset, vector spike stores
 ]
 
 
