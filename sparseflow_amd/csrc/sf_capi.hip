@@ -172,12 +172,68 @@ sf::ConvArgs conv_args(const sf_conv_desc* d, int64_t frames, const uint32_t* bi
   a.s = d->stride;
   a.p = d->pad;
   a.cwp = pl.cwp;
+  a.bm_ps = pl.cwp;  // the [hw][cwp] words of sf_prescan_pack
+  a.bm_ws = 1;
   a.chunk = pl.chunk;
   a.chunks_per_frame = pl.chunks_per_frame;
   a.T = 1;
   sf::conv_geometry(a, lif);
   a.total_groups = d->n * (int64_t)a.groups_per_frame;
   return a;
+}
+
+// ---- Stage 2 selection ----------------------------------------------------------
+
+enum class Stage2 { kMfma, kBand, kRowsKc, kPx3, kFlat, kGather };
+
+Stage2 pick_stage2(const sf_conv_desc* d, const sf::ConvArgs& a) {
+  // 3x3 with a reduction of at most 32 (an image stem): one dense tile on the
+  // matrix cores, whatever the density.
+  if (d->in_dtype == SF_F32 && sf::mfma_conv_applicable(a)) return Stage2::kMfma;
+  if (sf::band_applicable(a)) return Stage2::kBand;
+  // The row-band kernel where the pixel-tile kernel would have to stream its
+  // weights (C_in > 128 at 28x28 / 14x14); measured faster there, slower
+  // where the pixel-tile weights stay resident.
+  if (sf::rows_kc_applicable(a) && !(sf::px3_applicable(a) && sf::px3_resident(a))) return Stage2::kRowsKc;
+  if (sf::px3_applicable(a)) return Stage2::kPx3;
+  if (sf::flat_applicable(a)) return Stage2::kFlat;
+  return Stage2::kGather;
+}
+
+int run_stage2(Stage2 k, const sf_conv_desc* d, const sf::ConvArgs& a, void* stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = hipSuccess;
+  const char* what = "conv_gather launch";
+  switch (k) {
+    case Stage2::kMfma: rc = sf::launch_conv_mfma(a, d->in_dtype, d->out_dtype, st); what = "conv_mfma launch"; break;
+    case Stage2::kBand: rc = sf::launch_conv_band(a, d->in_dtype, d->out_dtype, st); what = "conv_rows launch"; break;
+    case Stage2::kRowsKc:
+      rc = sf::launch_conv_rows_kc(a, d->in_dtype, d->out_dtype, st);
+      what = "conv_rows_kc launch";
+      break;
+    case Stage2::kPx3: rc = sf::launch_conv_px3(a, d->in_dtype, d->out_dtype, st); what = "conv_px3 launch"; break;
+    case Stage2::kFlat: rc = sf::launch_conv_flat(a, d->in_dtype, d->out_dtype, st); what = "conv_flat launch"; break;
+    case Stage2::kGather: rc = sf::launch_conv(a, d->in_dtype, d->out_dtype, st); break;
+  }
+  if (rc != hipSuccess) return hip_fail(rc, what);
+  return SF_OK;
+}
+
+// Prescan into word planes ([frame][cwp][hw]) for the pixel-tile kernels,
+// which load one bitmap word of 64 neighbouring pixels at a time; every other
+// Stage 2 kernel reads the [hw][cwp] words of sf_prescan_pack.
+int prescan_for(const sf_conv_desc* d, int64_t frames, const void* x, float threshold, bool planar, uint32_t* bits,
+                uint32_t* flags, void* stream) {
+  sf::PackArgs pa = pack_args(x, frames, d->c_in, d->h_in, d->w_in, threshold, bits, flags);
+  pa.planar = planar ? 1 : 0;
+  const int rc = sf::launch_pack(pa, d->in_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "prescan_pack launch");
+  return SF_OK;
+}
+
+void use_planes(sf::ConvArgs& a) {
+  a.bm_ps = 1;
+  a.bm_ws = a.hw_in;
 }
 
 // ---- timing -----------------------------------------------------------------
@@ -352,39 +408,7 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
   if (bits == nullptr || flags == nullptr || x == nullptr || wt == nullptr || y == nullptr)
     return fail(SF_ERR_INVALID, "NULL pointer");
   const sf::ConvArgs a = conv_args(d, d->n, bits, flags, x, wt, bias, y, false);
-  // 3x3 with a reduction of at most 32 (an image stem): one dense tile on the
-  // matrix cores, whatever the density.
-  if (d->in_dtype == SF_F32 && sf::mfma_conv_applicable(a)) {
-    rc = sf::launch_conv_mfma(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
-    if (rc != hipSuccess) return hip_fail(rc, "conv_mfma launch");
-    return SF_OK;
-  }
-  if (sf::band_applicable(a)) {
-    rc = sf::launch_conv_band(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
-    if (rc != hipSuccess) return hip_fail(rc, "conv_rows launch");
-    return SF_OK;
-  }
-  // The row-band kernel where the pixel-tile kernel would have to stream its
-  // weights (C_in > 128 at 28x28 / 14x14); measured faster there, slower
-  // where the pixel-tile weights stay resident.
-  if (sf::rows_kc_applicable(a) && !(sf::px3_applicable(a) && sf::px3_resident(a))) {
-    rc = sf::launch_conv_rows_kc(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
-    if (rc != hipSuccess) return hip_fail(rc, "conv_rows_kc launch");
-    return SF_OK;
-  }
-  if (sf::px3_applicable(a)) {
-    rc = sf::launch_conv_px3(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
-    if (rc != hipSuccess) return hip_fail(rc, "conv_px3 launch");
-    return SF_OK;
-  }
-  if (sf::flat_applicable(a)) {
-    rc = sf::launch_conv_flat(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
-    if (rc != hipSuccess) return hip_fail(rc, "conv_flat launch");
-    return SF_OK;
-  }
-  rc = sf::launch_conv(a, d->in_dtype, d->out_dtype, static_cast<hipStream_t>(stream));
-  if (rc != hipSuccess) return hip_fail(rc, "conv_gather launch");
-  return SF_OK;
+  return run_stage2(pick_stage2(d, a), d, a, stream);
 }
 
 // ---- sparse linear ------------------------------------------------------------
@@ -629,9 +653,13 @@ int sf_conv2d_forward(const sf_conv_desc* d, const void* x, const float* wt, con
     }
   }
   const Workspace ws = carve(workspace, d->n, d->c_in, d->h_in, d->w_in);
-  rc = sf_prescan_pack(x, d->in_dtype, d->n, d->c_in, d->h_in, d->w_in, threshold, ws.bits, ws.flags, stream);
+  sf::ConvArgs a = conv_args(d, d->n, ws.bits, ws.flags, x, wt, bias, y, false);
+  const Stage2 k = pick_stage2(d, a);
+  const bool planar = k == Stage2::kPx3;
+  rc = prescan_for(d, d->n, x, threshold, planar, ws.bits, ws.flags, stream);
   if (rc != SF_OK) return rc;
-  return sf_conv2d_sparse(d, ws.bits, ws.flags, x, wt, bias, y, stream);
+  if (planar) use_planes(a);
+  return run_stage2(k, d, a, stream);
 }
 
 }  // extern "C"
@@ -708,10 +736,12 @@ int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const f
   if (workspace_bytes < sf_conv_lif_workspace_size(d, T)) return fail(SF_ERR_WORKSPACE, "workspace too small");
   const int64_t frames = d->n * (int64_t)T;
   const Workspace ws = carve(workspace, frames, d->c_in, d->h_in, d->w_in);
-  rc = sf_prescan_pack(x, d->in_dtype, frames, d->c_in, d->h_in, d->w_in, threshold, ws.bits, ws.flags, stream);
-  if (rc != SF_OK) return rc;
   // Flags/chunks are indexed by frame t*N + n over all T*N frames.
   sf::ConvArgs a = conv_args(d, frames, ws.bits, ws.flags, x, wt, bias, spikes, true);
+  const bool planar = sf::px3_applicable(a);
+  rc = prescan_for(d, frames, x, threshold, planar, ws.bits, ws.flags, stream);
+  if (rc != SF_OK) return rc;
+  if (planar) use_planes(a);
   a.total_groups = d->n * (int64_t)a.groups_per_frame;
   a.v_out = v_out;
   a.v_init = v_init;

@@ -211,7 +211,13 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
             const int r = j * BITS + px_first_bit(m);
             m &= m - 1;
             float xv = 1.f;
-            if (value) xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * xcs]);
+            if (value) {
+              xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * xcs]);
+              // Waited for here, in the value path: otherwise every round's
+              // products wait for all memory operations in flight (the next
+              // chunk's streamed rows and bitmap words among them).
+              __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+            }
             px_add_row(acc, chunk, r, xv);
           }
         }
@@ -407,7 +413,12 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(XV ? 2
               const int r = j * BITS + px_first_bit(m);
               m &= m - 1;
               float xv = 1.f;
-              if (value) xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * hw]);
+              if (value) {
+                xv = to_f32<TIn>(xp[(int64_t)(c * kPxChunkCh + r) * hw]);
+                // Waited for in the value path only (the step's prefetches
+                // stay in flight during the bitmap path's rounds).
+                __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+              }
               px_add_row(acc, chunk, r, xv);
             }
           }

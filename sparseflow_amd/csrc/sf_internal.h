@@ -45,6 +45,7 @@ struct PackArgs {
   int c, hw, cwp, csplit, vec;
   int64_t chunks_per_frame, total_chunks;
   float cutoff;
+  int planar;  // 1: words as [frame][cwp][hw] (word planes), 0: [frame][hw][cwp]
 };
 
 struct TilesArgs {
@@ -71,6 +72,11 @@ struct ConvArgs {
   int64_t n;           // frames of y (conv) / batch N (LIF)
   int64_t total_groups;
   int c_in, h_in, w_in, c_out, h_out, w_out, k, s, p, cwp;
+  // Bitmap word w of input pixel q of a frame sits at q * bm_ps + w * bm_ws
+  // words from the frame's start: (cwp, 1) for the [hw][cwp] layout of
+  // sf_prescan_pack, (1, hw_in) for word planes (kernels that load one word
+  // of 64 pixels at a time; px3 only).
+  int bm_ps, bm_ws;
   int hw_in, hw_out, groups_per_frame;
   int chunk;                 // flag chunk (pixels)
   int64_t chunks_per_frame;

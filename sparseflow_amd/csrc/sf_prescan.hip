@@ -80,8 +80,9 @@ __global__ __launch_bounds__(512) void k_pack(PackArgs a) {
   const float cut = a.cutoff;
   uint32_t nb = 0;
 
-  // Staging: chunk lc of the block owns s_words[lc * chunk * cwp ...].
-  const bool stage = cpb * 64 * VEC * a.cwp <= kPackStageWords;
+  // Staging: chunk lc of the block owns s_words[lc * chunk * cwp ...].  (Word
+  // planes need none: a lane's VEC words of one plane are consecutive.)
+  const bool stage = !a.planar && cpb * 64 * VEC * a.cwp <= kPackStageWords;
   uint32_t* sw = s_words + lc * (64 * VEC) * a.cwp;
   int64_t frame = 0, chk = 0;
   if (chunk_ok) {
@@ -123,7 +124,18 @@ __global__ __launch_bounds__(512) void k_pack(PackArgs a) {
             }
           }
         }
-        if (stage) {
+        if (a.planar) {
+          // Plane cw of the frame: pixels p0 .. p0+VEC-1 (hw is a multiple
+          // of VEC, so the VEC words are aligned to VEC words).
+          uint32_t* pw = a.bits + (frame * a.cwp + cw) * (int64_t)a.hw + p0;
+          if constexpr (VEC == 4) {
+            *reinterpret_cast<uint4*>(pw) = make_uint4(word[0], word[1], word[2], word[3]);
+          } else if constexpr (VEC == 2) {
+            *reinterpret_cast<uint2*>(pw) = make_uint2(word[0], word[1]);
+          } else {
+            pw[0] = word[0];
+          }
+        } else if (stage) {
 #pragma unroll
           for (int i = 0; i < VEC; ++i) sw[(lane * VEC + i) * a.cwp + cw] = word[i];
         } else if (a.cwp == 1) {

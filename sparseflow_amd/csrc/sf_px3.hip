@@ -112,19 +112,23 @@ __device__ __forceinline__ uint32_t px3_select(const uint32_t (&w)[9], int t) {
 }
 
 // Bitmap word c of each of the lane's nine input taps (0 outside the frame),
-// bf = the frame's bitmap.  Raw buffer loads over the frame's words: a tap
-// outside the frame gets an offset past num_records, which the hardware
-// returns as 0, so no instruction has to touch the loaded values until they
-// are used (the next chunk's words are requested a whole chunk walk ahead).
+// bf = the frame's bitmap (word c of pixel q at q * bm_ps + c * bm_ws).  Raw
+// buffer loads over the frame's words: a tap outside the frame gets an
+// offset past num_records, which the hardware returns as 0, so no
+// instruction has to touch the loaded values until they are used (the next
+// chunk's words are requested a whole chunk walk ahead).  With word planes
+// (bm_ps = 1) the 64 lanes of a load read one run of neighbouring words;
+// with [hw][cwp] words each lane touches its own cache line once cwp >= 8.
 __device__ __forceinline__ void px3_load_words(uint32_t (&w)[9], const uint32_t* __restrict__ bf,
                                                const ConvArgs& a, int ih0, int iw0, int c) {
   const uint32_t frame_bytes = (uint32_t)a.hw_in * (uint32_t)a.cwp * 4u;
   const auto rs = buf_rsrc(bf, frame_bytes);
+  const uint32_t cofs = (uint32_t)c * (uint32_t)a.bm_ws;
 #pragma unroll
   for (int tp = 0; tp < 9; ++tp) {
     const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
     const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
-    const uint32_t off = in ? ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.cwp + (uint32_t)c) * 4u : 0x80000000u;
+    const uint32_t off = in ? ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.bm_ps + cofs) * 4u : 0x80000000u;
     w[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
   }
 }
@@ -369,6 +373,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
             if (value) {
               const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
               xv = to_f32<TIn>(xf[(int64_t)(c * kPx3Ch + bit) * a.hw_in + ih * a.w_in + iw]);
+              // Waited for here, in the value path: otherwise every round's
+              // products wait for all memory operations in flight, which
+              // include the next chunk's streamed rows and bitmap words.
+              __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
             }
             px3_add_row<CO>(acc, chunk, bit * 9 + tap, xv);
           }
@@ -469,13 +477,15 @@ __device__ __forceinline__ void px3w_load_words(uint32_t (&lo)[9], uint32_t (&hi
   const uint32_t frame_bytes = (uint32_t)a.hw_in * (uint32_t)a.cwp * 4u;
   const auto rs = buf_rsrc(bf, frame_bytes);
   const bool two = c0 + 1 < a.cwp;
+  const uint32_t cofs = (uint32_t)c0 * (uint32_t)a.bm_ws;
+  const int next = a.bm_ws * 4;  // bytes from word c0 to word c0 + 1 of a pixel
 #pragma unroll
   for (int tp = 0; tp < 9; ++tp) {
     const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
     const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
-    const uint32_t off = in ? ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.cwp + (uint32_t)c0) * 4u : 0x80000000u;
+    const uint32_t off = in ? ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.bm_ps + cofs) * 4u : 0x80000000u;
     lo[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
-    hi[tp] = two ? __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(off + 4u), 0, 0) : 0u;
+    hi[tp] = two ? __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, next, 0) : 0u;
   }
 }
 

@@ -161,3 +161,38 @@ def test_px3_and_gather_agree(stride):
     y_gather, k2 = _run(x.to(DEV), w[:6].contiguous().to(DEV), None, stride)
     assert "conv_px3" in k1 and "conv_gather" in k2
     assert torch.allclose(y_px[:, :6], y_gather, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("case", [
+    (4, 256, 14, 14, 64, 2),    # streamed chunks, 8 words per pixel
+    (3, 512, 7, 9, 128, 1),     # 16 words per pixel, ragged plane
+    (3, 96, 12, 10, 40, 1),     # 32-channel slices, second super-chunk of one word
+    (2, 64, 9, 13, 64, 2),      # resident 64-channel walk, two words
+    (2, 300, 5, 6, 36, 1),      # last word partial, ragged channel group
+])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_px3_word_planes_equal_pixel_words(case, dtype):
+    # sf_conv2d_forward prescans into word planes for the pixel-tile kernels;
+    # sf_prescan_pack + sf_conv2d_sparse hand them the [hw][cwp] words.  Same
+    # kernel, same walk order: the outputs agree bit for bit, and with the
+    # float64 reference.
+    N, C, H, W, Co, s = case
+    announce(f"px3 word planes {case} {dtype}")
+    x = spikes((N, C, H, W), 0.05, seed=N + C + Co).to(dtype)
+    x[0, :, 1, 1:3] = x[0, :, 1, 1:3] * 0.5  # one non-binary tile: the value path
+    w = _weights(Co, C, seed=C * 3 + Co)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(8)) * 0.1
+    xd, wt, bd = x.to(DEV), _lib.tap_major_weight(w.to(DEV)), b.to(DEV)
+    Ho, Wo = (H + 2 - 3) // s + 1, (W + 2 - 3) // s + 1
+    code = _lib.dtype_code(dtype)
+    desc = _lib.conv_desc(N, C, H, W, Co, Ho, Wo, 3, s, 1, code, _lib.dtype_code(torch.float32))
+    ws = torch.empty(max(_lib.conv2d_workspace_size(desc), 1), dtype=torch.uint8, device=DEV)
+    y_planes = torch.empty((N, Co, Ho, Wo), dtype=torch.float32, device=DEV)
+    _lib.conv2d_forward(desc, xd, wt, bd, 0.0, ws, y_planes)
+    bits, flags = _lib.prescan_pack(xd, 0.0)
+    y_words = torch.empty_like(y_planes)
+    _lib.conv2d_sparse(desc, bits, flags, xd, wt, bd, y_words)
+    torch.cuda.synchronize()
+    assert torch.equal(y_planes, y_words)
+    ok, err, _ = close(y_planes, oconv.sparse_conv2d_ref(x.float(), w, b, s, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
