@@ -419,6 +419,179 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
 }
 
 // ---------------------------------------------------------------------------
+// Streamed variant for C_in > 128 (64 output channels per workgroup, weight
+// chunks of 32 input channels streamed through the two LDS buffers) over
+// tiles of the flattened (frame, pixel) axis: all 64 lanes carry an output
+// pixel on planes of 49 or 196 pixels (per-frame tiles leave 23% of them
+// idle there), and the host sizes the workgroup so that the wave-tiles
+// spread evenly over the CUs (one workgroup per CU, since the two chunk
+// buffers fill the LDS).  A lane's frame, input window and output offsets
+// are its own; the walk and the chunk pipeline are k_conv_px3's.  Output
+// element (co, oh, ow) = bias[co] + its active taps summed by one lane in
+// (chunk, tap, ci) order, as there.
+// ---------------------------------------------------------------------------
+
+// Direct-to-LDS loads of chunk c by the nw wavefronts of the workgroup.
+__device__ __forceinline__ void load_chunk_px3_nw(char* buf, const float* __restrict__ wt, int c, int krows,
+                                                  int c_out, int co0, int wave, int nw, int lane) {
+  typedef Px3Layout<64> L;
+  for (int u = wave; u < L::units; u += nw) {
+    const int pos = u * 64 + lane;
+    const int r = pos / L::stride;
+    const int q = pos - r * L::stride;
+    const int row = c * kPx3Rows + r;
+    const int col = co0 + 4 * q;
+    const float* src = (q < L::pieces && r < kPx3Rows && row < krows && col < c_out) ? wt + (int64_t)row * c_out + col : wt;
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+  }
+}
+
+// px3_load_words with the frame's start as a per-lane byte offset into one
+// buffer resource over every frame's bitmap (below 2^31 bytes).
+__device__ __forceinline__ void px3_load_words_at(uint32_t (&w)[9], __amdgpu_buffer_rsrc_t rs, uint32_t fbase,
+                                                  const ConvArgs& a, int ih0, int iw0, int c) {
+  const uint32_t cofs = (uint32_t)c * (uint32_t)a.bm_ws;
+#pragma unroll
+  for (int tp = 0; tp < 9; ++tp) {
+    const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
+    const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
+    const uint32_t off = in ? fbase + ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.bm_ps + cofs) * 4u : 0x80000000u;
+    w[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
+  }
+}
+
+template <typename TIn, typename TOut>
+__global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const uint32_t* __restrict__ bits,
+                                                               const uint32_t* __restrict__ flags,
+                                                               const TIn* __restrict__ x, const float* __restrict__ wt,
+                                                               const float* __restrict__ bias_p, TOut* __restrict__ y,
+                                                               int groups, int nchunks) {
+  typedef Px3Layout<64> LY;
+  extern __shared__ __align__(16) char smem[];
+  __shared__ float s_seed[64];
+  const int nw = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6));
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int blk = groups >= 8 ? xcd_local_block((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
+  const int grp = blk % groups;
+  const int co0 = grp * 64;
+  const int krows = a.c_in * 9;
+  const int hwo = a.hw_out;
+  const int total_px = (int)(a.n * hwo);  // below 2^31 (the host checks the output size)
+  const int total = (total_px + 63) / 64;
+  const int nblk = (int)(gridDim.x / groups);
+  const uint32_t frame_bytes = (uint32_t)a.hw_in * (uint32_t)a.cwp * 4u;
+  const auto rs_bits = buf_rsrc(bits, (uint32_t)((int64_t)a.n * frame_bytes));
+  if (threadIdx.x < 64) {
+    const int co = co0 + (int)threadIdx.x;
+    s_seed[threadIdx.x] = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
+  }
+  for (int pass = blk / groups; pass * nw < total; pass += nblk) {
+    // The lane index is formed anew in each pass (in asm, which the
+    // optimiser cannot hoist): kept live across the loop it was spilled, and
+    // its reload waited for the previous pass's stores.
+    int lane;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    const int t = pass * nw + wave;
+    const int g = t * 64 + lane;
+    const bool mine = g < total_px;
+    const int gc = mine ? g : total_px - 1;  // lanes past the end form valid addresses
+    const int sample = gc / hwo;
+    const int q = gc - sample * hwo;
+    const int oh = q / a.w_out, ow = q - (q / a.w_out) * a.w_out;
+    const int ih0 = oh * a.s - 1, iw0 = ow * a.s - 1;
+    const uint32_t fbase = (uint32_t)sample * frame_bytes;
+    // The lane's output offset (bytes), formed here so that only it, not the
+    // pixel index, stays live across the chunk loop; lanes without a pixel
+    // start past the end of y.
+    constexpr uint32_t B = (uint32_t)sizeof(TOut);
+    const uint32_t yrange = (uint32_t)total_px * (uint32_t)a.c_out * B;
+    const uint32_t ybase =
+        mine ? (((uint32_t)sample * (uint32_t)a.c_out + (uint32_t)co0) * (uint32_t)hwo + (uint32_t)q) * B : yrange;
+    // This pass's first words, in flight during the first chunk's load.
+    uint32_t wn[9];
+    px3_load_words_at(wn, rs_bits, fbase, a, ih0, iw0, 0);
+    // The multiply-by-x path for the whole tile when any lane's input rows
+    // hold a non-binary value.
+    const bool value = __ballot(mine && rows_value_path(a, flags, sample, ih0, ih0 + 2)) != 0ull;
+    __syncthreads();  // the previous pass is done with both buffers (and s_seed is written)
+    {
+      int ll = lane;
+      asm volatile("" : "+v"(ll));
+      load_chunk_px3_nw(smem, wt, 0, krows, a.c_out, co0, wave, nw, ll);
+    }
+    float acc[64];
+#pragma unroll
+    for (int co = 0; co < 64; ++co) acc[co] = s_seed[co];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+      // Chunk c+1 streams into the other buffer; it was last read during
+      // chunk c-1, which every wavefront finished before the last barrier.
+      if (c + 1 < nchunks) {
+        int ll = lane;
+        asm volatile("" : "+v"(ll));
+        load_chunk_px3_nw(smem + ((c + 1) & 1) * LY::chunk_bytes, wt, c + 1, krows, a.c_out, co0, wave, nw, ll);
+      }
+      uint32_t w[9];
+#pragma unroll
+      for (int tp = 0; tp < 9; ++tp) w[tp] = wn[tp];
+      // Opaque to the optimiser: a select between array elements would
+      // otherwise be folded into an indexed load from scratch memory.
+      asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]),
+                   "+v"(w[7]), "+v"(w[8]));
+      if (c + 1 < nchunks) px3_load_words_at(wn, rs_bits, fbase, a, ih0, iw0, c + 1);
+      if (mine) {
+        uint32_t nz = 0u;
+#pragma unroll
+        for (int tp = 0; tp < 9; ++tp) nz |= (w[tp] != 0u ? 1u : 0u) << tp;
+        const char* chunk = smem + (c & 1) * LY::chunk_bytes;
+        uint32_t m = 0u;
+        int tap = 0;
+        // Per-lane cursor over (tap, ci): the wavefront loops while any
+        // lane has spikes left.
+        while ((m | nz) != 0u) {
+          if (m == 0u) {
+            tap = __builtin_ctz(nz);
+            nz &= nz - 1u;
+            m = px3_select(w, tap);
+          }
+          const int bit = __builtin_ctz(m);
+          m &= m - 1u;
+          float xv = 1.f;
+          if (value) {
+            const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+            const TIn* __restrict__ xf = x + (int64_t)sample * a.c_in * a.hw_in;
+            xv = to_f32<TIn>(xf[(int64_t)(c * kPx3Ch + bit) * a.hw_in + ih * a.w_in + iw]);
+            // Waited for here, in the value path: otherwise every round's
+            // products wait for the next chunk's rows and words too.
+            __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+          }
+          px3_add_row<64>(acc, chunk, bit * 9 + tap, xv);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+    {
+      // Every frame's output planes as one buffer (below 2^31 bytes): lanes
+      // without a pixel start at its end; channels past C_out are skipped.
+      int hwo_t = hwo, c_out_t = a.c_out;
+      asm volatile("" : "+s"(hwo_t), "+s"(c_out_t));
+      const int nco = min(64, c_out_t - co0);
+      const auto rs = buf_rsrc(y, yrange);
+      const uint32_t plane = (uint32_t)hwo_t * B;
+      uint32_t off = ybase;
+#pragma unroll
+      for (int co = 0; co < 64; ++co) {
+        if (co < nco) BufIO<TOut>::store(from_f32<TOut>(acc[co]), rs, (int)off, 0);
+        off += plane;
+        asm volatile("" : "+v"(off));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Wide-chunk variant of the plain conv for C_in <= 64 and 64 output channels
 // per workgroup: the weight rows of all 64 input channels (576 rows of 272
 // bytes, 156.7 KB) are resident, and each lane walks its nine taps'
@@ -727,6 +900,40 @@ int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
+// Wavefronts per workgroup for the flattened streamed kernel: as many
+// rounds of one workgroup per CU as 16-wave workgroups would need, with the
+// wave-tiles spread evenly over them.
+int px3s_waves(int64_t wave_tiles) {
+  const int64_t cus = num_cus();
+  const int64_t rounds = (wave_tiles + cus * kRowsWaves - 1) / (cus * kRowsWaves);
+  const int64_t w = (wave_tiles + cus * rounds - 1) / (cus * rounds);
+  return (int)(w < 1 ? 1 : (w > kRowsWaves ? kRowsWaves : w));
+}
+
+template <typename TIn, typename TOut>
+int launch_px3s_to(const ConvArgs& a, hipStream_t stream) {
+  typedef Px3Layout<64> LY;
+  const int groups = (a.c_out + 63) / 64;
+  const int nchunks = (a.c_in + kPx3Ch - 1) / kPx3Ch;
+  const int64_t tiles = (a.n * (int64_t)a.hw_out + 63) / 64;
+  const int nw = px3s_waves(tiles * groups);
+  const int64_t per_group = (tiles + nw - 1) / nw;
+  const int grid = (int)(groups * per_group);
+  constexpr auto kern = k_conv_px3s<TIn, TOut>;
+  const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
+  if (e != (int)hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), (size_t)2 * LY::chunk_bytes, stream, a, a.bits, a.flags,
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, nchunks);
+  return (int)hipGetLastError();
+}
+
+template <typename TIn>
+int launch_px3s_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+  if (out_dtype == SF_F16) return launch_px3s_to<TIn, __half>(a, stream);
+  if (out_dtype == SF_BF16) return launch_px3s_to<TIn, __hip_bfloat16>(a, stream);
+  return launch_px3s_to<TIn, float>(a, stream);
+}
+
 template <int CO>
 int launch_px3_co(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
   if (in_dtype == SF_F16) return launch_px3_t<__half, float, CO, false>(a, out_dtype, stream);
@@ -760,6 +967,15 @@ int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
   const int nch = (a.c_in + kPx3Ch - 1) / kPx3Ch;
   if (nch > Px3Layout<64>::resident_chunks && nch <= Px3Layout<32>::resident_chunks)
     return launch_px3_co<32>(a, in_dtype, out_dtype, stream);
+  // C_in > 128: streamed chunks over flattened tiles, when every frame's
+  // bitmap and every frame's output planes are addressable by one buffer
+  // resource each.
+  if (nch > Px3Layout<32>::resident_chunks && a.n * (int64_t)a.hw_in * a.cwp * 4 < 0x7fffffffLL &&
+      a.n * (int64_t)(a.c_out + 64) * a.hw_out * out_bytes < 0x7fffffffLL) {
+    if (in_dtype == SF_F16) return launch_px3s_t<__half>(a, out_dtype, stream);
+    if (in_dtype == SF_BF16) return launch_px3s_t<__hip_bfloat16>(a, out_dtype, stream);
+    return launch_px3s_t<float>(a, out_dtype, stream);
+  }
   return launch_px3_co<64>(a, in_dtype, out_dtype, stream);
 }
 

@@ -196,3 +196,21 @@ def test_px3_word_planes_equal_pixel_words(case, dtype):
     assert torch.equal(y_planes, y_words)
     ok, err, _ = close(y_planes, oconv.sparse_conv2d_ref(x.float(), w, b, s, 1), **FP32_TOL)
     assert ok, f"max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", [(3, 256, 9, 9, 64, 2), (5, 160, 7, 7, 100, 1)])
+def test_px3_streamed_half_output(case, dtype):
+    # C_in > 128: streamed chunks over tiles of the flattened (frame, pixel)
+    # axis (a tile spans up to three 25- or 49-pixel planes), half output.
+    N, C, H, W, Co, s = case
+    x = spikes((N, C, H, W), 0.05, seed=C + N)
+    x[1, :, 2] = x[1, :, 2] * 0.75  # a non-binary row inside a frame-spanning tile
+    w = _weights(Co, C, seed=C + 1)
+    b = torch.linspace(-0.3, 0.3, Co)
+    announce(f"px3 streamed {case} {dtype}")
+    xr = x.to(dtype).float()
+    y, kernels = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), s)
+    assert "conv_px3" in kernels and y.dtype == dtype
+    ok, err, _ = close(y, oconv.conv2d_ref(xr, w, b, s, 1), atol=1e-2, rtol=1e-2)
+    assert ok, f"max abs err {err}"
