@@ -150,7 +150,10 @@ int sf_conv2d_sparse(const sf_conv_desc* desc, const uint32_t* bits,
 /* Stage 1a + Stage 2 in one call; the bitmap lives in `workspace`.  3x3
  * stride-1 layers with c_in <= 64 on 32-wide frames (other than an image
  * stem) run as one launch with the prescan fused into the conv
- * ("conv_rows_fused"; the workspace is then unused).
+ * ("conv_rows_fused"; the workspace is then unused).  The workspace's
+ * contents are private to the call: when Stage 2 is the pixel-tile kernel
+ * the bitmap is written as word planes [n, cwp, h_in*w_in] instead of
+ * sf_prescan_pack's [n, h_in*w_in, cwp] (same words, same size).
  * Replaces sparse_conv2d_forward's device work (Kernels/conv2d.py:893-1178). */
 int sf_conv2d_forward(const sf_conv_desc* desc, const void* x, const float* wt,
                       const float* bias, float threshold, void* workspace,

@@ -651,14 +651,16 @@ __device__ __forceinline__ void px3w_load_words(uint32_t (&lo)[9], uint32_t (&hi
   const auto rs = buf_rsrc(bf, frame_bytes);
   const bool two = c0 + 1 < a.cwp;
   const uint32_t cofs = (uint32_t)c0 * (uint32_t)a.bm_ws;
-  const int next = a.bm_ws * 4;  // bytes from word c0 to word c0 + 1 of a pixel
+  const uint32_t next = (uint32_t)a.bm_ws * 4u;  // bytes from word c0 to word c0 + 1 of a pixel
 #pragma unroll
   for (int tp = 0; tp < 9; ++tp) {
     const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
     const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
     const uint32_t off = in ? ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.bm_ps + cofs) * 4u : 0x80000000u;
     lo[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
-    hi[tp] = two ? __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, next, 0) : 0u;
+    // The whole offset in the VGPR (soffset stays 0, as in every buffer
+    // access of this library); past the frame it stays past num_records.
+    hi[tp] = two ? __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(off + next), 0, 0) : 0u;
   }
 }
 
