@@ -214,3 +214,46 @@ def test_px3_streamed_half_output(case, dtype):
     assert "conv_px3" in kernels and y.dtype == dtype
     ok, err, _ = close(y, oconv.conv2d_ref(xr, w, b, s, 1), atol=1e-2, rtol=1e-2)
     assert ok, f"max abs err {err}"
+
+
+def _random_cases(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(n):
+        c_in = int(torch.randint(1, 600, (1,), generator=g))
+        c_out = 4 * int(torch.randint(1, 50, (1,), generator=g))
+        h = int(torch.randint(1, 24, (1,), generator=g))
+        w = int(torch.randint(1, 40, (1,), generator=g))
+        frames = int(torch.randint(1, 9, (1,), generator=g))
+        s = 1 + int(torch.randint(0, 2, (1,), generator=g))
+        dens = [0.003, 0.03, 0.2][int(torch.randint(0, 3, (1,), generator=g))]
+        out.append((frames, c_in, h, w, c_out, s, dens))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(40, 2026))
+def test_px3_random_shapes(case):
+    # Random geometry across every pixel-tile variant (resident 64- and
+    # 32-channel slices, streamed chunks over flattened tiles, ragged words,
+    # planes smaller than a tile): the forward (word planes) against the
+    # float64 reference, and bit for bit against the two-stage path with the
+    # [hw][cwp] words.
+    N, C, H, W, Co, s, dens = case
+    announce(f"px3 random {case}")
+    x = spikes((N, C, H, W), dens, seed=C * 7 + H)
+    w = _weights(Co, C, seed=Co + W)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(C)) * 0.1
+    xd, wt, bd = x.to(DEV), _lib.tap_major_weight(w.to(DEV)), b.to(DEV)
+    Ho, Wo = (H + 2 - 3) // s + 1, (W + 2 - 3) // s + 1
+    desc = _lib.conv_desc(N, C, H, W, Co, Ho, Wo, 3, s, 1, _lib.dtype_code(torch.float32),
+                          _lib.dtype_code(torch.float32))
+    ws = torch.empty(max(_lib.conv2d_workspace_size(desc), 1), dtype=torch.uint8, device=DEV)
+    y1 = torch.empty((N, Co, Ho, Wo), dtype=torch.float32, device=DEV)
+    _lib.conv2d_forward(desc, xd, wt, bd, 0.0, ws, y1)
+    bits, flags = _lib.prescan_pack(xd, 0.0)
+    y2 = torch.empty_like(y1)
+    _lib.conv2d_sparse(desc, bits, flags, xd, wt, bd, y2)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    ok, err, _ = close(y1, oconv.sparse_conv2d_ref(x, w, b, s, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
