@@ -622,9 +622,9 @@ constexpr int px3w_bytes() { return CO == 64 ? kPx3wBytes : kPx3w32Bytes; }
 // never used.
 template <int CO>
 __device__ __forceinline__ void load_rows_px3w(char* buf, const float* __restrict__ wt, int krows, int c_out, int co0,
-                                               int wave, int lane) {
+                                               int wave, int nw, int lane) {
   if constexpr (CO == 64) {
-    for (int u = wave; u < kPx3wUnits; u += kRowsWaves) {
+    for (int u = wave; u < kPx3wUnits; u += nw) {
       const int pos = u * 64 + lane;
       const int r = pos / 17, q = pos - r * 17;
       const int col = co0 + 4 * q;
@@ -632,7 +632,7 @@ __device__ __forceinline__ void load_rows_px3w(char* buf, const float* __restric
       __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
     }
   } else {
-    for (int u = wave; u < kPx3w32Units; u += kRowsWaves) {
+    for (int u = wave; u < kPx3w32Units; u += nw) {
       const int pos = u * 64 + lane;
       const int r = pos >> 3, q = pos & 7;
       const int col = co0 + 4 * (q ^ ((r >> 1) & 7));
@@ -692,6 +692,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   __shared__ float s_seed[CO];
   const int lane0 = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6));  // tiles per pass
   const int blk = groups >= 8 ? xcd_local_block((int)blockIdx.x, (int)gridDim.x) : (int)blockIdx.x;
   const int grp = blk % groups;
   const int co0 = grp * CO;
@@ -707,14 +708,14 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
     const float b = (bias_p != nullptr && co < a.c_out) ? bias_p[co] : 0.f;
     s_seed[threadIdx.x] = LIF ? L.vr_term + b : b;
   }
-  load_rows_px3w<CO>(smem, wt, a.c_in * 9, a.c_out, co0, wave, lane0);
+  load_rows_px3w<CO>(smem, wt, a.c_in * 9, a.c_out, co0, wave, nw, lane0);
   // The first tile's words; later tiles' are requested before the previous
   // tile's stores (the vector memory counter retires in issue order).  The
   // fused LIF form requests a tile's first words at the tile and prefetches
   // per step (the T steps of a tile are its long stretch of work).
   uint32_t nlo[9], nhi[9];
   if constexpr (!LIF) {
-    const int t = (blk / groups) * kRowsWaves + wave;
+    const int t = (blk / groups) * nw + wave;
     if (t < total) {
       const int sample = t / tpf, p0 = (t - sample * tpf) * 64;
       const int q = p0 + min(lane0, hwo - p0 - 1);
@@ -724,10 +725,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   }
   __builtin_amdgcn_s_waitcnt(0);  // this wavefront's direct weight loads have landed
   __syncthreads();
-  for (int pass = blk / groups; pass * kRowsWaves < total; pass += nblk) {
+  for (int pass = blk / groups; pass * nw < total; pass += nblk) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
-    const int t = pass * kRowsWaves + wave;
+    const int t = pass * nw + wave;
     const bool valid = t < total;
     const int sample = valid ? t / tpf : 0;
     const int p0 = valid ? (t - sample * tpf) * 64 : 0;
@@ -831,7 +832,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
       }
     } else {
       {
-        const int tn = (pass + nblk) * kRowsWaves + wave;
+        const int tn = (pass + nblk) * nw + wave;
         if (tn < total) {
           const int ns = tn / tpf, np0 = (tn - ns * tpf) * 64;
           const int nq = np0 + min(lane, hwo - np0 - 1);
@@ -861,17 +862,31 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   }
 }
 
+// Wavefronts per workgroup for the pixel-tile kernels that run one
+// workgroup per CU: as many rounds as 16-wave workgroups would need, with
+// the wave-tiles spread evenly over them.
+int px3s_waves(int64_t wave_tiles) {
+  const int64_t cus = num_cus();
+  const int64_t rounds = (wave_tiles + cus * kRowsWaves - 1) / (cus * kRowsWaves);
+  const int64_t w = (wave_tiles + cus * rounds - 1) / (cus * rounds);
+  return (int)(w < 1 ? 1 : (w > kRowsWaves ? kRowsWaves : w));
+}
+
 template <typename TIn, typename TOut, int CO, bool LIF = false>
 int launch_px3w_to(const ConvArgs& a, hipStream_t stream) {
   const int groups = (a.c_out + CO - 1) / CO;
   const int64_t tiles = a.n * (int64_t)((a.hw_out + 63) / 64);
-  const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
-  const int per_group = (int)(need < num_cus() ? need : num_cus());
-  const int grid = groups * (per_group > 0 ? per_group : 1);
+  // One workgroup per CU (the weights fill the LDS) making the same number
+  // of passes: as many as 16-wave workgroups would need, with the wave-tiles
+  // spread evenly over them (no CU idles through another's last pass).
+  const int nw = px3s_waves(tiles * groups);
+  const int64_t passes = (tiles * groups + (int64_t)num_cus() * nw - 1) / ((int64_t)num_cus() * nw);
+  const int64_t per_group = (tiles + (int64_t)nw * passes - 1) / ((int64_t)nw * passes);
+  const int grid = (int)(groups * (per_group > 0 ? per_group : 1));
   constexpr auto kern = k_conv_px3w<TIn, TOut, CO, LIF>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), (size_t)px3w_bytes<CO>(), stream, a, a.bits, a.flags,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), (size_t)px3w_bytes<CO>(), stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups);
   return (int)hipGetLastError();
 }
@@ -900,16 +915,6 @@ int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype);
   return (int)hipGetLastError();
-}
-
-// Wavefronts per workgroup for the flattened streamed kernel: as many
-// rounds of one workgroup per CU as 16-wave workgroups would need, with the
-// wave-tiles spread evenly over them.
-int px3s_waves(int64_t wave_tiles) {
-  const int64_t cus = num_cus();
-  const int64_t rounds = (wave_tiles + cus * kRowsWaves - 1) / (cus * kRowsWaves);
-  const int64_t w = (wave_tiles + cus * rounds - 1) / (cus * rounds);
-  return (int)(w < 1 ? 1 : (w > kRowsWaves ? kRowsWaves : w));
 }
 
 template <typename TIn, typename TOut>
