@@ -64,6 +64,21 @@ __device__ __forceinline__ void load_chunk_px(char* buf, const float* __restrict
   }
 }
 
+// load_chunk_px by the nw wavefronts of a workgroup sized at run time.
+__device__ __forceinline__ void load_chunk_px_nw(char* buf, const float* __restrict__ wt, int c, int c_in, int c_out,
+                                                 int co0, int wave, int nw, int lane) {
+  const int rows = min(kPxChunkCh, c_in - c * kPxChunkCh);
+  const int units = (rows + 1) / 2;
+  for (int u = wave; u < units; u += nw) {
+    const int r = 2 * u + (lane >> 5);
+    const int piece = ((lane & 31) - r) & 15;
+    const int row = c * kPxChunkCh + r;
+    const int col = co0 + 4 * piece;
+    const float* src = (row < c_in && col < c_out) ? wt + (int64_t)row * c_out + col : wt;
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)(buf + u * 1024), 16, 0, 0);
+  }
+}
+
 // Bitmap words as a lane walks them: 64-bit (two channel words) except for
 // single-word pixels.
 template <int CW>
@@ -133,6 +148,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
   extern __shared__ __align__(16) char smem[];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6));  // tiles per pass
   const int blk = xcd_local_block((int)blockIdx.x, (int)gridDim.x);
   const int grp = blk % groups;
   const int co0 = grp * 64;
@@ -152,14 +168,14 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
 
   if (resident) {
     for (int c = 0; c < nchunks; ++c)
-      load_chunk_px(smem + c * kPxChunkBytes, wt, c, a.c_in, a.c_out, co0, wave, lane);
+      load_chunk_px_nw(smem + c * kPxChunkBytes, wt, c, a.c_in, a.c_out, co0, wave, nw, lane);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
-  // Passes of kRowsWaves tiles.  With more than two chunks every wavefront
-  // takes part in every barrier, including those of a pass past the end.
-  for (int pass = (blk / groups); pass * kRowsWaves < total; pass += nblk) {
-    const int t = pass * kRowsWaves + wave;
+  // Passes of nw tiles.  With more than two chunks every wavefront takes
+  // part in every barrier, including those of a pass past the end.
+  for (int pass = (blk / groups); pass * nw < total; pass += nblk) {
+    const int t = pass * nw + wave;
     const bool valid = t < total;
     const int frame = valid ? t / tpf : 0;
     const int p0 = valid ? (t - frame * tpf) * 64 : 0;
@@ -185,7 +201,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
     const int64_t xcs = ROWS ? 1 : hw;
     if (!resident) {
       __syncthreads();  // the previous pass is done with both buffers
-      load_chunk_px(smem, wt, 0, a.c_in, a.c_out, co0, wave, lane);
+      load_chunk_px_nw(smem, wt, 0, a.c_in, a.c_out, co0, wave, nw, lane);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
@@ -193,7 +209,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
       // Stream chunk c+1 into the other buffer; it was last read during
       // chunk c-1, which every wavefront finished before the last barrier.
       if (!resident && c + 1 < nchunks)
-        load_chunk_px(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, lane);
+        load_chunk_px_nw(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, nw, lane);
       if (mine) {
         WT w[NW];
         const WT* __restrict__ bp =
@@ -576,14 +592,17 @@ int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   const size_t lds = nchunks <= 2 ? (size_t)(nchunks - 1) * kPxChunkBytes + (size_t)last_units * 1024
                                   : (size_t)2 * kPxChunkBytes;
   const int64_t tiles = a.n * (int64_t)((a.hw_in + 63) / 64);
-  const int64_t need = (tiles + kRowsWaves - 1) / kRowsWaves;
-  const int per_group = (int)(need < num_cus() ? need : num_cus());
-  const int grid = groups * (per_group > 0 ? per_group : 1);
+  // Every CU makes the same number of passes (workgroup size from the
+  // wave-tile count).
+  const int nw = even_pass_waves(tiles * groups);
+  const int64_t passes = (tiles * groups + (int64_t)num_cus() * nw - 1) / ((int64_t)num_cus() * nw);
+  const int64_t per_group = (tiles + (int64_t)nw * passes - 1) / ((int64_t)nw * passes);
+  const int grid = (int)(groups * (per_group > 0 ? per_group : 1));
   constexpr auto kern = k_conv_flat<CW, TIn, ROWS>;
   // 1 KB of the LDS is left to the kernel's static arrays.
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype);
   return (int)hipGetLastError();
 }

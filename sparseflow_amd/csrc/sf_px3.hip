@@ -862,16 +862,6 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   }
 }
 
-// Wavefronts per workgroup for the pixel-tile kernels that run one
-// workgroup per CU: as many rounds as 16-wave workgroups would need, with
-// the wave-tiles spread evenly over them.
-int px3s_waves(int64_t wave_tiles) {
-  const int64_t cus = num_cus();
-  const int64_t rounds = (wave_tiles + cus * kRowsWaves - 1) / (cus * kRowsWaves);
-  const int64_t w = (wave_tiles + cus * rounds - 1) / (cus * rounds);
-  return (int)(w < 1 ? 1 : (w > kRowsWaves ? kRowsWaves : w));
-}
-
 template <typename TIn, typename TOut, int CO, bool LIF = false>
 int launch_px3w_to(const ConvArgs& a, hipStream_t stream) {
   const int groups = (a.c_out + CO - 1) / CO;
@@ -879,7 +869,7 @@ int launch_px3w_to(const ConvArgs& a, hipStream_t stream) {
   // One workgroup per CU (the weights fill the LDS) making the same number
   // of passes: as many as 16-wave workgroups would need, with the wave-tiles
   // spread evenly over them (no CU idles through another's last pass).
-  const int nw = px3s_waves(tiles * groups);
+  const int nw = even_pass_waves(tiles * groups);
   const int64_t passes = (tiles * groups + (int64_t)num_cus() * nw - 1) / ((int64_t)num_cus() * nw);
   const int64_t per_group = (tiles + (int64_t)nw * passes - 1) / ((int64_t)nw * passes);
   const int grid = (int)(groups * (per_group > 0 ? per_group : 1));
@@ -923,7 +913,7 @@ int launch_px3s_to(const ConvArgs& a, hipStream_t stream) {
   const int groups = (a.c_out + 63) / 64;
   const int nchunks = (a.c_in + kPx3Ch - 1) / kPx3Ch;
   const int64_t tiles = (a.n * (int64_t)a.hw_out + 63) / 64;
-  const int nw = px3s_waves(tiles * groups);
+  const int nw = even_pass_waves(tiles * groups);
   const int64_t per_group = (tiles + nw - 1) / nw;
   const int grid = (int)(groups * per_group);
   constexpr auto kern = k_conv_px3s<TIn, TOut>;

@@ -11,6 +11,17 @@ constexpr int kRowsWaves = 16;  // wavefronts per row-tile workgroup (one workgr
 // Number of compute units of the current device (cached per device).
 int num_cus();
 
+// Wavefronts per workgroup for a persistent kernel that runs one workgroup
+// per CU over `wave_tiles` wave-sized tiles: as many passes as 16-wave
+// workgroups would need, with the tiles spread evenly over them, so that no
+// CU works through a last pass while the others idle.
+inline int even_pass_waves(int64_t wave_tiles) {
+  const int64_t cus = num_cus();
+  const int64_t rounds = (wave_tiles + cus * kRowsWaves - 1) / (cus * kRowsWaves);
+  const int64_t w = (wave_tiles + cus * rounds - 1) / (cus * rounds);
+  return (int)(w < 1 ? 1 : (w > kRowsWaves ? kRowsWaves : w));
+}
+
 namespace {
 
 // Exchange lane bit S with quad-slot bit S over v[4 * QP] (a butterfly stage
