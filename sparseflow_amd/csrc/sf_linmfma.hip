@@ -19,8 +19,9 @@
 // copy the 64 accumulators between AGPRs and VGPRs every step, which costs
 // more than the products it would skip (an all-zero 128 x 32 slice of x is
 // vanishingly rare at these densities; the spike walk serves sparse inputs).
-// Row blocks are the slow index of the grid so the column blocks of one row
-// block run together and share its x tile through L2.
+// Row blocks are the slow index of the grid and workgroups are placed
+// XCD-locally, so the column blocks of one row block run together on one
+// XCD and share its x tile through that XCD's L2.
 //
 // Replaces the reference's sparse_linear_grouped_kernel (Kernels/linear.py:
 // 360-457: fp16 tl.dot over active groups, dense tiles when all groups are
@@ -123,8 +124,11 @@ __global__ __launch_bounds__(256) void k_linear_mfma(LinMfmaArgs a) {
   const int wave = tid >> 6;
   const int wr = wave >> 1, wc = wave & 1;
   const int ncb = (a.c_out + kLmCols - 1) / kLmCols;
-  const int64_t rb = blockIdx.x / ncb;
-  const int cb = (int)(blockIdx.x - rb * ncb);
+  // The column blocks of a row block share its x tile through L2, which is
+  // per XCD: placed XCD-locally, consecutive tiles run on one XCD.
+  const int bid = xcd_range_block((int)blockIdx.x, (int)gridDim.x);
+  const int64_t rb = bid / ncb;
+  const int cb = (int)(bid - rb * ncb);
   const int64_t r0 = rb * kLmRows;
   const int c0 = cb * kLmCols;
   const int nsteps = a.kp / kLmK;

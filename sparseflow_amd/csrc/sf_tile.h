@@ -177,6 +177,15 @@ __device__ __forceinline__ int xcd_local_block(int i, int n) {
   return (n % kXcds == 0) ? (i % kXcds) * (n / kXcds) + i / kXcds : i;
 }
 
+// xcd_local_block for any n: XCD x (workgroups i with i % 8 == x) takes the
+// contiguous work range [x q + min(x, r), ...) of q + (x < r) items, q = n / 8,
+// r = n % 8.  A bijection on [0, n).
+__device__ __forceinline__ int xcd_range_block(int i, int n) {
+  constexpr int kXcds = 8;
+  const int q = n / kXcds, r = n % kXcds, x = i % kXcds;
+  return x * q + min(x, r) + i / kXcds;
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
