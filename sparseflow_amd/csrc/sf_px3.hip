@@ -1,27 +1,36 @@
 // Stage 2 for 3x3 convolutions (stride 1 or 2, padding 1): 64-pixel output
 // tiles, lane = output pixel.
 //
-// One wavefront owns 64 consecutive output pixels of one frame (a flat run of
-// the h_out*w_out plane) for 64 output channels: lane = output pixel, one
-// accumulator register per output channel.  Input channels are taken in
-// chunks of 32 (one bitmap word per input pixel).  For a chunk, each lane
-// loads the word of each of its 9 input taps (0 outside the frame) and then
-// walks its own spikes in (tap, ci) order with a per-lane cursor: a divergent
-// loop whose round count is the busiest pixel's spike count.  Every spike adds
-// weight row (ci, tap) -- 64 output channels, read from LDS as 16 x 16-byte
-// pieces at immediate offsets -- to the lane's accumulators.  The finished
-// tile is stored one output channel per instruction (64 consecutive pixels =
-// one 256-byte run of the channel plane).
+// One wavefront owns 64 consecutive output pixels (a flat run of the
+// h_out*w_out plane) for a slice of 64 or 32 output channels: lane = output
+// pixel, one accumulator register per output channel.  For a run of input
+// channels each lane loads the bitmap words of its 9 input taps (0 outside
+// the frame) and walks its own spikes in (tap, ci) order with a per-lane
+// cursor: a divergent loop whose round count is the busiest pixel's spike
+// count.  Every spike adds weight row (ci, tap) -- the slice's output
+// channels, read from LDS as 16-byte pieces -- to the lane's accumulators.
+// The finished tile is stored one output channel per instruction (64
+// consecutive pixels = one 256-byte run of the channel plane).
 //
-// LDS: a chunk is 288 weight rows (32 ci x 9 taps) of 64 output channels,
-// each row padded to 272 bytes so that lanes reading different rows spread
-// over the banks (77 KB per chunk).  With at most two chunks (C_in <= 64) the
-// weights stay resident for the whole persistent launch and the wavefronts
-// never synchronise; beyond that chunk c+1 streams into the second buffer
-// (direct global->LDS loads) while chunk c is walked.
+// Variants (launch_px3_conv picks one):
+//  k_conv_px3w  C_in <= 128: every weight row of the slice resident in LDS
+//               (64 input channels x 64 output channels, rows padded to 272
+//               bytes, or 128 x 32 with 128-byte rows, pieces swizzled), the
+//               spikes walked 64 channels at a time (64-bit masks); also the
+//               fused conv-LIF for C_in <= 128.
+//  k_conv_px3s  C_in > 128: 32-channel chunks of 64 output channels streamed
+//               through two LDS buffers (chunk c+1 arrives while chunk c is
+//               walked), tiles of the flattened (frame, pixel) axis.
+//  k_conv_px3   the per-frame-tile form (32-channel chunks, resident or
+//               streamed): the fused conv-LIF for C_in > 128 and the
+//               fallback for tensors beyond one buffer resource.
+// The persistent forms size their workgroups so that every CU makes the same
+// number of passes.  The bitmap words are read through two strides, so the
+// same kernels take the [hw][cwp] words of sf_prescan_pack and the word
+// planes sf_conv2d_forward packs for them.
 //
 // Output element (co, oh, ow) = bias[co] + its active taps summed by one lane
-// in (chunk, tap, ci) order: deterministic from run to run.
+// in (channel, tap, ci) order: deterministic from run to run.
 // Replaces the reference's sparse_conv3x3s1_nhwc_kernel_8x8/8x16 and
 // sparse_conv3x3s2 kernels (Kernels/conv2d.py:564-886) for these shapes.
 #include <type_traits>
