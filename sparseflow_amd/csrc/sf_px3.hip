@@ -30,7 +30,7 @@
 // planes sf_conv2d_forward packs for them.
 //
 // Output element (co, oh, ow) = bias[co] + its active taps summed by one lane
-// in (channel, tap, ci) order: deterministic from run to run.
+// in (channel block, tap, ci) order: deterministic from run to run.
 // Replaces the reference's sparse_conv3x3s1_nhwc_kernel_8x8/8x16 and
 // sparse_conv3x3s2 kernels (Kernels/conv2d.py:564-886) for these shapes.
 #include <type_traits>
