@@ -141,3 +141,34 @@ def test_flat_and_gather_agree():
     y_gather, k2 = _run(x.to(DEV), w[:6].contiguous().to(DEV), None)
     assert "conv_flat" in k1 and "conv_gather" in k2
     assert torch.allclose(y_flat[:, :6], y_gather, atol=1e-5, rtol=1e-5)
+
+
+def _random_flat_cases(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(n):
+        N = int(torch.randint(1, 9, (1,), generator=g))
+        C = int(torch.randint(1, 1100, (1,), generator=g))
+        Co = 4 * int(torch.randint(1, 80, (1,), generator=g))
+        H = int(torch.randint(1, 30, (1,), generator=g))
+        W = int(torch.randint(1, 40, (1,), generator=g))
+        dens = [0.005, 0.05, 0.3][int(torch.randint(0, 3, (1,), generator=g))]
+        out.append((N, C, H, W, Co, dens))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_flat_cases(30, 5150))
+def test_flat_random_shapes(case):
+    # Random geometry through the 1x1 pixel-tile kernel: resident and
+    # streamed chunks, ragged words and channel groups, planes from one
+    # pixel, workgroups of one to sixteen wavefronts (sized so that every
+    # CU makes the same number of passes).
+    N, C, H, W, Co, dens = case
+    announce(f"flat random {case}")
+    x = spikes((N, C, H, W), dens, seed=C + H * W)
+    w = _weights(Co, C, seed=Co + N)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(C)) * 0.1
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV))
+    assert "conv_flat" in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 0), **FP32_TOL)
+    assert ok, f"max abs err {err}"

@@ -206,3 +206,38 @@ def test_fused_lif_pixel_kernel_value_path():
     (spk, v, _), kernels = _lif_kernels(lambda: sparse_fused_conv_lif_multistep(x.to(DEV), w.to(DEV), None))
     assert "conv_lif_px3" in kernels
     _check(spk, v, x, w, None, 3, 2.0, 1.0, 0.0, True)
+
+
+def _random_lif_cases(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(n):
+        T = int(torch.randint(1, 6, (1,), generator=g))
+        N = int(torch.randint(1, 4, (1,), generator=g))
+        C = int(torch.randint(1, 200, (1,), generator=g))
+        Co = 4 * int(torch.randint(1, 30, (1,), generator=g))
+        H = int(torch.randint(1, 20, (1,), generator=g))
+        W = int(torch.randint(1, 24, (1,), generator=g))
+        dens = [0.02, 0.1][int(torch.randint(0, 2, (1,), generator=g))]
+        v_reset = [0.0, None, -0.3][int(torch.randint(0, 3, (1,), generator=g))]
+        decay = bool(torch.randint(0, 2, (1,), generator=g))
+        out.append((T, N, C, H, W, Co, dens, v_reset, decay))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_lif_cases(24, 77))
+def test_fused_lif_pixel_kernel_random_shapes(case):
+    # Random geometry through the 3x3 fused conv-LIF (resident 64-channel
+    # super-chunks for C_in <= 128, streamed 32-channel chunks beyond; ragged
+    # channel groups; planes smaller than a tile; one wavefront per workgroup
+    # for the smallest launches) against the float64 closed form.
+    T, N, C, H, W, Co, dens, v_reset, decay_input = case
+    announce(f"lif px3 random {case}")
+    x = spikes((T, N, C, H, W), dens, seed=C * 3 + W)
+    g = torch.Generator().manual_seed(C + Co + H)
+    w = torch.randn(Co, C, 3, 3, generator=g) * (4.0 / (C * 9)) ** 0.5 * 3.0
+    b = torch.randn(Co, generator=g) * 0.2
+    (spk, v, _), kernels = _lif_kernels(lambda: sparse_fused_conv_lif_multistep(
+        x.to(DEV), w.to(DEV), b.to(DEV), tau=2.0, v_threshold=1.0, v_reset=v_reset, decay_input=decay_input))
+    assert "conv_lif_px3" in kernels, kernels
+    _check(spk, v, x, w, b, 3, 2.0, 1.0, v_reset, decay_input)
