@@ -158,3 +158,32 @@ def test_sparse_linear_module_shapes():
     x5 = spikes((2, 3, 4, 4, 24), 0.2, seed=17).to(DEV)
     sl5 = SparseLinear.from_dense(torch.nn.Linear(4 * 4 * 24, 8).to(DEV))
     assert sl5(x5).shape == (2, 3, 8)
+
+
+def _random_linear_cases(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(n):
+        m = int(torch.randint(1, 3000, (1,), generator=g))
+        k = int(torch.randint(1, 1600, (1,), generator=g))
+        co = 4 * int(torch.randint(1, 200, (1,), generator=g))
+        dens = [0.02, 0.1, 0.5][int(torch.randint(0, 3, (1,), generator=g))]
+        out.append((m, k, co, dens))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_linear_cases(20, 909))
+@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+def test_linear_random_shapes(case, kernel):
+    # Random (m, k, c_out): ragged row and column blocks, grids of every size
+    # (the matrix-core kernel's XCD-local placement is a bijection for any
+    # grid), walk workgroups of one to sixteen wavefronts.
+    m, k, co, dens = case
+    announce(f"linear random {kernel} {case}")
+    x = spikes((m, k), dens, seed=m + 3 * k)
+    w = _w(co, k, seed=co + m)
+    b = torch.randn(co, generator=torch.Generator().manual_seed(k)) * 0.1
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV), kernel=kernel)
+    assert ("linear_flat" if kernel == "walk" else "linear_mfma") in kernels, kernels
+    ok, err, _ = close(y, olin.linear_ref(x, w, b), **FP32_TOL)
+    assert ok, f"max abs err {err}"
