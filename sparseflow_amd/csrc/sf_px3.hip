@@ -88,12 +88,11 @@ __device__ __forceinline__ void load_chunk_px3(char* buf, const float* __restric
   }
 }
 
-// Add weight row r of the chunk, times xv, to the CO accumulators.
+// Add the weight row at rowp (piece swizzle key for CO = 32), times xv, to
+// the CO accumulators.
 template <int CO>
-__device__ __forceinline__ void px3_add_row(float (&acc)[CO], const char* chunk, int r, float xv) {
+__device__ __forceinline__ void px3_add_row_at(float (&acc)[CO], const char* rowp, int key, float xv) {
   typedef Px3Layout<CO> L;
-  const char* rowp = chunk + (r * L::stride) * 16;
-  const int key = CO == 64 ? 0 : ((r >> 1) & L::xmask) << 4;
 #pragma unroll
   for (int s = 0; s < L::pieces; ++s) {
     // Groups of four pieces: the scheduler may not hoist more than 16
@@ -106,6 +105,30 @@ __device__ __forceinline__ void px3_add_row(float (&acc)[CO], const char* chunk,
     acc[4 * s + 2] = fmaf(xv, v.z, acc[4 * s + 2]);
     acc[4 * s + 3] = fmaf(xv, v.w, acc[4 * s + 3]);
   }
+}
+
+// Add weight row r of the chunk, times xv, to the CO accumulators.
+template <int CO>
+__device__ __forceinline__ void px3_add_row(float (&acc)[CO], const char* chunk, int r, float xv) {
+  typedef Px3Layout<CO> L;
+  px3_add_row_at<CO>(acc, chunk + (r * L::stride) * 16, CO == 64 ? 0 : ((r >> 1) & L::xmask) << 4, xv);
+}
+
+// Rows (ci, tap) of a 64-channel chunk (272-byte rows, row ci * 9 + tap):
+// the tap's row start is formed once per refill of a lane's word, the
+// channel's offset per spike with one 24-bit multiply-add (a chunk spans
+// fewer than 2^24 bytes) instead of a full 32-bit multiply of the row index.
+constexpr uint32_t kPx3RowBytes = Px3Layout<64>::stride * 16;
+__device__ __forceinline__ const char* px3_tap_rows(const char* chunk, int tap) {
+  return chunk + __umul24((uint32_t)tap, kPx3RowBytes);
+}
+__device__ __forceinline__ const char* px3_spike_row(const char* tap_rows, int ci) {
+  return tap_rows + __umul24((uint32_t)ci, 9u * kPx3RowBytes);
+}
+// The tap back from its row start (the multiply-by-x path only: the walk keeps
+// one register per lane for the tap, its row start).
+__device__ __forceinline__ int px3_rows_tap(const char* chunk, const char* tap_rows) {
+  return (int)((uint32_t)(tap_rows - chunk) / kPx3RowBytes);
 }
 
 // Word of tap t among the lane's nine: a per-lane 9-way multiplexer on the
@@ -555,19 +578,21 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const
         for (int tp = 0; tp < 9; ++tp) nz |= (w[tp] != 0u ? 1u : 0u) << tp;
         const char* chunk = smem + (c & 1) * LY::chunk_bytes;
         uint32_t m = 0u;
-        int tap = 0;
+        const char* trows = chunk;
         // Per-lane cursor over (tap, ci): the wavefront loops while any
         // lane has spikes left.
         while ((m | nz) != 0u) {
           if (m == 0u) {
-            tap = __builtin_ctz(nz);
+            const int tap = __builtin_ctz(nz);
             nz &= nz - 1u;
             m = px3_select(w, tap);
+            trows = px3_tap_rows(chunk, tap);
           }
           const int bit = __builtin_ctz(m);
           m &= m - 1u;
           float xv = 1.f;
           if (value) {
+            const int tap = px3_rows_tap(chunk, trows);
             const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
             const TIn* __restrict__ xf = x + (int64_t)sample * a.c_in * a.hw_in;
             xv = to_f32<TIn>(xf[(int64_t)(c * kPx3Ch + bit) * a.hw_in + ih * a.w_in + iw]);
@@ -575,7 +600,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const
             // products wait for the next chunk's rows and words too.
             __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
           }
-          px3_add_row<64>(acc, chunk, bit * 9 + tap, xv);
+          px3_add_row_at<64>(acc, px3_spike_row(trows, bit), 0, xv);
         }
       }
       __builtin_amdgcn_s_waitcnt(0);
@@ -799,18 +824,35 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
           // Per-lane cursor over (tap, ci): the wavefront loops while any
           // lane has spikes left.
           uint64_t m = 0ull;
-          int tap = 0;
+          int tap = 0;               // CO = 32
+          const char* trows = smem;  // CO = 64: the tap's rows (row0 = 0)
           while ((m != 0ull) || (nz != 0u)) {
             if (m == 0ull) {
-              tap = __builtin_ctz(nz);
+              const int t = __builtin_ctz(nz);
               nz &= nz - 1u;
-              m = ((uint64_t)px3_select(wh, tap) << 32) | px3_select(wl, tap);
+              m = ((uint64_t)px3_select(wh, t) << 32) | px3_select(wl, t);
+              if constexpr (CO == 64) trows = px3_tap_rows(smem, t);
+              else tap = t;
             }
             const int bit = __builtin_ctzll(m);
             m &= m - 1ull;
             float xv = 1.f;
             if (value) {
-              const int ih = ih0 + tap / 3, iw = iw0 + tap % 3;
+              int ih = ih0, iw = iw0;
+              if constexpr (CO == 64) {
+                // The tap and the lane's window origin formed here (the
+                // lane index anew, in asm): kept live across the walk they
+                // take registers the walk needs.
+                tap = px3_rows_tap(smem, trows);
+                int ln;
+                asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+                const int qv = p0 + min(ln, npx - 1);
+                const int ohv = qv / a.w_out;
+                ih = ohv * a.s - 1;
+                iw = (qv - ohv * a.w_out) * a.s - 1;
+              }
+              ih += tap / 3;
+              iw += tap % 3;
               xv = to_f32<TIn>(xf[(int64_t)(64 * sc + bit) * a.hw_in + ih * a.w_in + iw]);
               // Waited for here, in the value path: otherwise the products
               // below wait for every memory operation in flight (the
@@ -818,7 +860,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
               // bitmap path too.
               __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
             }
-            px3_add_row<CO>(acc, smem, row0 + bit * 9 + tap, xv);
+            if constexpr (CO == 64) px3_add_row_at<64>(acc, px3_spike_row(trows, bit), 0, xv);
+            else px3_add_row<CO>(acc, smem, row0 + bit * 9 + tap, xv);
           }
         }
       }
