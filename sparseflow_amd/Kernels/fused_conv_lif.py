@@ -32,6 +32,42 @@ __all__ = [
 
 FALLBACK_RATIO = SPARSE_DENSE_RATIO_THRESHOLD
 
+# The fused 1x1 conv + LIF kernel keeps the weights of up to two 128-channel
+# input chunks resident in LDS.  Beyond that it streams every chunk again at
+# every time step through two 64 KB buffers (one 8-wavefront workgroup per
+# CU), and its parallelism is one wavefront per (sample, 64-pixel tile, 64
+# output channels) carrying all T steps.
+CONV1X1_LIF_RESIDENT_CIN = 256
+CONV1X1_LIF_STREAMED_WAVES_PER_CU = 8
+# With streamed weights the fused kernel is kept when its wavefronts fill at
+# least this share of the GPU's workgroup slots; below it the conv over all
+# T*N frames followed by the neuron pass is faster, although it writes and
+# reads the currents (Spiking-ResNet50, T=16, batch 32, 1% spikes: 1024->256
+# at 14x14 fills 25%: 687 us fused, 335 us as the pair; 512->128 at 28x28
+# fills 41%: 380 / 314 us; 1024->512 at 14x14 fills 50%: 646 / 548 us;
+# 512->256 at 28x28 fills 81%: 402 / 491 us).
+CONV1X1_LIF_MIN_FILL = 0.75
+
+_num_cus: dict = {}
+
+
+def _cus(device: torch.device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _num_cus:
+        _num_cus[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return _num_cus[idx]
+
+
+def conv1x1_lif_prefers_fused(c_in: int, c_out: int, n: int, h: int, w: int, num_cus: int) -> bool:
+    """Whether the fused 1x1 conv + LIF kernel is the faster form for n
+    samples of C_in x h x w (the alternative: the sparse conv over all frames,
+    then the neuron layer): always with resident weights, with streamed ones
+    when its wavefronts fill at least CONV1X1_LIF_MIN_FILL of the GPU."""
+    if c_in <= CONV1X1_LIF_RESIDENT_CIN:
+        return True
+    waves = n * -(-(h * w) // 64) * -(-c_out // 64)
+    return waves >= CONV1X1_LIF_MIN_FILL * CONV1X1_LIF_STREAMED_WAVES_PER_CU * num_cus
+
 
 def lif_params(tau, v_threshold, v_reset, decay_input) -> _lib.LifParams:
     hard = v_reset is not None

@@ -196,9 +196,10 @@ class SparseConv1x1LIF(nn.Module):
     """A 1x1 stride-1 SparseConv2d followed by its multi-step LIFNode (and an
     optional residual added before the neuron), run as one fused kernel on
     device tensors (Kernels.fused_conv_lif.sparse_conv1x1_lif_multistep).
-    Holds the two original modules: host tensors, and shapes the kernel does
-    not take, run them one after the other.  The membrane is the LIFNode's
-    `v` (so reset_net clears it)."""
+    Holds the two original modules: host tensors, shapes the kernel does
+    not take, and inputs for which the pair is faster (see runs_fused) run
+    them one after the other.  The membrane is the LIFNode's `v` (so
+    reset_net clears it)."""
 
     def __init__(self, conv: nn.Module, lif: nn.Module):
         super().__init__()
@@ -216,11 +217,22 @@ class SparseConv1x1LIF(nn.Module):
 
     def runs_fused(self, x: torch.Tensor) -> bool:
         """The fused kernel runs for [T, N, C, H, W] device tensors of a
-        supported dtype, unless a dispatch decision put the conv on the
-        dense path (then conv and neuron run one after the other, so the
-        decision is honoured)."""
-        return (x.dim() == 5 and x.is_cuda and x.dtype in (torch.float32, torch.float16, torch.bfloat16)
-                and getattr(self.conv, "backend_mode", "sparse") != "dense")
+        supported dtype where it is the faster form
+        (Kernels.fused_conv_lif.conv1x1_lif_prefers_fused: resident weights,
+        or streamed ones with enough samples to fill the GPU), unless a
+        dispatch decision put the conv on the dense path.  Otherwise conv and
+        neuron run one after the other.  (The two forms agree up to rounding:
+        the fused kernel adds the weights into the decayed membrane, the pair
+        adds the finished current, so spikes can differ at threshold ties.)"""
+        from ..Kernels.fused_conv_lif import CONV1X1_LIF_RESIDENT_CIN, _cus, conv1x1_lif_prefers_fused
+
+        if not (x.dim() == 5 and x.is_cuda and x.dtype in (torch.float32, torch.float16, torch.bfloat16)
+                and getattr(self.conv, "backend_mode", "sparse") != "dense"):
+            return False
+        _, n, c, h, w = (int(v) for v in x.shape)
+        if c <= CONV1X1_LIF_RESIDENT_CIN:  # resident weights: no device query needed
+            return True
+        return conv1x1_lif_prefers_fused(c, self.conv.out_channels, n, h, w, _cus(x.device))
 
     def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         from ..Kernels.fused_conv_lif import sparse_conv1x1_lif_multistep

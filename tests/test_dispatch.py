@@ -156,3 +156,20 @@ def test_runtime_policy_force_zero_output_on_cpu():
     y = m(x)
     assert y.shape == (2, 3, 6, 5, 5) and m.fallback_reason == "force_zero"
     assert torch.equal(y, m.bias.detach().view(1, 1, -1, 1, 1).expand_as(y))
+
+
+def test_conv1x1_lif_fused_or_pair_rule():
+    # Host rule of the fused 1x1 conv + LIF module (no GPU needed): resident
+    # weights always fuse; streamed ones fuse only when the fused launch's
+    # wavefronts fill at least 3/4 of the GPU (Spiking-ResNet50 shapes at
+    # batch 32 on 256 CUs: only layer3.0's conv1 qualifies).
+    from sparseflow_amd.Kernels.fused_conv_lif import conv1x1_lif_prefers_fused
+
+    cus = 256
+    assert conv1x1_lif_prefers_fused(64, 64, 1, 8, 8, cus)        # resident, tiny
+    assert conv1x1_lif_prefers_fused(256, 1024, 32, 14, 14, cus)  # resident (two chunks)
+    assert not conv1x1_lif_prefers_fused(1024, 256, 32, 14, 14, cus)  # 512 wavefronts
+    assert not conv1x1_lif_prefers_fused(512, 128, 32, 28, 28, cus)   # 832
+    assert not conv1x1_lif_prefers_fused(1024, 512, 32, 14, 14, cus)  # 1024
+    assert conv1x1_lif_prefers_fused(512, 256, 32, 28, 28, cus)       # 1664 >= 1536
+    assert conv1x1_lif_prefers_fused(1024, 256, 128, 14, 14, cus)     # 2048 at batch 128

@@ -140,7 +140,17 @@ def test_resnet50_fused_matches_unfused():
         _lib.timing_enable(False)
         for h in hooks:
             h.remove()
-    assert stats["conv_lif_flat"][0] == n_fused
+    # One fused launch per pair whose weights the kernel keeps resident; the
+    # pairs with more input channels run as conv + neuron (at batch 2 none of
+    # them has the samples to fill the GPU).
+    from sparseflow_amd.Kernels.fused_conv_lif import CONV1X1_LIF_RESIDENT_CIN
+    from sparseflow_amd.Ops.sparse_fused_conv_lif import SparseConv1x1LIF
+
+    pairs = [mod for mod in fused.modules() if isinstance(mod, SparseConv1x1LIF)]
+    assert len(pairs) == n_fused
+    n_resident = sum(1 for mod in pairs if mod.conv.in_channels <= CONV1X1_LIF_RESIDENT_CIN)
+    assert 0 < n_resident < n_fused
+    assert stats["conv_lif_flat"][0] == n_resident
     assert torch.allclose(out, ref, atol=1e-2, rtol=1e-2), (out - ref).abs().max()
     assert any(float(s.float().mean()) > 0.01 for s in rec.values())
 
@@ -264,3 +274,31 @@ def test_conv1x1_lif_module_honours_dense_dispatch():
     assert stats.get("conv_lif_flat", (0,))[0] == 0
     s_u = lif_ref(conv(x.flatten(0, 1)).reshape(T, N, Co, H, W))
     assert torch.equal(s_f, s_u)
+
+
+def test_conv1x1_lif_module_streamed_weights_run_as_pair():
+    # C_in above the fused kernel's resident limit: the module runs the conv
+    # over all frames and then the neuron (no fused launch), and its spikes
+    # and membrane match the closed form.
+    from sparseflow_amd.Kernels.fused_conv_lif import CONV1X1_LIF_RESIDENT_CIN
+
+    T, N, C, Co, H, W = 3, 2, 512, 128, 7, 9
+    assert C > CONV1X1_LIF_RESIDENT_CIN
+    announce("conv1x1 lif module with streamed weights (C_in 512)")
+    fused, conv, lif_ref = _fused_pair(C, Co, 0.0, seed=61)
+    with torch.no_grad():
+        conv.weight.mul_(4.0 / C ** 0.5)
+    x = spikes((T, N, C, H, W), 0.05, seed=62).to(DEV)
+    spike_map.clear()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    s_f = fused(x)
+    torch.cuda.synchronize()
+    stats = _lib.timing_collect()
+    _lib.timing_enable(False)
+    assert stats.get("conv_lif_flat", (0,))[0] == 0
+    s_ref, v_ref, h_ref = _ref(x.cpu(), conv.weight.detach().cpu(), conv.bias.detach().cpu(), None,
+                               2.0, 1.0, 0.0, True)
+    _check(s_f, fused.lif.v, s_ref, v_ref, h_ref, 1.0)
+    assert 0.0 < float(s_f.mean()) < 1.0
+

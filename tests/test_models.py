@@ -86,7 +86,9 @@ def test_fused_pairs_follow_dispatch_swaps_and_dense_decisions():
         reset_net(m)
         m(x)
         assert calls == []          # stale pair not used
-    cuda_like = SimpleNamespace(dim=lambda: 5, is_cuda=True, dtype=torch.float32)
+    cuda_like = SimpleNamespace(dim=lambda: 5, is_cuda=True, dtype=torch.float32,
+                                shape=(2, 1, pair.conv.in_channels, 16, 16))
+    assert pair.conv.in_channels <= 256  # resident weights: fused whatever the batch
     assert pair.runs_fused(cuda_like)
     pair.conv.backend_mode = "dense"
     assert not pair.runs_fused(cuda_like)
