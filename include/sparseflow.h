@@ -249,6 +249,20 @@ int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T,
                      const float* v_init, void* spikes, int32_t out_dtype,
                      float* v_out, uint32_t* bits, uint32_t* flags, void* stream);
 
+/* Max pooling (kernel k, stride, padding <= k/2, floor mode) of n frames of a
+ * binary spike tensor [c, h_in, w_in] given only by its spike map `bits`
+ * (the pixel-major words sf_prescan_pack and sf_lif_multistep write): the max
+ * of 0 / 1 values over a window is the OR of the window's words.  Writes the
+ * pooled spikes y [n, c, h_out, w_out] (0 / 1 in out_dtype) and their spike
+ * map out_bits in the same layout (its flags are all zero: the caller hands
+ * zeroed flags of sf_prescan_flags_bytes(n, c, h_out, w_out) bytes with it).
+ * c <= 256.  Replaces, for spike inputs, the nn.MaxPool2d after the stem
+ * neuron of the reference's spiking ResNets (F.max_pool2d on the dense
+ * spikes); the spike-map form has no counterpart in the reference. */
+int sf_spike_maxpool2d(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in,
+                       int32_t w_in, int32_t k, int32_t stride, int32_t padding,
+                       void* y, int32_t out_dtype, uint32_t* out_bits, void* stream);
+
 /* ---- sparse linear ------------------------------------------------------------ */
 
 /* y[m, c_out] = x[m, k] @ wt[k, c_out] + bias for a spike-sparse row-major x

@@ -124,6 +124,8 @@ class _SpikeLeafTracer(torch.fx.Tracer):
     def is_leaf_module(self, m: nn.Module, qualname: str) -> bool:
         if self._registry.is_spike_op(m) or is_attention_like_module(m):
             return True
+        if isinstance(m, nn.MaxPool2d):  # incl. Ops.spike_pool.SpikeMaxPool2d (data-dependent forward)
+            return True
         return super().is_leaf_module(m, qualname)
 
 

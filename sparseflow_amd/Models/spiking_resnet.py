@@ -26,6 +26,8 @@ from typing import List, Optional
 import torch
 import torch.nn as nn
 
+from ..Ops.spike_pool import SpikeMaxPool2d
+
 from ..neuron import LIFNode
 
 
@@ -88,7 +90,8 @@ class SpikingResNet(nn.Module):
         self.conv1 = nn.Conv2d(3, width, 7, 2, 3, bias=False)
         self.bn1 = nn.BatchNorm2d(width)
         self.sn1 = _lif(**self.neuron)
-        self.maxpool = nn.MaxPool2d(3, 2, 1)
+        # nn.MaxPool2d that pools handed spike maps on the GPU (Ops.spike_pool).
+        self.maxpool = SpikeMaxPool2d(3, 2, 1)
         self.layer1 = self._make_layer(width, layers[0], 1)
         self.layer2 = self._make_layer(width * 2, layers[1], 2)
         self.layer3 = self._make_layer(width * 4, layers[2], 2)

@@ -55,6 +55,8 @@ EXPORTS = {
     "sf_conv1x1_lif_sparse_binres": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_lif_multistep": (c_int, [_P, _P, c_int32, c_int32, c_int64, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P, _P,
                                  _P]),
+    "sf_spike_maxpool2d": (c_int, [_P, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, _P, c_int32,
+                                   _P, _P]),
     "sf_linear_bitmap_bytes": (c_size_t, [c_int64, c_int32]),
     "sf_linear_flags_bytes": (c_size_t, [c_int64]),
     "sf_linear_workspace_size": (c_size_t, [c_int64, c_int32]),
@@ -355,6 +357,24 @@ def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torc
                                 _ptr(flags), _stream(x.device))
     _check(rc, "sf_lif_multistep")
     return spikes, v_out, (None if bits is None else (bits, flags))
+
+
+def spike_maxpool2d(bits: torch.Tensor, n: int, c: int, h: int, w: int, k: int, stride: int, padding: int,
+                    dtype: torch.dtype, device: torch.device):
+    """Max pooling of n frames of binary spikes [c, h, w] given by their spike
+    map `bits` (sf_spike_maxpool2d): (y [n, c, h_out, w_out] in dtype, (out
+    bits, zeroed flags)) -- the pooled spikes and their own spike map."""
+    h_out = (h + 2 * padding - k) // stride + 1
+    w_out = (w + 2 * padding - k) // stride + 1
+    y = torch.empty((n, c, h_out, w_out), dtype=dtype, device=device)
+    out_bits = torch.empty(n * h_out * w_out * int(lib().sf_bitmap_words_per_pixel(c)), dtype=torch.int32,
+                           device=device)
+    flags = torch.zeros((int(lib().sf_prescan_flags_bytes(n, c, h_out, w_out)) + 3) // 4, dtype=torch.int32,
+                        device=device)
+    rc = lib().sf_spike_maxpool2d(_ptr(bits), int(n), int(c), int(h), int(w), int(k), int(stride), int(padding),
+                                  _ptr(y), dtype_code(dtype), _ptr(out_bits), _stream(device))
+    _check(rc, "sf_spike_maxpool2d")
+    return y, (out_bits, flags)
 
 
 def conv1x1_lif_sparse(desc: ConvDesc, T: int, bits: torch.Tensor, flags: torch.Tensor, x: torch.Tensor,

@@ -811,6 +811,26 @@ int sf_conv1x1_lif_sparse_binres(const sf_conv_desc* d, int32_t T, const uint32_
                           out_flags, stream);
 }
 
+int sf_spike_maxpool2d(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in, int32_t w_in, int32_t k,
+                       int32_t stride, int32_t padding, void* y, int32_t out_dtype, uint32_t* out_bits,
+                       void* stream) {
+  if (!dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (n < 0 || c < 0 || h_in < 0 || w_in < 0) return fail(SF_ERR_INVALID, "negative size");
+  if (k < 1 || stride < 1 || padding < 0 || 2 * padding > k)
+    return fail(SF_ERR_INVALID, "kernel >= 1, stride >= 1, 0 <= padding <= kernel / 2");
+  if (c > 32 * sf::kSpikePoolMaxWords) return fail(SF_ERR_UNSUPPORTED, "spike max pooling: c <= 256");
+  if ((int64_t)h_in * w_in > INT32_MAX) return fail(SF_ERR_UNSUPPORTED, "h_in * w_in < 2^31");
+  const int h_out = h_in + 2 * padding < k ? 0 : (h_in + 2 * padding - k) / stride + 1;
+  const int w_out = w_in + 2 * padding < k ? 0 : (w_in + 2 * padding - k) / stride + 1;
+  if (n == 0 || c == 0 || h_out == 0 || w_out == 0) return SF_OK;
+  if (bits == nullptr || y == nullptr || out_bits == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
+  const int cwp = sf::words_per_pixel(c);
+  if (cwp > sf::kSpikePoolMaxWords) return fail(SF_ERR_UNSUPPORTED, "spike max pooling: c <= 256");
+  const int rc = sf::launch_spike_maxpool(bits, n, c, h_in, w_in, h_out, w_out, k, stride, padding, cwp, out_dtype,
+                                          y, out_bits, static_cast<hipStream_t>(stream));
+  return rc == (int)hipSuccess ? SF_OK : fail(SF_ERR_HIP, hipGetErrorString((hipError_t)rc));
+}
+
 int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T, int64_t n, int32_t c, int64_t hw,
                      const sf_lif_params* lif, const float* v_init, void* spikes, int32_t out_dtype, float* v_out,
                      uint32_t* bits, uint32_t* flags, void* stream) {

@@ -141,6 +141,11 @@ int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const v
 // second input summed into the current; bits: optional spike map output in
 // the prescan layout with cwp words per pixel, with its nflags chunk flags
 // cleared).
+// Spike max pooling from a spike map (at most kSpikePoolMaxWords words, 256
+// channels, per pixel).
+constexpr int kSpikePoolMaxWords = 8;
+int launch_spike_maxpool(const uint32_t* bits, int64_t n, int c, int h_in, int w_in, int h_out, int w_out, int k,
+                         int st, int pd, int cwp, int out_dtype, void* y, uint32_t* out_bits, hipStream_t stream);
 int launch_lif_multistep(const void* x, const void* x2, int in_dtype, int T, int64_t n, int c, int64_t hw, float tau,
                          float v_th, float v_reset, int hard_reset, int decay_input, const float* v_init, void* spikes,
                          int out_dtype, float* v_out, uint32_t* bits, int cwp, uint32_t* flags, int64_t nflags,

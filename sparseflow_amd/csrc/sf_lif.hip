@@ -387,4 +387,75 @@ int launch_lif_multistep(const void* x, const void* x2, int in_dtype, int T, int
   return rc;
 }
 
+// ---------------------------------------------------------------------------
+// Max pooling of a binary spike tensor given by its spike map (the pixel-major
+// words a neuron layer hands over): the max of 0/1 values over a window is
+// the OR of the window's words, so the pooled spikes and their own map come
+// from the words alone (cwp words per input pixel read, no float input).
+// One thread per output pixel: the OR of its window's in-frame words is
+// written as the output map's words and, one channel plane per store
+// (consecutive threads = consecutive pixels of the plane), as 0 / 1 values.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <typename TOut>
+__global__ __launch_bounds__(256) void k_spike_maxpool(const uint32_t* __restrict__ bits, int64_t n, int c,
+                                                       int h_in, int w_in, int h_out, int w_out, int k, int st,
+                                                       int pd, int cwp, TOut* __restrict__ y,
+                                                       uint32_t* __restrict__ out_bits) {
+  const int64_t hwo = (int64_t)h_out * w_out;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * hwo) return;
+  const int64_t frame = i / hwo;
+  const int q = (int)(i - frame * hwo);
+  const int oh = q / w_out, ow = q - (q / w_out) * w_out;
+  uint32_t w[kSpikePoolMaxWords];
+#pragma unroll
+  for (int j = 0; j < kSpikePoolMaxWords; ++j) w[j] = 0u;
+  const uint32_t* __restrict__ fb = bits + frame * h_in * w_in * cwp;
+  for (int kh = 0; kh < k; ++kh) {
+    const int ih = oh * st - pd + kh;
+    if (ih < 0 || ih >= h_in) continue;
+    for (int kw = 0; kw < k; ++kw) {
+      const int iw = ow * st - pd + kw;
+      if (iw < 0 || iw >= w_in) continue;
+      const uint32_t* __restrict__ src = fb + ((int64_t)ih * w_in + iw) * cwp;
+#pragma unroll
+      for (int j = 0; j < kSpikePoolMaxWords; ++j)
+        if (j < cwp) w[j] |= src[j];
+    }
+  }
+  uint32_t* __restrict__ ob = out_bits + i * cwp;
+#pragma unroll
+  for (int j = 0; j < kSpikePoolMaxWords; ++j)
+    if (j < cwp) ob[j] = w[j];
+  TOut* __restrict__ yp = y + frame * c * hwo + q;
+#pragma unroll
+  for (int j = 0; j < kSpikePoolMaxWords; ++j) {
+    if (j < cwp) {
+      const uint32_t wv = w[j];
+      for (int b = 0; b < 32 && 32 * j + b < c; ++b)
+        yp[(int64_t)(32 * j + b) * hwo] = from_f32<TOut>((float)((wv >> b) & 1u));
+    }
+  }
+}
+
+}  // namespace
+
+int launch_spike_maxpool(const uint32_t* bits, int64_t n, int c, int h_in, int w_in, int h_out, int w_out, int k,
+                         int st, int pd, int cwp, int out_dtype, void* y, uint32_t* out_bits, hipStream_t stream) {
+  const int64_t total = n * (int64_t)h_out * w_out;
+  const int64_t blocks = (total + 255) / 256;
+  if (out_dtype == SF_F16)
+    hipLaunchKernelGGL(k_spike_maxpool<__half>, dim3((unsigned)blocks), dim3(256), 0, stream, bits, n, c, h_in, w_in,
+                       h_out, w_out, k, st, pd, cwp, static_cast<__half*>(y), out_bits);
+  else if (out_dtype == SF_BF16)
+    hipLaunchKernelGGL(k_spike_maxpool<__hip_bfloat16>, dim3((unsigned)blocks), dim3(256), 0, stream, bits, n, c,
+                       h_in, w_in, h_out, w_out, k, st, pd, cwp, static_cast<__hip_bfloat16*>(y), out_bits);
+  else
+    hipLaunchKernelGGL(k_spike_maxpool<float>, dim3((unsigned)blocks), dim3(256), 0, stream, bits, n, c, h_in, w_in,
+                       h_out, w_out, k, st, pd, cwp, static_cast<float*>(y), out_bits);
+  return (int)hipGetLastError();
+}
+
 }  // namespace sf
