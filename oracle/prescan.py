@@ -141,13 +141,6 @@ def bitmap(x: np.ndarray, threshold: float) -> np.ndarray:
     return np.ascontiguousarray(np.moveaxis(words.astype(np.uint32), 1, -1))  # [N, HW, cwp]
 
 
-def nonbinary_pixels(x: np.ndarray) -> np.ndarray:
-    """bool [N, H*W]: any channel value outside {0, 1} (NaN included)."""
-    N, C, H, W = x.shape
-    xv = x.astype(np.float32).reshape(N, C, H * W)
-    return ((xv != 0) & (xv != 1)).any(axis=1)
-
-
 def tile_channel_lists(x: np.ndarray, k: int, s: int, p: int, th: int, tw: int, threshold: float):
     """Per output tile at th x tw, group size 1: (mask uint32 [T, cwp],
     count int32 [T], lists: list of ascending int arrays)."""
@@ -163,7 +156,3 @@ def tile_channel_lists(x: np.ndarray, k: int, s: int, p: int, th: int, tw: int, 
     lists = [np.nonzero(row)[0].astype(np.int32) for row in act]
     return mask, count, lists
 
-
-def popcount32(v: np.ndarray) -> np.ndarray:
-    u = v.astype(np.int64) & 0xFFFFFFFF
-    return np.array([bin(int(t)).count("1") for t in u.reshape(-1)], dtype=np.int32).reshape(v.shape)

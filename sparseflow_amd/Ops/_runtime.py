@@ -1,4 +1,4 @@
-"""Per-module runtime state shared by SparseConv2d and SparseLinear.
+"""Per-module runtime state shared by the operator modules.
 
 Three small pieces, one per concern:
 
@@ -19,6 +19,16 @@ Three small pieces, one per concern:
   bf16 split) rebuilt only when the parameter changes, keyed on its version
   counter, storage and device (the reference keys its fp16 copy on
   `weight._version`, Ops/sparse_conv2d.py:339-350).
+
+Two more are shared by every replaced operator module:
+
+* `OpReporting` - the observability attributes a replaced module exposes
+  (their names and defaults are the drop-in contract the reference's
+  harness and replacer read) and `set_inference_mode`, set up in one call.
+* `ExactZeroOp` + `bias_rows` - the exact-zero backends: an operator whose
+  input is all zero returns its bias broadcast over the output (zeros
+  without a bias); SparseConv2d's zero path, StaticZeroConv2d and
+  StaticZeroLinear all build that tensor with `bias_rows`.
 """
 
 from __future__ import annotations
@@ -185,3 +195,69 @@ def bias_rows(bias: Optional[torch.Tensor], lead, channels: int, trailing, dtype
         return torch.zeros(shape, dtype=dtype, device=device)
     b = bias.detach().to(device=device, dtype=dtype).reshape(channels, *([1] * len(trailing)))
     return b.expand(shape).clone()
+
+
+class OpReporting:
+    """Mixin for nn.Module operators: the reporting state a replaced module
+    carries.  Attribute names and their defaults follow the reference
+    modules' observability contract (Ops/sparse_conv2d.py:191-250,
+    Ops/sparse_attention.py, Ops/sparse_bmm.py, Ops/sparse_fused_conv_lif.py);
+    the values are this build's.  `_init_reporting` is called once from the
+    module's constructor, after any `profile_runtime` property's backing
+    state exists."""
+
+    def _init_reporting(self, backend_family: str, diag_path: str, score_family: Optional[str] = None,
+                        profile_runtime: Optional[bool] = None) -> None:
+        self._last_sparse_ms = 0.0
+        self._last_diag = {}
+        self.collect_diag = False
+        self._inference_mode = False
+        self.backend_family = backend_family
+        self.diag_path = diag_path
+        self.fallback_reason = ""
+        self.meta_source = self.diag_source = "measured"
+        self.support_status = "supported"
+        if score_family is not None:
+            self.score_family = score_family
+        if profile_runtime is not None:
+            self.profile_runtime = bool(profile_runtime)
+
+    def set_inference_mode(self, enabled: bool) -> None:
+        """Inference mode turns diagnostics and host-timed profiling off, so
+        a forward never waits on the device."""
+        self._inference_mode = bool(enabled)
+        if enabled:
+            self.collect_diag = False
+            self.profile_runtime = False
+
+
+class ExactZeroOp:
+    """Mixin for the exact-zero backends (StaticZeroConv2d,
+    StaticZeroLinear): the bias kept as an fp32 buffer, a call counter and
+    the diagnostics record.  Such a module never reads its input's values,
+    only its shape."""
+
+    backend_family = "exact_zero"
+
+    def _init_exact_zero(self, bias: Optional[torch.Tensor], zero_reason: str, diag_path: str) -> None:
+        self.register_buffer("bias_buf", None if bias is None else bias.detach().float().clone())
+        self.zero_reason = zero_reason
+        self.diag_path = diag_path
+        self.fallback_reason = "exact_zero_shortcut"
+        self.calls = 0
+        self.collect_diag = False
+        self.profile_runtime = False
+        self._last_diag = {}
+        self._last_sparse_ms = 0.0
+
+    def _zero_output(self, lead, channels: int, trailing, like: torch.Tensor) -> torch.Tensor:
+        self.calls += 1
+        y = bias_rows(self.bias_buf, lead, channels, trailing, like.dtype, like.device)
+        if self.collect_diag:
+            self._last_diag = self.get_diag()
+        return y
+
+    def _zero_diag(self, **shape_keys) -> dict:
+        return dict(backend_family=self.backend_family, zero_reason=self.zero_reason, diag_path=self.diag_path,
+                    fallback_reason=self.fallback_reason, has_bias=self.bias_buf is not None,
+                    forward_count=self.calls, sparse_path_executed=False, sparse_total_ms=0.0, **shape_keys)

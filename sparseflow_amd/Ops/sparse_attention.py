@@ -6,15 +6,15 @@ in place); host tensors run torch.matmul in f32 as the reference does."""
 from __future__ import annotations
 
 import math
-from typing import Any, Dict
 
 import torch
 import torch.nn as nn
 
 from ..Kernels.attention import sparse_attn_v_forward, sparse_qk_forward, sparse_spike_attention_forward
+from ._runtime import OpReporting
 
 
-class SparseAttention(nn.Module):
+class SparseAttention(OpReporting, nn.Module):
     def __init__(self, num_heads: int = 8, head_dim: int = 64, threshold: float = 1e-6, return_ms: bool = False):
         super().__init__()
         self.num_heads = int(num_heads)
@@ -22,24 +22,7 @@ class SparseAttention(nn.Module):
         self.scale = 1.0 / math.sqrt(head_dim)
         self.threshold = float(threshold)
         self.return_ms = bool(return_ms)
-        self._last_sparse_ms = 0.0
-        self._last_diag: Dict[str, Any] = {}
-        self.collect_diag = False
-        self.profile_runtime = False
-        self._inference_mode = False
-        self.backend_family = "sparse_kernel"
-        self.diag_path = "attention"
-        self.fallback_reason = ""
-        self.meta_source = "measured"
-        self.diag_source = "measured"
-        self.support_status = "supported"
-        self.score_family = "attn_matmul"
-
-    def set_inference_mode(self, enabled: bool):
-        self._inference_mode = bool(enabled)
-        if enabled:
-            self.collect_diag = False
-            self.profile_runtime = False
+        self._init_reporting("sparse_kernel", "attention", "attn_matmul", profile_runtime=False)
 
     def qk(self, q: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
         """[B, heads, seq, head_dim] x2 -> attention logits [B, heads, seq, seq] (scaled)."""

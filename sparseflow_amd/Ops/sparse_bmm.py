@@ -12,6 +12,7 @@ import torch.nn as nn
 
 from ..Kernels.bmm import sparse_bmm_forward
 from ..Kernels.matmul import sparse_matmul_forward
+from ._runtime import OpReporting
 
 
 def _tile_diag(ts) -> Dict[str, Any]:
@@ -26,29 +27,14 @@ def _tile_diag(ts) -> Dict[str, Any]:
     return out
 
 
-class _SparseMM(nn.Module):
+class _SparseMM(OpReporting, nn.Module):
     def __init__(self, threshold: float = 1e-6, fallback_ratio: float = 0.85, return_ms: bool = False,
                  profile_runtime: bool = False):
         super().__init__()
         self.threshold = float(threshold)
         self.fallback_ratio = float(fallback_ratio)
         self.return_ms = bool(return_ms)
-        self.profile_runtime = bool(profile_runtime)
-        self._last_sparse_ms = 0.0
-        self._last_diag: Dict[str, Any] = {}
-        self.collect_diag = False
-        self._inference_mode = False
-        self.backend_family = "sparse_kernel"
-        self.fallback_reason = ""
-        self.meta_source = "measured"
-        self.diag_source = "measured"
-        self.support_status = "supported"
-
-    def set_inference_mode(self, enabled: bool):
-        self._inference_mode = bool(enabled)
-        if enabled:
-            self.collect_diag = False
-            self.profile_runtime = False
+        self._init_reporting("sparse_kernel", self.diag_path, self.score_family, profile_runtime=profile_runtime)
 
     def _bmm(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         self._last_diag = {}
@@ -76,10 +62,7 @@ class _SparseMM(nn.Module):
 class SparseBMM(_SparseMM):
     """C[b] = A[b] @ B[b] with A [B, M, K] spike-sparse."""
 
-    def __init__(self, *args, **kwargs):
-        super().__init__(*args, **kwargs)
-        self.diag_path = "bmm"
-        self.score_family = "bmm"
+    diag_path = score_family = "bmm"
 
     def forward(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         if a.ndim != 3 or b.ndim != 3:
@@ -91,10 +74,7 @@ class SparseMatmul(_SparseMM):
     """C = A @ B with A [M, K] or [*, M, K] spike-sparse; B [K, N] or
     [*, K, N] (batched B takes the batched-matmul path)."""
 
-    def __init__(self, *args, **kwargs):
-        super().__init__(*args, **kwargs)
-        self.diag_path = "matmul"
-        self.score_family = "matmul"
+    diag_path = score_family = "matmul"
 
     def forward(self, a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
         if a.ndim > 2:

@@ -17,7 +17,6 @@ from __future__ import annotations
 
 import ctypes
 import math
-from typing import Optional
 
 import torch
 import torch.nn as nn
@@ -28,7 +27,7 @@ from ..Kernels import spike_map
 from ..Kernels.conv2d import BACKEND_NAME, _select_tile_sizes, choose_group_size, sparse_conv2d_forward
 from ..Utils import config as _config
 from ..Utils.block_selector import select_block_size
-from ._runtime import DispatchAudit, FallbackPolicy, PathProfile, WeightLayout, bias_rows
+from ._runtime import DispatchAudit, FallbackPolicy, OpReporting, PathProfile, WeightLayout, bias_rows
 from .static_zero_conv2d import ZERO_BACKEND_FAMILY, make_zero_conv_output  # noqa: F401
 
 
@@ -88,7 +87,7 @@ class _InferencePlan:
         return y
 
 
-class SparseConv2d(nn.Module):
+class SparseConv2d(OpReporting, nn.Module):
     """Conv2d whose forward skips inactive (zero) spikes.
 
     Supported sparse patterns: 3x3/s1/p1, 3x3/s2/p1, 1x1/s1/p0 with
@@ -137,9 +136,7 @@ class SparseConv2d(nn.Module):
         self._workspace = None
         self._plan = None  # _InferencePlan of the last eligible input shape
         self._plan_candidate = False
-        self._last_sparse_ms = 0.0
         self._last_dense_ms = 0.0
-        self._inference_mode = False
         # Runtime fallback policy (dense above an averaged active ratio, the
         # bias-only output after a run of all-zero inputs; sticky zero as in
         # Ops/sparse_conv2d.py:449-496).  Off unless enabled in Utils.config
@@ -149,14 +146,7 @@ class SparseConv2d(nn.Module):
         self._audit = DispatchAudit()
         self._profile = PathProfile("SparseConv2d")
         self._profile.enabled = bool(profile_runtime)
-        self.collect_diag = False
-        self._last_diag = {}
-        self.backend_family = "sparse_kernel"
-        self.diag_path = "conv2d_two_stage_hip"
-        self.fallback_reason = ""
-        self.meta_source = self.diag_source = "measured"
-        self.support_status = "supported"
-        self.score_family = "conv"
+        self._init_reporting("sparse_kernel", "conv2d_two_stage_hip", "conv")
         # "sparse" (library kernels) or "dense" (F.conv2d), set per layer by
         # Utils.dispatch from measurements.
         self.backend_mode = "sparse"
@@ -166,13 +156,6 @@ class SparseConv2d(nn.Module):
         """Kept for API compatibility: the HIP path always launches every
         tile group and skips zero work on the device."""
         self.launch_all_tiles = bool(enabled)
-
-    def set_inference_mode(self, enabled: bool):
-        """Disable diagnostics/profiling so a forward never syncs the host."""
-        self._inference_mode = bool(enabled)
-        if enabled:
-            self.collect_diag = False
-            self.profile_runtime = False
 
     @property
     def runtime_policy(self) -> bool:

@@ -27,13 +27,14 @@ import torch.nn.functional as F
 
 from .. import _lib
 from ..Kernels.fused_conv_lif import _torch_lif_step, sparse_fused_conv_lif_multistep
+from ._runtime import OpReporting
 
 
 def _pair(v):
     return (int(v), int(v)) if isinstance(v, int) else tuple(int(t) for t in v)
 
 
-class FusedSparseConvLIF(nn.Module):
+class FusedSparseConvLIF(OpReporting, nn.Module):
     def __init__(
         self,
         in_channels,
@@ -83,31 +84,14 @@ class FusedSparseConvLIF(nn.Module):
             nn.init.uniform_(self.bias, -bound, bound)
 
         self.v: Optional[torch.Tensor] = None
-        self._last_sparse_ms = 0.0
         self._w_tap = None
         self._w_tap_key = None
         self._workspace = None
-        self._last_diag = {}
-        self.collect_diag = False
-        self.profile_runtime = False
-        self._inference_mode = False
-        self.backend_family = "fused_sparse"
-        self.diag_path = "fused_conv_lif_hip"
-        self.fallback_reason = ""
-        self.meta_source = "measured"
-        self.diag_source = "measured"
-        self.support_status = "supported"
-        self.score_family = "conv"
+        self._init_reporting("fused_sparse", "fused_conv_lif_hip", "conv", profile_runtime=False)
 
     # spikingjelly MemoryModule protocol
     def reset(self):
         self.v = None
-
-    def set_inference_mode(self, enabled: bool):
-        self._inference_mode = bool(enabled)
-        if enabled:
-            self.collect_diag = False
-            self.profile_runtime = False
 
     @classmethod
     def from_conv_and_lif(cls, conv: nn.Conv2d, lif_node, block_size=None, threshold: float = 1e-6,

@@ -25,7 +25,7 @@ import torch.nn.functional as F
 from ..Kernels.linear import BACKEND_NAME, sparse_linear_forward, split_weight_bf16, tap_weight
 from ..Utils import config as _config
 from ..Utils.config import PRESCAN_ACTIVITY_EPS, SPARSE_DENSE_RATIO_THRESHOLD
-from ._runtime import DispatchAudit, FallbackPolicy, PathProfile, WeightLayout, bias_rows
+from ._runtime import DispatchAudit, FallbackPolicy, OpReporting, PathProfile, WeightLayout, bias_rows
 
 
 def _rows_of(x: torch.Tensor, in_features: int) -> Tuple[torch.Tensor, Tuple[int, ...]]:
@@ -38,7 +38,7 @@ def _rows_of(x: torch.Tensor, in_features: int) -> Tuple[torch.Tensor, Tuple[int
                      f"the last dimension, or C*H*W of a [T, B, C, H, W] input, must equal in_features")
 
 
-class SparseLinear(nn.Module):
+class SparseLinear(OpReporting, nn.Module):
     """Linear whose forward skips inactive (zero) input elements."""
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True,
@@ -67,18 +67,8 @@ class SparseLinear(nn.Module):
         self._w_t = WeightLayout(tap_weight)
         self._w_split = WeightLayout(split_weight_bf16)
         self._workspace: Optional[torch.Tensor] = None
-        self._inference_mode = False
-        self._last_sparse_ms = 0.0
+        self._init_reporting("sparse_linear", "runtime", "linear")
         self._last_dense_ms = 0.0
-        self._last_diag: dict = {}
-        self.collect_diag = False
-        # Observability attributes read by the replacer and dispatch.
-        self.backend_family = "sparse_linear"
-        self.diag_path = "runtime"
-        self.fallback_reason = ""
-        self.meta_source = self.diag_source = "measured"
-        self.support_status = "supported"
-        self.score_family = "linear"
         self.backend_mode = "sparse"
 
     @classmethod
@@ -112,14 +102,6 @@ class SparseLinear(nn.Module):
     @property
     def _last_avg_active_ratio(self) -> float:
         return self.policy.last_ratio
-
-    def set_inference_mode(self, enabled: bool):
-        """Inference mode: no diagnostics, no profiling, no ratio sampling,
-        so a forward never waits on the device."""
-        self._inference_mode = bool(enabled)
-        if enabled:
-            self.collect_diag = False
-            self.profile_runtime = False
 
     def get_profile_summary(self) -> str:
         return self._profile.summary()

@@ -14,19 +14,15 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from ._runtime import bias_rows
+from ._runtime import ExactZeroOp
 
 
-class StaticZeroLinear(nn.Module):
-    backend_family = "exact_zero"
-    diag_path = "staticzero_linear"
-
+class StaticZeroLinear(ExactZeroOp, nn.Module):
     def __init__(self, out_features: int, bias: Optional[torch.Tensor] = None):
         super().__init__()
         self.out_features = int(out_features)
-        self.register_buffer("bias_buf", None if bias is None else bias.detach().float().clone())
+        self._init_exact_zero(bias, "static_zero_input_linear", "staticzero_linear")
         self.fallback_reason = ""
-        self.calls = 0
 
     @classmethod
     def from_linear(cls, linear: nn.Linear) -> "StaticZeroLinear":
@@ -35,13 +31,10 @@ class StaticZeroLinear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.dim() < 2:
             raise ValueError(f"StaticZeroLinear takes [..., in_features] input of rank >= 2, not {tuple(x.shape)}")
-        self.calls += 1
-        return bias_rows(self.bias_buf, tuple(x.shape[:-1]), self.out_features, (), x.dtype, x.device)
+        return self._zero_output(tuple(x.shape[:-1]), self.out_features, (), x)
 
     def get_diag(self) -> dict:
-        return dict(backend_family=self.backend_family, diag_path=self.diag_path,
-                    zero_reason="static_zero_input_linear", out_features=self.out_features,
-                    has_bias=self.bias_buf is not None, forward_count=self.calls)
+        return self._zero_diag(out_features=self.out_features)
 
     def extra_repr(self) -> str:
         return f"out_features={self.out_features}, bias={'yes' if self.bias_buf is not None else 'no'}, exact_zero"

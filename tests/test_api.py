@@ -232,3 +232,61 @@ def test_package_exposes_reference_layout():
     assert hasattr(KF, "sparse_fused_conv_lif_forward")
     assert hasattr(O, "SparseConv2d") and hasattr(O, "FusedSparseConvLIF")
     assert cfg.PRESCAN_ACTIVITY_EPS == 1e-6 and cfg.ENABLE_RUNTIME_FALLBACK_POLICY is False
+
+
+# Key names of the reference's exact-zero diagnostics (Ops/static_zero_conv2d.py
+# get_diag and make_synthetic_zero_diag): the schema its harness reads.
+_STATIC_ZERO_DIAG_KEYS = {"backend_family", "zero_reason", "diag_path", "fallback_reason", "has_bias",
+                          "out_channels", "forward_count", "template_cache_size", "sparse_path_executed",
+                          "sparse_total_ms"}
+_SYNTHETIC_ZERO_DIAG_KEYS = {"active_group_ratio", "tile_zero_ratio", "total_group_count", "nonzero_group_count",
+                             "tile_zero_count", "total_tile_count", "effective_k_ratio", "sparse_compute_ms",
+                             "sparse_total_ms", "zero_tiles", "sparse_tiles", "denseish_tiles", "stage1_zero_tiles",
+                             "stage2_tiles", "prescan_mode", "_synthetic", "_diag_path", "backend_family",
+                             "zero_reason"}
+
+
+def test_static_zero_conv_matches_dense_conv_of_zeros_for_every_geometry():
+    from sparseflow_amd.Ops.static_zero_conv2d import make_synthetic_zero_diag
+
+    for k, s, p, d, bias in [(3, 1, 1, 1, True), (3, 2, 1, 1, False), (1, 1, 0, 1, True), (5, 3, 2, 2, True),
+                             ((3, 1), (2, 1), (0, 1), (1, 1), True)]:
+        conv = nn.Conv2d(4, 6, k, s, p, d, bias=bias)
+        sz = StaticZeroConv2d.from_conv(conv, zero_reason="probe")
+        sz.collect_diag = True
+        x = torch.zeros(2, 3, 4, 11, 13)
+        y = sz(x)
+        ref = conv(x.flatten(0, 1)).reshape(2, 3, *conv(x[0]).shape[1:])
+        torch.testing.assert_close(y, ref, rtol=0, atol=0)
+        assert y.dtype == x.dtype
+        diag = sz.get_diag()
+        assert set(diag) == _STATIC_ZERO_DIAG_KEYS and sz._last_diag == diag
+        assert diag["forward_count"] == 1 and diag["has_bias"] == bias and diag["zero_reason"] == "probe"
+    assert sz(torch.zeros(2, 4, 7, 7, dtype=torch.float16)).dtype == torch.float16
+    with pytest.raises(ValueError):
+        sz(torch.zeros(4, 7, 7))
+    syn = make_synthetic_zero_diag("layer1.0.conv2", total_group_count=8.0, total_tile_count=12.0)
+    assert set(syn) - {"layer_name"} == _SYNTHETIC_ZERO_DIAG_KEYS
+    assert syn["zero_tiles"] == syn["stage1_zero_tiles"] == 12 and syn["tile_zero_ratio"] == 1.0
+    assert make_synthetic_zero_diag()["zero_tiles"] == -1
+
+
+def test_static_zero_linear_and_reporting_mixin():
+    from sparseflow_amd.Ops import StaticZeroLinear
+    from sparseflow_amd.Ops.sparse_attention import SparseAttention
+    from sparseflow_amd.Ops.sparse_bmm import SparseBMM, SparseMatmul
+    from sparseflow_amd.Ops.sparse_linear import SparseLinear
+
+    lin = nn.Linear(5, 3)
+    z = StaticZeroLinear.from_linear(lin)
+    torch.testing.assert_close(z(torch.zeros(2, 4, 5)), lin(torch.zeros(2, 4, 5)), rtol=0, atol=0)
+    assert z.get_diag()["forward_count"] == 1 and z.get_diag()["out_features"] == 3
+    mods = [SparseConv2d(4, 4, 3, 1, 1), SparseLinear(4, 4), SparseAttention(2, 4), SparseBMM(), SparseMatmul(),
+            FusedSparseConvLIF(4, 4, 3, padding=1)]
+    for m in mods:
+        assert m._last_sparse_ms == 0.0 and m._last_diag == {} and m.support_status == "supported"
+        m.collect_diag = True
+        m.profile_runtime = True
+        m.set_inference_mode(True)
+        assert m._inference_mode and not m.collect_diag and not m.profile_runtime
+    assert mods[3].diag_path == "bmm" and mods[4].score_family == "matmul"
