@@ -255,12 +255,127 @@ E2E_LIVE_DENSITY = 0.01
 ATTN_WORKLOAD = "config5_spikformer_block"  # T=4, N=64, 196 tokens, dim 384, 12 heads, Bernoulli(0.1)
 
 
+# The 3x3 sparse convs whose live inputs the live run times on their own:
+# one per stage shape (stride 1 and the stride-2 first blocks).
+LIVE_LAYERS = ("layer1.0.conv2", "layer2.0.conv2", "layer2.1.conv2", "layer3.0.conv2", "layer3.1.conv2",
+               "layer4.0.conv2")
+
+
+def spike_spread(x, stride, T):
+    """How the spikes of x [frames, C, H, W] (frames = t*N + n) are spread,
+    computed on the CPU: density per frame and per time step, channel
+    concentration, and the count of active (tap, channel) pairs per output
+    pixel of a 3x3 conv (stride `stride`, padding 1) -- the walk length of
+    that pixel -- with its ratio of tile maximum to tile mean over tiles of
+    64 consecutive output pixels (a lane = pixel wavefront walks as long as
+    its busiest pixel)."""
+    x = x.detach().float().cpu()
+    F_, C, H, W = x.shape
+    dens = float(x.mean())
+    pf = x.mean(dim=(1, 2, 3))
+    pt = pf.reshape(T, -1).mean(1)
+    pc = x.mean(dim=(0, 2, 3))
+    top = torch.sort(pc, descending=True).values
+    k10 = max(1, C // 10)
+    per_px = x.sum(1, keepdim=True)                                   # active channels per input pixel
+    rf = torch.nn.functional.conv2d(per_px, torch.ones(1, 1, 3, 3), stride=stride, padding=1)[:, 0]
+    flat = rf.reshape(-1)
+    n64 = flat.numel() // 64 * 64
+    tiles = flat[:n64].reshape(-1, 64)
+    tm = tiles.mean(1)
+    busy = tm > 0
+    return {
+        "density": round(dens, 6),
+        "frame_density_cv": round(float(pf.std() / max(pf.mean(), 1e-12)), 3),
+        "frame_density_max_over_mean": round(float(pf.max() / max(pf.mean(), 1e-12)), 2),
+        "density_by_step": [round(float(v), 5) for v in pt],
+        "dead_channel_frac": round(float((pc == 0).float().mean()), 3),
+        "top10pct_channel_spike_share": round(float(top[:k10].sum() / max(top.sum(), 1e-12)), 3),
+        "rf_count_mean": round(float(flat.mean()), 2),
+        "rf_count_p99": round(float(torch.quantile(flat[:1 << 22], 0.99)), 1),
+        "rf_count_max": int(flat.max()),
+        "tile_max_over_mean": round(float((tiles.max(1).values[busy] / tm[busy]).mean()), 2) if busy.any() else 0.0,
+    }
+
+
+def live_layer_study(model, img, dev, steps, T):
+    """The 3x3 sparse convs of the calibrated network (LIVE_LAYERS) on the
+    inputs they receive in its forward, timed on their own next to i.i.d.
+    Bernoulli input of the same shape and density; per-kernel times from the
+    library's HIP events; how the spikes are spread (spike_spread) for both
+    inputs."""
+    from sparseflow_amd.neuron import reset_net
+
+    mods = dict(model.named_modules())
+    captured = {}
+    hooks = [mods[n].register_forward_pre_hook(lambda _m, a, n=n: captured.__setitem__(n, a[0].detach().clone()))
+             for n in LIVE_LAYERS if n in mods]
+    with torch.no_grad():
+        reset_net(model)
+        model(img)
+    for h in hooks:
+        h.remove()
+    out = {}
+    for name in LIVE_LAYERS:
+        if name not in captured:
+            continue
+        x = captured.pop(name)  # a copy: no neuron-handed map, so the module prescans it
+        mod = mods[name]
+        s = mod.stride[0]
+        live = spike_spread(x, s, T)
+        xi = make_input(tuple(x.shape), "iid", live["density"], dev, seed=7)
+        with torch.no_grad():
+            live_us = time_gpu(lambda: mod(x), steps, 3) * 1e3
+            iid_us = time_gpu(lambda: mod(xi), steps, 3) * 1e3
+            kl = kernel_times(lambda: mod(x), max(3, steps // 2))
+            ki = kernel_times(lambda: mod(xi), max(3, steps // 2))
+        iid = spike_spread(xi, s, T)
+        out[name] = {
+            "shape": list(x.shape), "stride": s, "c_out": mod.out_channels,
+            "us_live": round(live_us, 1), "us_iid": round(iid_us, 1), "live_over_iid": round(live_us / iid_us, 2),
+            "kernels_us_live": {k: round(v[1] * 1e3, 1) for k, v in kl.items()},
+            "kernels_us_iid": {k: round(v[1] * 1e3, 1) for k, v in ki.items()},
+            "spread_live": live,
+            "spread_iid": {k: iid[k] for k in ("frame_density_cv", "dead_channel_frac", "top10pct_channel_spike_share",
+                                               "rf_count_mean", "rf_count_p99", "rf_count_max", "tile_max_over_mean")},
+        }
+        log(f"[bench] live layer {name}: live {live_us:.1f} us, iid {iid_us:.1f} us; "
+            f"tile max/mean live {live['tile_max_over_mean']} iid {iid['tile_max_over_mean']}")
+        del x, xi
+    return out
+
+
+def spike_flips(sparse_model, dense_model, img):
+    """Per neuron layer, the fraction of spikes that differ between the
+    optimized and the dense model on the same input (a spike that flips at a
+    threshold tie propagates to the layers after it)."""
+    from sparseflow_amd.neuron import LIFNode, reset_net
+
+    def record(m):
+        outs = {}
+        hooks = [mod.register_forward_hook(lambda _m, _i, o, n=name: outs.__setitem__(n, o > 0.5))
+                 for name, mod in m.named_modules() if isinstance(mod, LIFNode)]
+        with torch.no_grad():
+            reset_net(m)
+            m(img)
+        for h in hooks:
+            h.remove()
+        return outs
+
+    a, b = record(sparse_model), record(dense_model)
+    return {n: float((a[n] != b[n]).float().mean()) for n in a if n in b}
+
+
 def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32, live=False):
     """Spiking-ResNet50 forward (random init, BN folded, multi-step LIF
     tau=2 v_th=1 hard reset) through optimize(): images/s = batch / t.
-    live=True first calibrates every neuron layer's threshold on the timed
-    input to E2E_LIVE_DENSITY spikes (Models.calibrate_lif_thresholds_); the
-    dense baseline then has the same thresholds."""
+    live=True first calibrates every neuron layer's threshold to
+    E2E_LIVE_DENSITY spikes (Models.calibrate_lif_thresholds_) on a separate
+    calibration batch, then times the network on another batch and reports
+    the densities measured on that one; the dense baseline has the same
+    thresholds.  The live run also times single layers on their live inputs
+    (live_layer_study) and counts spike flips against the dense model
+    (spike_flips, on two images)."""
     import copy
 
     import sparseflow_amd as sf
@@ -278,7 +393,11 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32, live=False):
     img = torch.randn(batch, 3, 224, 224, generator=g, device=dev)
     calib = None
     if live:
-        calib = calibrate_lif_thresholds_(model, img, target_density=E2E_LIVE_DENSITY)
+        # Calibrated on other images than the timed ones.
+        gc = torch.Generator(device=dev).manual_seed(1)
+        img_cal = torch.randn(batch, 3, 224, 224, generator=gc, device=dev)
+        calib = calibrate_lif_thresholds_(model, img_cal, target_density=E2E_LIVE_DENSITY)
+        del img_cal
         log(f"[bench] e2e live: thresholds calibrated to {E2E_LIVE_DENSITY} in {time.time() - t0:.1f} s")
     dense = copy.deepcopy(model) if with_dense else None
     sf.optimize(model, sample_input=img, verbose=False)
@@ -299,6 +418,10 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32, live=False):
         h.remove()
     torch.cuda.synchronize()
     log(f"[bench] e2e: first forward done at {time.time() - t0:.1f} s")
+    flips = None
+    if live and dense is not None:
+        flips = spike_flips(model, dense, img[:2])
+        log(f"[bench] e2e live: spike flips vs dense at batch 2, max layer {max(flips.values()):.2e}")
     with torch.no_grad():
         ums = time_gpu(lambda: run(model), steps, warmup)
         log(f"[bench] e2e: unfused {ums:.2f} ms per forward ({time.time() - t0:.1f} s)")
@@ -315,9 +438,12 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32, live=False):
             "mean_spike_density": sum(densities.values()) / max(1, len(densities)),
             "spike_density_by_layer": {k: round(v, 5) for k, v in densities.items()},
         }
+        if flips is not None:
+            res["spike_flip_frac_vs_dense_batch2"] = {k: float(f"{v:.3g}") for k, v in flips.items()}
         if calib is not None:
             res["threshold_calibration"] = {
                 "target_density": E2E_LIVE_DENSITY,
+                "calibration_input": "a separate batch (seed 1); timed input seed 0",
                 "method": "per neuron layer, in network order: bisection of v_threshold on the layer's input "
                           "currents over 2^20 sampled neurons (Models.calibrate_lif_thresholds_)",
                 "v_threshold_min": round(min(v for v, _ in calib.values()), 4),
@@ -333,6 +459,10 @@ def bench_e2e(steps, warmup, dev, with_dense=True, T=16, batch=32, live=False):
             res["speedup_vs_dense"] = dms / ms
             res["max_abs_logit_diff_vs_dense"] = float((out - ref).abs().max())
             res["max_abs_logit_vs_dense"] = float(ref.abs().max())
+            del dense
+        if live:
+            torch.cuda.empty_cache()
+            res["live_layers"] = live_layer_study(model, img, dev, max(5, steps * 2), T)
     return res
 
 

@@ -13,6 +13,8 @@
  *                                          (c & 31) of word (c >> 5) of pixel
  *                                          p is 1 iff f16(|x[n,c,p]|) > f16(thr)
  *                                          cwp = sf_bitmap_words_per_pixel(c_in)
+ *           (sf_bitmap_layout: the same words may also be laid out as word
+ *           planes [n, cwp, h_in*w_in], see the *_layout entry points)
  *   flags   [n, ceil(h*w / chunk)] uint32  1 where a pixel chunk holds a value
  *                                          outside {0, 1} (chunk is chosen by
  *                                          the library from the shape)
@@ -54,6 +56,13 @@ typedef struct sf_conv_desc {
   int32_t kernel, stride, pad;   /* supported: (3,1,1) (3,2,1) (1,1,0) (1,2,0) */
   int32_t in_dtype, out_dtype;   /* sf_dtype */
 } sf_conv_desc;
+
+/* Order of a spike bitmap's words.  PIXEL_MAJOR: [n, h*w, cwp] (the
+ * cwp words of a pixel together; sf_prescan_pack's layout).  PLANES:
+ * [n, cwp, h*w] (word w of every pixel of a frame together), which the 3x3
+ * pixel-tile and row kernels read one run per load.  With cwp == 1 the two
+ * coincide. */
+typedef enum sf_bitmap_layout { SF_BITMAP_PIXEL_MAJOR = 0, SF_BITMAP_PLANES = 1 } sf_bitmap_layout;
 
 /* Multi-step LIF neuron (spikingjelly LIFNode semantics). */
 typedef struct sf_lif_params {
@@ -147,6 +156,24 @@ int sf_conv2d_sparse(const sf_conv_desc* desc, const uint32_t* bits,
                      const uint32_t* flags, const void* x, const float* wt,
                      const float* bias, void* y, void* stream);
 
+/* The bitmap layout that the Stage-2 kernel sf_conv2d_sparse picks for desc
+ * reads fastest: SF_BITMAP_PLANES for the 3x3 pixel-tile ("conv_px3") and
+ * K-chunked row ("conv_rows_kc") kernels, SF_BITMAP_PIXEL_MAJOR otherwise.
+ * A neuron layer that hands its spike map to this convolution writes it in
+ * that layout (sf_lif_multistep_layout, sf_conv1x1_lif_sparse_layout).
+ * Returns a negative sf_status for an invalid desc. */
+int sf_conv2d_bitmap_layout(const sf_conv_desc* desc);
+
+/* sf_conv2d_sparse on a bitmap in the given sf_bitmap_layout.  PLANES is
+ * taken where sf_conv2d_bitmap_layout(desc) is PLANES or cwp == 1, else
+ * SF_ERR_UNSUPPORTED (the caller prescans x instead).  Same kernels and
+ * results as sf_conv2d_sparse, bit for bit.  Same reference interface as
+ * sf_conv2d_sparse (the handed map itself has no counterpart there). */
+int sf_conv2d_sparse_layout(const sf_conv_desc* desc, const uint32_t* bits,
+                            int32_t layout, const uint32_t* flags,
+                            const void* x, const float* wt, const float* bias,
+                            void* y, void* stream);
+
 /* Stage 1a + Stage 2 in one call; the bitmap lives in `workspace`.  3x3
  * stride-1 layers with c_in <= 64 on 32-wide frames (other than an image
  * stem) run as one launch with the prescan fused into the conv
@@ -227,6 +254,17 @@ int sf_conv1x1_lif_sparse_binres(const sf_conv_desc* desc, int32_t T,
                                  const float* v_init, void* spikes, float* v_out,
                                  uint32_t* out_bits, uint32_t* out_flags, void* stream);
 
+/* sf_conv1x1_lif_sparse with the output spike map written in out_layout
+ * (sf_bitmap_layout); the input bitmap is pixel-major as there.  Same
+ * reference interface as sf_conv1x1_lif_sparse. */
+int sf_conv1x1_lif_sparse_layout(const sf_conv_desc* desc, int32_t T,
+                                 const uint32_t* bits, const uint32_t* flags,
+                                 const void* x, const float* wt, const float* bias,
+                                 const void* x2, const sf_lif_params* lif,
+                                 const float* v_init, void* spikes, float* v_out,
+                                 uint32_t* out_bits, uint32_t* out_flags,
+                                 int32_t out_layout, void* stream);
+
 /* ---- spiking neuron -------------------------------------------------------- */
 
 /* Multi-step LIF over T steps of n x c x hw neurons: x [T, n, c, hw] input
@@ -248,6 +286,15 @@ int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T,
                      int64_t n, int32_t c, int64_t hw, const sf_lif_params* lif,
                      const float* v_init, void* spikes, int32_t out_dtype,
                      float* v_out, uint32_t* bits, uint32_t* flags, void* stream);
+
+/* sf_lif_multistep with the spike map written in bits_layout
+ * (sf_bitmap_layout).  Same reference interface as sf_lif_multistep. */
+int sf_lif_multistep_layout(const void* x, const void* x2, int32_t in_dtype,
+                            int32_t T, int64_t n, int32_t c, int64_t hw,
+                            const sf_lif_params* lif, const float* v_init,
+                            void* spikes, int32_t out_dtype, float* v_out,
+                            uint32_t* bits, uint32_t* flags, int32_t bits_layout,
+                            void* stream);
 
 /* Max pooling (kernel k, stride, padding <= k/2, floor mode) of n frames of a
  * binary spike tensor [c, h_in, w_in] given only by its spike map `bits`

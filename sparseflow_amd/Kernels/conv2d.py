@@ -95,6 +95,21 @@ def _build_active_tile_ids(tile_class_buf, N_TILES, active_tile_ids_buf=None):
     return active.contiguous(), count
 
 
+_layout_cache: dict = {}
+
+
+def _bitmap_layout(desc) -> int:
+    """sf_conv2d_bitmap_layout(desc), cached by shape (a pure function of it)."""
+    key = (desc.n, desc.c_in, desc.h_in, desc.w_in, desc.c_out, desc.h_out, desc.w_out, desc.kernel, desc.stride,
+           desc.pad, desc.in_dtype, desc.out_dtype)
+    v = _layout_cache.get(key)
+    if v is None:
+        if len(_layout_cache) > 256:
+            _layout_cache.clear()
+        v = _layout_cache[key] = _lib.conv2d_bitmap_layout(desc)
+    return v
+
+
 def _out_hw(H, W, k, s, p, d=1):
     return (H + 2 * p - d * (k - 1) - 1) // s + 1, (W + 2 * p - d * (k - 1) - 1) // s + 1
 
@@ -242,11 +257,18 @@ def sparse_conv2d_forward(
     stats = None
     ms = 0.0
 
-    handed = None if (need_meta or return_ms) else spike_map.lookup(x, threshold)
+    handed = None
+    if not (need_meta or return_ms) and spike_map.recorded(x):
+        # The neuron layer that produced x may have written its spike map;
+        # tell it which word layout this shape's Stage-2 kernel reads
+        # fastest (it writes that layout from its next forward on).
+        want = _bitmap_layout(desc)
+        accept = (spike_map.PIXEL_MAJOR, spike_map.PLANES) if want == spike_map.PLANES else (spike_map.PIXEL_MAJOR,)
+        handed = spike_map.lookup(x, threshold, accept=accept, want=want, consumer=("conv2d", weight.data_ptr()))
     if handed is not None:
-        # The neuron layer that produced x already wrote its spike map.
         meta["reason"] = "bitmap_gather_handed_spike_map"
-        _lib.conv2d_sparse(desc, handed[0], handed[1], x, wt, b, y)
+        meta["bitmap_layout"] = "planes" if handed[2] == spike_map.PLANES else "pixel_major"
+        _lib.conv2d_sparse(desc, handed[0], handed[1], x, wt, b, y, layout=handed[2])
     elif not (need_meta or return_ms):
         _lib.conv2d_forward(desc, x, wt, b, threshold, workspace, y)
     else:

@@ -219,6 +219,7 @@ def sparse_conv1x1_lif_multistep(
     w_tap: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
     emit_spike_map: bool = True,
+    map_requests: Optional["spike_map.LayoutRequests"] = None,
 ):
     """Fused 1x1 conv + multi-step LIF (+ residual) on device tensors:
     x [T, N, C, H, W] -> (spikes [T, N, C_out, H, W] in x.dtype, v_T
@@ -228,7 +229,9 @@ def sparse_conv1x1_lif_multistep(
     when it handed one over (else x is prescanned into `workspace`); the
     output's spike map is attached to the spikes for the next sparse conv.
     One launch (sf_conv1x1_lif_sparse); the currents never reach HBM.
-    The membrane starts at v_init, or 0."""
+    The membrane starts at v_init, or 0.  `map_requests` (the neuron's
+    LayoutRequests) picks the output map's layout and records it with the
+    map."""
     from . import spike_map
 
     if x.dim() != 5 or not x.is_cuda:
@@ -247,14 +250,17 @@ def sparse_conv1x1_lif_multistep(
     desc = _lib.conv_desc(N, C, H, W, C_OUT, H, W, 1, 1, 0, code, code)
     # A residual that is itself a registered spike tensor (the spikes entering
     # a bottleneck) is read from its bitmap: 1/32 of its fp32 bytes.
+    # The flat kernel reads pixel-major words (input map and residual map).
+    pm = spike_map.PIXEL_MAJOR
     res_bits = None
     if residual is not None:
-        rmap = spike_map.lookup(residual.view(T * N, C_OUT, H, W), threshold)
+        rmap = spike_map.lookup(residual.view(T * N, C_OUT, H, W), threshold, want=pm,
+                                consumer=("conv1x1_lif_residual", weight.data_ptr()))
         if rmap is not None:
             res_bits = rmap[0]
-    handed = spike_map.lookup(x4, threshold)
+    handed = spike_map.lookup(x4, threshold, want=pm, consumer=("conv1x1_lif", weight.data_ptr()))
     if handed is not None:
-        bits, flags = handed
+        bits, flags = handed[0], handed[1]
     else:
         bits, flags = _lib.prescan_pack(x4, threshold)
     wt = w_tap if w_tap is not None else _lib.tap_major_weight(weight)
@@ -267,6 +273,11 @@ def sparse_conv1x1_lif_multistep(
     spikes = torch.empty((T, N, C_OUT, H, W), dtype=x.dtype, device=x.device)
     v_out = torch.empty((N, C_OUT, H, W), dtype=torch.float32, device=x.device)
     out_bits = out_flags = None
+    # Word planes only where asked for and without a residual map (the
+    # kernel reads a residual map in the output map's pixel-major layout).
+    out_layout = pm
+    if map_requests is not None and res_bits is None:
+        out_layout = map_requests.layout
     if emit_spike_map:
         L = _lib.lib()
         frames = T * N
@@ -276,7 +287,7 @@ def sparse_conv1x1_lif_multistep(
                                 device=x.device)
     _lib.conv1x1_lif_sparse(desc, T, bits, flags, x, wt, b, residual, lif_params(tau, v_threshold, v_reset,
                                                                                  decay_input),
-                            vi, spikes, v_out, out_bits, out_flags, res_bits=res_bits)
+                            vi, spikes, v_out, out_bits, out_flags, res_bits=res_bits, out_layout=out_layout)
     if emit_spike_map:
-        spike_map.attach(spikes, T * N, C_OUT, H, W, out_bits, out_flags)
+        spike_map.attach(spikes, T * N, C_OUT, H, W, out_bits, out_flags, out_layout, map_requests)
     return spikes, v_out

@@ -238,5 +238,5 @@ class SparseConv1x1LIF(nn.Module):
         spikes, lif.v = sparse_conv1x1_lif_multistep(
             x, self.conv.weight, self.conv.bias, tau=lif.tau, v_threshold=lif.v_threshold, v_reset=lif.v_reset,
             decay_input=lif.decay_input, residual=residual, threshold=self.conv.threshold, v_init=v0,
-            w_tap=self.conv._get_w_tap())
+            w_tap=self.conv._get_w_tap(), map_requests=getattr(lif, "map_requests", None))
         return spikes

@@ -31,7 +31,8 @@ class SpikeMaxPool2d(nn.MaxPool2d):
             return None
         if not spike_map.recorded(x):
             return None
-        handed = spike_map.lookup(x, 0.0)
+        # The pooling kernel reads pixel-major words.
+        handed = spike_map.lookup(x, 0.0, want=spike_map.PIXEL_MAJOR, consumer=("spike_maxpool", id(self)))
         if handed is None:
             return None
         n, c, h, w = (int(v) for v in x.shape)

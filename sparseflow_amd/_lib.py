@@ -27,6 +27,7 @@ SF_ERR_WORKSPACE = 3
 SF_ERR_HIP = 4
 
 SF_F32, SF_F16, SF_BF16 = 0, 1, 2
+SF_BITMAP_PIXEL_MAJOR, SF_BITMAP_PLANES = 0, 1
 _DTYPE_CODE = {torch.float32: SF_F32, torch.float16: SF_F16, torch.bfloat16: SF_BF16}
 
 # Every exported symbol of include/sparseflow.h with its ctypes signature.
@@ -48,13 +49,19 @@ EXPORTS = {
          c_int32, c_int32, c_int32, _P, _P, _P, _P, _P, _P],
     ),
     "sf_conv2d_sparse": (c_int, [_P, _P, _P, _P, _P, _P, _P, _P]),
+    "sf_conv2d_bitmap_layout": (c_int, [_P]),
+    "sf_conv2d_sparse_layout": (c_int, [_P, _P, c_int32, _P, _P, _P, _P, _P, _P]),
     "sf_conv2d_forward": (c_int, [_P, _P, _P, _P, c_float, _P, c_size_t, _P, _P]),
     "sf_conv2d_forward_noalloc": (c_int, [_P, _P, _P, _P, c_float, _P, _P]),
     "sf_conv_lif_forward": (c_int, [_P, c_int32, _P, _P, _P, _P, c_float, _P, _P, _P, _P, c_size_t, _P]),
     "sf_conv1x1_lif_sparse": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "sf_conv1x1_lif_sparse_binres": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "sf_conv1x1_lif_sparse_layout": (c_int, [_P, c_int32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, c_int32,
+                                             _P]),
     "sf_lif_multistep": (c_int, [_P, _P, c_int32, c_int32, c_int64, c_int32, c_int64, _P, _P, _P, c_int32, _P, _P, _P,
                                  _P]),
+    "sf_lif_multistep_layout": (c_int, [_P, _P, c_int32, c_int32, c_int64, c_int32, c_int64, _P, _P, _P, c_int32, _P,
+                                        _P, _P, c_int32, _P]),
     "sf_spike_maxpool2d": (c_int, [_P, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, _P, c_int32,
                                    _P, _P]),
     "sf_linear_bitmap_bytes": (c_size_t, [c_int64, c_int32]),
@@ -273,11 +280,27 @@ def prescan_tiles(bits: torch.Tensor, n: int, c: int, h_in: int, w_in: int, h_ou
 # ---------------------------------------------------------------------------
 
 def conv2d_sparse(desc: ConvDesc, bits: torch.Tensor, flags: torch.Tensor, x: torch.Tensor,
-                  wt: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor) -> torch.Tensor:
-    rc = lib().sf_conv2d_sparse(ctypes.byref(desc), _ptr(bits), _ptr(flags), _ptr(x), _ptr(wt),
-                                _ptr(bias), _ptr(y), _stream(x.device))
-    _check(rc, "sf_conv2d_sparse")
+                  wt: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor,
+                  layout: int = SF_BITMAP_PIXEL_MAJOR) -> torch.Tensor:
+    """Stage 2 over a bitmap in `layout` (word planes raise UnsupportedError
+    for shapes whose Stage-2 kernel reads pixel-major words)."""
+    if layout == SF_BITMAP_PIXEL_MAJOR:
+        rc = lib().sf_conv2d_sparse(ctypes.byref(desc), _ptr(bits), _ptr(flags), _ptr(x), _ptr(wt),
+                                    _ptr(bias), _ptr(y), _stream(x.device))
+        _check(rc, "sf_conv2d_sparse")
+        return y
+    rc = lib().sf_conv2d_sparse_layout(ctypes.byref(desc), _ptr(bits), int(layout), _ptr(flags), _ptr(x), _ptr(wt),
+                                       _ptr(bias), _ptr(y), _stream(x.device))
+    _check(rc, "sf_conv2d_sparse_layout")
     return y
+
+
+def conv2d_bitmap_layout(desc: ConvDesc) -> int:
+    """The bitmap layout the shape's Stage-2 kernel reads fastest."""
+    rc = int(lib().sf_conv2d_bitmap_layout(ctypes.byref(desc)))
+    if rc < 0:
+        _check(-rc, "sf_conv2d_bitmap_layout")
+    return rc
 
 
 def conv2d_forward(desc: ConvDesc, x: torch.Tensor, wt: torch.Tensor, bias: Optional[torch.Tensor],
@@ -315,11 +338,11 @@ def conv_lif_forward(desc: ConvDesc, T: int, x: torch.Tensor, wt: torch.Tensor, 
 def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torch.Tensor] = None,
                   spikes: Optional[torch.Tensor] = None, v_out: Optional[torch.Tensor] = None,
                   out_dtype: Optional[torch.dtype] = None, x2: Optional[torch.Tensor] = None,
-                  spike_map: bool = False):
+                  spike_map: bool = False, map_layout: int = SF_BITMAP_PIXEL_MAJOR):
     """x [T, ...] currents (+ x2, same shape) -> (spikes [T, ...] in out_dtype
     (default x's), v [...] f32, map) where map is None or, with spike_map=True
-    on a [T, N, C, H, W] input, (bits, flags) of the T*N output frames in the
-    prescan's layout."""
+    on a [T, N, C, H, W] input, (bits, flags) of the T*N output frames in
+    `map_layout` (the prescan's pixel-major words, or word planes)."""
     _require_device(x, "x")
     x = x.contiguous()
     if x.shape[0] != T:
@@ -352,10 +375,10 @@ def lif_multistep(x: torch.Tensor, T: int, lif: LifParams, v_init: Optional[torc
                            device=x.device)
         flags = torch.empty(max(int(L.sf_prescan_flags_bytes(frames, c, 1, hw)) // 4, 1), dtype=torch.int32,
                             device=x.device)
-    rc = lib().sf_lif_multistep(_ptr(x), _ptr(x2), dtype_code(x.dtype), int(T), n, c, hw, ctypes.byref(lif),
-                                _ptr(v_init), _ptr(spikes), dtype_code(out_dtype), _ptr(v_out), _ptr(bits),
-                                _ptr(flags), _stream(x.device))
-    _check(rc, "sf_lif_multistep")
+    rc = lib().sf_lif_multistep_layout(_ptr(x), _ptr(x2), dtype_code(x.dtype), int(T), n, c, hw, ctypes.byref(lif),
+                                       _ptr(v_init), _ptr(spikes), dtype_code(out_dtype), _ptr(v_out), _ptr(bits),
+                                       _ptr(flags), int(map_layout), _stream(x.device))
+    _check(rc, "sf_lif_multistep_layout")
     return spikes, v_out, (None if bits is None else (bits, flags))
 
 
@@ -381,20 +404,24 @@ def conv1x1_lif_sparse(desc: ConvDesc, T: int, bits: torch.Tensor, flags: torch.
                        wt: torch.Tensor, bias: Optional[torch.Tensor], x2: Optional[torch.Tensor], lif: LifParams,
                        v_init: Optional[torch.Tensor], spikes: torch.Tensor, v_out: torch.Tensor,
                        out_bits: Optional[torch.Tensor], out_flags: Optional[torch.Tensor],
-                       res_bits: Optional[torch.Tensor] = None) -> None:
-    """res_bits: a binary residual's spike map, read instead of x2
-    (sf_conv1x1_lif_sparse_binres)."""
+                       res_bits: Optional[torch.Tensor] = None, out_layout: int = SF_BITMAP_PIXEL_MAJOR) -> None:
+    """res_bits: a binary residual's pixel-major spike map, read instead of
+    x2 (sf_conv1x1_lif_sparse_binres); out_layout: the output map's layout
+    (word planes only without res_bits)."""
     if res_bits is not None:
+        if out_layout != SF_BITMAP_PIXEL_MAJOR:
+            raise UnsupportedError("a binary residual's map is read with a pixel-major output map")
         rc = lib().sf_conv1x1_lif_sparse_binres(ctypes.byref(desc), int(T), _ptr(bits), _ptr(flags), _ptr(x),
                                                 _ptr(wt), _ptr(bias), _ptr(res_bits), ctypes.byref(lif),
                                                 _ptr(v_init), _ptr(spikes), _ptr(v_out), _ptr(out_bits),
                                                 _ptr(out_flags), _stream(x.device))
         _check(rc, "sf_conv1x1_lif_sparse_binres")
         return
-    rc = lib().sf_conv1x1_lif_sparse(ctypes.byref(desc), int(T), _ptr(bits), _ptr(flags), _ptr(x), _ptr(wt),
-                                     _ptr(bias), _ptr(x2), ctypes.byref(lif), _ptr(v_init), _ptr(spikes), _ptr(v_out),
-                                     _ptr(out_bits), _ptr(out_flags), _stream(x.device))
-    _check(rc, "sf_conv1x1_lif_sparse")
+    rc = lib().sf_conv1x1_lif_sparse_layout(ctypes.byref(desc), int(T), _ptr(bits), _ptr(flags), _ptr(x), _ptr(wt),
+                                            _ptr(bias), _ptr(x2), ctypes.byref(lif), _ptr(v_init), _ptr(spikes),
+                                            _ptr(v_out), _ptr(out_bits), _ptr(out_flags), int(out_layout),
+                                            _stream(x.device))
+    _check(rc, "sf_conv1x1_lif_sparse_layout")
 
 
 # ---------------------------------------------------------------------------

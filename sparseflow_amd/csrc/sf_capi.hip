@@ -219,9 +219,13 @@ int run_stage2(Stage2 k, const sf_conv_desc* d, const sf::ConvArgs& a, void* str
   return SF_OK;
 }
 
-// Prescan into word planes ([frame][cwp][hw]) for the pixel-tile kernels,
-// which load one bitmap word of 64 neighbouring pixels at a time; every other
-// Stage 2 kernel reads the [hw][cwp] words of sf_prescan_pack.
+// Whether the Stage 2 kernel reads word planes ([frame][cwp][hw]): the
+// pixel-tile and K-chunked row kernels load one bitmap word of 64
+// neighbouring pixels at a time; every other Stage 2 kernel reads the
+// [hw][cwp] words of sf_prescan_pack.
+bool reads_planes(Stage2 k) { return k == Stage2::kPx3 || k == Stage2::kRowsKc; }
+
+// Prescan into word planes or pixel-major words.
 int prescan_for(const sf_conv_desc* d, int64_t frames, const void* x, float threshold, bool planar, uint32_t* bits,
                 uint32_t* flags, void* stream) {
   sf::PackArgs pa = pack_args(x, frames, d->c_in, d->h_in, d->w_in, threshold, bits, flags);
@@ -282,7 +286,7 @@ void timing_end(int kernel_id, hipStream_t stream) {
 
 extern "C" {
 
-int sf_version(void) { return 100; }
+int sf_version(void) { return 101; }
 
 const char* sf_last_error(void) { return g_last_error.c_str(); }
 
@@ -409,6 +413,31 @@ int sf_conv2d_sparse(const sf_conv_desc* d, const uint32_t* bits, const uint32_t
     return fail(SF_ERR_INVALID, "NULL pointer");
   const sf::ConvArgs a = conv_args(d, d->n, bits, flags, x, wt, bias, y, false);
   return run_stage2(pick_stage2(d, a), d, a, stream);
+}
+
+int sf_conv2d_bitmap_layout(const sf_conv_desc* d) {
+  const int rc = check_desc(d);
+  if (rc != SF_OK) return -rc;
+  const sf::ConvArgs a = conv_args(d, d->n, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, false);
+  return reads_planes(pick_stage2(d, a)) ? SF_BITMAP_PLANES : SF_BITMAP_PIXEL_MAJOR;
+}
+
+int sf_conv2d_sparse_layout(const sf_conv_desc* d, const uint32_t* bits, int32_t layout, const uint32_t* flags,
+                            const void* x, const float* wt, const float* bias, void* y, void* stream) {
+  if (layout != SF_BITMAP_PIXEL_MAJOR && layout != SF_BITMAP_PLANES) return fail(SF_ERR_INVALID, "unknown bitmap layout");
+  int rc = check_desc(d);
+  if (rc != SF_OK) return rc;
+  if (d->n == 0) return SF_OK;
+  if (bits == nullptr || flags == nullptr || x == nullptr || wt == nullptr || y == nullptr)
+    return fail(SF_ERR_INVALID, "NULL pointer");
+  sf::ConvArgs a = conv_args(d, d->n, bits, flags, x, wt, bias, y, false);
+  const Stage2 k = pick_stage2(d, a);
+  // With one word per pixel the two layouts are the same words.
+  if (layout == SF_BITMAP_PLANES && a.cwp > 1) {
+    if (!reads_planes(k)) return fail(SF_ERR_UNSUPPORTED, "word planes: this shape's Stage 2 reads pixel-major words");
+    use_planes(a);
+  }
+  return run_stage2(k, d, a, stream);
 }
 
 // ---- sparse linear ------------------------------------------------------------
@@ -655,7 +684,7 @@ int sf_conv2d_forward(const sf_conv_desc* d, const void* x, const float* wt, con
   const Workspace ws = carve(workspace, d->n, d->c_in, d->h_in, d->w_in);
   sf::ConvArgs a = conv_args(d, d->n, ws.bits, ws.flags, x, wt, bias, y, false);
   const Stage2 k = pick_stage2(d, a);
-  const bool planar = k == Stage2::kPx3;
+  const bool planar = reads_planes(k);
   rc = prescan_for(d, d->n, x, threshold, planar, ws.bits, ws.flags, stream);
   if (rc != SF_OK) return rc;
   if (planar) use_planes(a);
@@ -764,7 +793,10 @@ int sf_conv_lif_forward(const sf_conv_desc* d, int32_t T, const void* x, const f
 static int conv1x1_lif_impl(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags,
                             const void* x, const float* wt, const float* bias, const void* x2,
                             const uint32_t* res_bits, const sf_lif_params* lif, const float* v_init, void* spikes,
-                            float* v_out, uint32_t* out_bits, uint32_t* out_flags, void* stream) {
+                            float* v_out, uint32_t* out_bits, uint32_t* out_flags, int32_t out_layout,
+                            void* stream) {
+  if (out_layout != SF_BITMAP_PIXEL_MAJOR && out_layout != SF_BITMAP_PLANES)
+    return fail(SF_ERR_INVALID, "unknown bitmap layout");
   int rc = check_desc(d, false);
   if (rc != SF_OK) return rc;
   if (d->kernel != 1 || d->stride != 1) return fail(SF_ERR_UNSUPPORTED, "fused conv1x1-LIF: 1x1 stride 1 only");
@@ -788,8 +820,9 @@ static int conv1x1_lif_impl(const sf_conv_desc* d, int32_t T, const uint32_t* bi
   a.hard_reset = lif->hard_reset != 0;
   a.decay_input = lif->decay_input != 0;
   const sf::PackPlan op = sf::make_pack_plan(frames, d->c_out, d->h_out, d->w_out);
-  rc = sf::launch_conv_lif_flat(a, d->in_dtype, d->out_dtype, x2, res_bits, out_bits, out_flags, op.cwp, op.chunk,
-                                op.chunks_per_frame, static_cast<hipStream_t>(stream));
+  rc = sf::launch_conv_lif_flat(a, d->in_dtype, d->out_dtype, x2, res_bits, out_bits, out_flags, op.cwp,
+                                out_layout == SF_BITMAP_PLANES ? 1 : 0, op.chunk, op.chunks_per_frame,
+                                static_cast<hipStream_t>(stream));
   if (rc != hipSuccess) return hip_fail(rc, "conv_lif_flat launch");
   return SF_OK;
 }
@@ -799,7 +832,15 @@ int sf_conv1x1_lif_sparse(const sf_conv_desc* d, int32_t T, const uint32_t* bits
                           const float* v_init, void* spikes, float* v_out, uint32_t* out_bits, uint32_t* out_flags,
                           void* stream) {
   return conv1x1_lif_impl(d, T, bits, flags, x, wt, bias, x2, nullptr, lif, v_init, spikes, v_out, out_bits,
-                          out_flags, stream);
+                          out_flags, SF_BITMAP_PIXEL_MAJOR, stream);
+}
+
+int sf_conv1x1_lif_sparse_layout(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags,
+                                 const void* x, const float* wt, const float* bias, const void* x2,
+                                 const sf_lif_params* lif, const float* v_init, void* spikes, float* v_out,
+                                 uint32_t* out_bits, uint32_t* out_flags, int32_t out_layout, void* stream) {
+  return conv1x1_lif_impl(d, T, bits, flags, x, wt, bias, x2, nullptr, lif, v_init, spikes, v_out, out_bits,
+                          out_flags, out_layout, stream);
 }
 
 int sf_conv1x1_lif_sparse_binres(const sf_conv_desc* d, int32_t T, const uint32_t* bits, const uint32_t* flags,
@@ -808,7 +849,7 @@ int sf_conv1x1_lif_sparse_binres(const sf_conv_desc* d, int32_t T, const uint32_
                                  uint32_t* out_bits, uint32_t* out_flags, void* stream) {
   if (d != nullptr && d->n > 0 && res_bits == nullptr) return fail(SF_ERR_INVALID, "res_bits NULL");
   return conv1x1_lif_impl(d, T, bits, flags, x, wt, bias, nullptr, res_bits, lif, v_init, spikes, v_out, out_bits,
-                          out_flags, stream);
+                          out_flags, SF_BITMAP_PIXEL_MAJOR, stream);
 }
 
 int sf_spike_maxpool2d(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in, int32_t w_in, int32_t k,
@@ -834,6 +875,15 @@ int sf_spike_maxpool2d(const uint32_t* bits, int64_t n, int32_t c, int32_t h_in,
 int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T, int64_t n, int32_t c, int64_t hw,
                      const sf_lif_params* lif, const float* v_init, void* spikes, int32_t out_dtype, float* v_out,
                      uint32_t* bits, uint32_t* flags, void* stream) {
+  return sf_lif_multistep_layout(x, x2, in_dtype, T, n, c, hw, lif, v_init, spikes, out_dtype, v_out, bits, flags,
+                                 SF_BITMAP_PIXEL_MAJOR, stream);
+}
+
+int sf_lif_multistep_layout(const void* x, const void* x2, int32_t in_dtype, int32_t T, int64_t n, int32_t c,
+                            int64_t hw, const sf_lif_params* lif, const float* v_init, void* spikes, int32_t out_dtype,
+                            float* v_out, uint32_t* bits, uint32_t* flags, int32_t bits_layout, void* stream) {
+  if (bits_layout != SF_BITMAP_PIXEL_MAJOR && bits_layout != SF_BITMAP_PLANES)
+    return fail(SF_ERR_INVALID, "unknown bitmap layout");
   if (lif == nullptr) return fail(SF_ERR_INVALID, "lif params NULL");
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
   if (out_dtype != in_dtype && out_dtype != SF_F32)
@@ -856,7 +906,7 @@ int sf_lif_multistep(const void* x, const void* x2, int32_t in_dtype, int32_t T,
   }
   const int rc = sf::launch_lif_multistep(x, x2, in_dtype, T, n, c, hw, lif->tau, lif->v_threshold, lif->v_reset,
                                           lif->hard_reset, lif->decay_input, v_init, spikes, out_dtype, v_out, bits, cwp,
-                                          flags, nflags, s);
+                                          bits_layout == SF_BITMAP_PLANES ? 1 : 0, flags, nflags, s);
   if (rc != hipSuccess) return hip_fail(rc, "lif_multistep launch");
   return SF_OK;
 }

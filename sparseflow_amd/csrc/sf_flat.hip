@@ -259,16 +259,19 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
   }
 }
 
-// Output spike map of the fused LIF variant (the prescan layout of the
-// spikes: cwp words per pixel, chunk flags cleared).
+// Output spike map of the fused LIF variant (cwp words per pixel, chunk
+// flags cleared): word w of pixel p of a frame at p * ps + w * ws words from
+// the frame's start, (cwp, 1) pixel-major or (1, hw) as word planes.
 struct FlatLifOut {
   uint32_t* bits;     // nullable
   uint32_t* flags;
   int cwp, chunk;
   int64_t cpf;        // flag chunks per frame
-  // Nullable: a binary residual given by its spike map (same layout as bits),
-  // read instead of x2: two words per pixel instead of 64 values.
+  // Nullable: a binary residual given by its pixel-major spike map (cwp
+  // words per pixel), read instead of x2: two words per pixel instead of 64
+  // values.
   const uint32_t* rbits;
+  int ps, ws;
 };
 
 // Fused 1x1 conv + multi-step LIF: a tile of 64 pixels of one sample runs all
@@ -506,12 +509,12 @@ __global__ __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(XV ? 2
         }
       }
       if (o.bits != nullptr && mine) {
-        uint32_t* ob = o.bits + (frame * hw_t + p0 + lane) * o.cwp;
+        uint32_t* ob = o.bits + frame * hw_t * o.cwp + (int64_t)(p0 + lane) * o.ps;
         const int w_0 = co0 / 32;
-        ob[w_0] = w0;
-        if (w_0 + 1 < o.cwp) ob[w_0 + 1] = w1;
+        ob[(int64_t)w_0 * o.ws] = w0;
+        if (w_0 + 1 < o.cwp) ob[(int64_t)(w_0 + 1) * o.ws] = w1;
         if (grp == groups - 1)  // the words past the last group's channels
-          for (int wd = w_0 + 2; wd < o.cwp; ++wd) ob[wd] = 0u;
+          for (int wd = w_0 + 2; wd < o.cwp; ++wd) ob[(int64_t)wd * o.ws] = 0u;
       }
       if (o.bits != nullptr && valid && grp == 0 && lane == 0 && p0 % o.chunk == 0)
         o.flags[frame * o.cpf + p0 / o.chunk] = 0u;  // spikes are binary
@@ -642,9 +645,11 @@ int launch_linear_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream
 }
 
 int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, const uint32_t* res_bits,
-                         uint32_t* out_bits, uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf,
-                         hipStream_t stream) {
-  FlatLifOut o{out_bits, out_flags, out_cwp, out_chunk, out_cpf, res_bits};
+                         uint32_t* out_bits, uint32_t* out_flags, int out_cwp, int out_planes, int out_chunk,
+                         int64_t out_cpf, hipStream_t stream) {
+  const int hw_out = a.h_out * a.w_out;
+  FlatLifOut o{out_bits, out_flags, out_cwp, out_chunk, out_cpf, res_bits, out_planes ? 1 : out_cwp,
+               out_planes ? hw_out : 1};
   if (a.chunk <= 0 || a.chunk % 64 != 0) return (int)hipErrorInvalidValue;  // one flag per 64-pixel tile
   timing_begin(K_LIF_FLAT, stream);
   int rc;

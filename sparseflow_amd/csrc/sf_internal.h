@@ -74,8 +74,8 @@ struct ConvArgs {
   int c_in, h_in, w_in, c_out, h_out, w_out, k, s, p, cwp;
   // Bitmap word w of input pixel q of a frame sits at q * bm_ps + w * bm_ws
   // words from the frame's start: (cwp, 1) for the [hw][cwp] layout of
-  // sf_prescan_pack, (1, hw_in) for word planes (kernels that load one word
-  // of 64 pixels at a time; px3 only).
+  // sf_prescan_pack, (1, hw_in) for word planes (the kernels that load one
+  // word of 64 pixels at a time: px3 and rows_kc).
   int bm_ps, bm_ws;
   int hw_in, hw_out, groups_per_frame;
   int chunk;                 // flag chunk (pixels)
@@ -129,18 +129,18 @@ int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStrea
 // Fused 1x1 s1 conv + multi-step LIF on the flat pixel-tile kernel (a: n =
 // samples, T steps, bits of the T*n input frames); x2: optional residual
 // (conv-output layout, x's dtype) added into each step's current; out_bits /
-// out_flags: optional spike map of the output in the prescan layout
-// (out_cwp words per pixel, flag chunks of out_chunk pixels, out_cpf per
-// frame); res_bits: optional binary residual as its spike map in that same
-// layout, read instead of x2.
+// out_flags: optional spike map of the output (out_cwp words per pixel,
+// pixel-major or as word planes when out_planes != 0; flag chunks of
+// out_chunk pixels, out_cpf per frame); res_bits: optional binary residual
+// as its pixel-major spike map, read instead of x2.
 int launch_conv_lif_flat(const ConvArgs& a, int in_dtype, int out_dtype, const void* x2, const uint32_t* res_bits,
-                         uint32_t* out_bits, uint32_t* out_flags, int out_cwp, int out_chunk, int64_t out_cpf,
-                         hipStream_t stream);
+                         uint32_t* out_bits, uint32_t* out_flags, int out_cwp, int out_planes, int out_chunk,
+                         int64_t out_cpf, hipStream_t stream);
 
 // Standalone multi-step LIF over T steps of n x c x hw neurons (x2: optional
-// second input summed into the current; bits: optional spike map output in
-// the prescan layout with cwp words per pixel, with its nflags chunk flags
-// cleared).
+// second input summed into the current; bits: optional spike map output
+// with cwp words per pixel, pixel-major or as word planes (planes != 0),
+// with its nflags chunk flags cleared).
 // Spike max pooling from a spike map (at most kSpikePoolMaxWords words, 256
 // channels, per pixel).
 constexpr int kSpikePoolMaxWords = 8;
@@ -148,8 +148,8 @@ int launch_spike_maxpool(const uint32_t* bits, int64_t n, int c, int h_in, int w
                          int st, int pd, int cwp, int out_dtype, void* y, uint32_t* out_bits, hipStream_t stream);
 int launch_lif_multistep(const void* x, const void* x2, int in_dtype, int T, int64_t n, int c, int64_t hw, float tau,
                          float v_th, float v_reset, int hard_reset, int decay_input, const float* v_init, void* spikes,
-                         int out_dtype, float* v_out, uint32_t* bits, int cwp, uint32_t* flags, int64_t nflags,
-                         hipStream_t stream);
+                         int out_dtype, float* v_out, uint32_t* bits, int cwp, int planes, uint32_t* flags,
+                         int64_t nflags, hipStream_t stream);
 
 // Sparse linear (row-major x [m, k], weight wt [k, c_out]): row prescan and
 // the flat lane = row Stage 2.  Bitmap words per row: ceil(k/32), rounded up

@@ -122,10 +122,13 @@ __global__ __launch_bounds__(256) void k_lif_multistep(const TIn* __restrict__ x
 // also writes the spike map word of each step (bit c & 31 of word c >> 5 of
 // pixel p of frame t*N + n), so the next sparse convolution can skip its
 // prescan.  Consecutive threads take consecutive pixels: every channel
-// plane is read and written in 256-byte runs.
+// plane is read and written in 256-byte runs.  Word w of pixel p of a frame
+// sits at p * ps + w * ws words from the frame's start: (cwp, 1) pixel-major,
+// (1, hw) as word planes.
 struct LifMap {
   int64_t n, hw;
   int c, cwp;
+  int64_t ps, ws;
 };
 
 template <typename TIn, typename TOut>
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(256) void k_lif_bits(const TIn* __restrict__ x, con
         if (j < nc && px) (sr + (int64_t)j * g.hw)[pl] = from_f32<TOut>(sp);
         word |= (fire && j < nc ? 1u : 0u) << j;
       }
-      if (px) bits[(f * g.hw + p) * g.cwp + w] = word;
+      if (px) bits[f * g.hw * g.cwp + p * g.ps + w * g.ws] = word;
     }
     if (px) {
 #pragma unroll
@@ -289,7 +292,7 @@ __global__ __launch_bounds__(256) void k_lif_bits4(const TIn* __restrict__ x, co
       }
       __syncthreads();
       const int64_t pw = p0 + threadIdx.x;
-      if (pw < g.hw) bits[(f * g.hw + pw) * g.cwp + w] = s_word[threadIdx.x];
+      if (pw < g.hw) bits[f * g.hw * g.cwp + pw * g.ps + w * g.ws] = s_word[threadIdx.x];
       __syncthreads();
     }
     if (px) {
@@ -354,8 +357,8 @@ int launch_lif_ms_t(const void* x, const void* x2, const float* v_init, void* sp
 
 int launch_lif_multistep(const void* x, const void* x2, int in_dtype, int T, int64_t n, int c, int64_t hw, float tau,
                          float v_th, float v_reset, int hard_reset, int decay_input, const float* v_init, void* spikes,
-                         int out_dtype, float* v_out, uint32_t* bits, int cwp, uint32_t* flags, int64_t nflags,
-                         hipStream_t stream) {
+                         int out_dtype, float* v_out, uint32_t* bits, int cwp, int planes, uint32_t* flags,
+                         int64_t nflags, hipStream_t stream) {
   LifRun r;
   r.m = n * c * hw;
   r.T = T;
@@ -371,6 +374,8 @@ int launch_lif_multistep(const void* x, const void* x2, int in_dtype, int T, int
   g.hw = hw;
   g.c = c;
   g.cwp = cwp;
+  g.ps = planes ? 1 : cwp;
+  g.ws = planes ? hw : 1;
 #define SF_LIF_LAUNCH(TI, TO)                                                                   \
   (bits != nullptr ? launch_lif_bits_t<TI, TO>(x, x2, v_init, spikes, v_out, bits, flags, nflags, r, g, stream) \
                    : launch_lif_ms_t<TI, TO>(x, x2, v_init, spikes, v_out, r, stream))

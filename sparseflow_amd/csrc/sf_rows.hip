@@ -120,17 +120,19 @@ __device__ __forceinline__ void kc_rows(float (&acc)[64], const KcTile& k) {
 }
 
 // Chunk c's words of the tile's halo positions (rows oh0 - 1 .. oh0 + TH of
-// the frame; rows outside it read position 0 and are never walked).
+// the frame; rows outside it read position 0 and are never walked).  Word c
+// of pixel q at q * ps + c * ws words from the frame's start: with word
+// planes (ps = 1) the 64 lanes of a load read one run.
 template <int TH, int W>
 __device__ __forceinline__ void kc_load_words(uint32_t& v0, uint32_t& v1, const uint32_t* __restrict__ fbits,
-                                              int oh0, int h, int cwp, int lane, int c) {
+                                              int oh0, int h, int ps, int ws, int lane, int c) {
   constexpr int NP = (TH + 2) * W;
   const int p0 = lane, p1 = 64 + lane;
   const int ih0 = oh0 - 1 + p0 / W, ih1 = oh0 - 1 + p1 / W;
   const bool ok0 = p0 < NP && ih0 >= 0 && ih0 < h, ok1 = p1 < NP && ih1 >= 0 && ih1 < h;
   const int64_t q0 = ok0 ? (int64_t)(oh0 - 1) * W + p0 : 0, q1 = ok1 ? (int64_t)(oh0 - 1) * W + p1 : 0;
-  v0 = fbits[q0 * cwp + c];
-  v1 = fbits[q1 * cwp + c];
+  v0 = fbits[q0 * ps + (int64_t)c * ws];
+  v1 = fbits[q1 * ps + (int64_t)c * ws];
 }
 
 template <int TH, int W>
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
     // Chunk 0's halo words; chunk c+1's are requested while chunk c is walked.
     const uint32_t* __restrict__ fbits = bits + (int64_t)frame * a.hw_in * a.cwp;
     uint32_t nw0 = 0u, nw1 = 0u;
-    if (valid) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.cwp, lane, 0);
+    if (valid) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.bm_ps, a.bm_ws, lane, 0);
     if (!resident) {
       __syncthreads();  // the previous pass is done with both buffers
       load_chunk(smem, wt, 0, krows, a.c_out, co0, wave, lane);
@@ -201,7 +203,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
       if (valid) {
         k.vw0 = nw0;
         k.vw1 = nw1;
-        if (c + 1 < nchunks) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.cwp, lane, c + 1);
+        if (c + 1 < nchunks) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.bm_ps, a.bm_ws, lane, c + 1);
         k.c0 = c * 32;
         k.wlb = smem + (c & 1) * kChunkBytes + lane * 4;
         kc_rows<TH, W, 0>(acc, k);

@@ -23,6 +23,8 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
+from .Kernels.spike_map import LayoutRequests
+
 
 class BaseNode(nn.Module):
     def __init__(self, v_threshold: float = 1.0, v_reset: Optional[float] = 0.0, detach_reset: bool = False,
@@ -80,6 +82,8 @@ class LIFNode(BaseNode):
         self.tau = float(tau)
         self.decay_input = bool(decay_input)
         self.emit_spike_map = True
+        # The layouts this neuron's spike-map consumers read fastest.
+        self.map_requests = LayoutRequests()
 
     def neuronal_charge(self, x, v):
         vr = 0.0 if self.v_reset is None else self.v_reset
@@ -98,11 +102,12 @@ class LIFNode(BaseNode):
         # [T, N, C, H, W] spikes also leave as a spike map for the next
         # sparse convolution (skips its prescan).
         want_map = self.emit_spike_map and x_seq.dim() == 5
+        layout = self.map_requests.layout
         spikes, self.v, smap = _lib.lif_multistep(x_seq, int(x_seq.shape[0]), lif, v_init=v0, x2=residual,
-                                                  spike_map=want_map)
+                                                  spike_map=want_map, map_layout=layout)
         if smap is not None:
             T, N, C, H, W = (int(v) for v in x_seq.shape)
-            spike_map.attach(spikes, T * N, C, H, W, smap[0], smap[1])
+            spike_map.attach(spikes, T * N, C, H, W, smap[0], smap[1], layout, self.map_requests)
         return spikes
 
     def single_step_forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -33,7 +33,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 
 def test_version_and_empty_error():
-    assert _lib.version() == 100
+    assert _lib.version() == 101
     assert isinstance(_lib.lib().sf_last_error(), bytes)
 
 
@@ -192,3 +192,60 @@ def test_noalloc_entry_point_refuses_oversized_bitmaps_on_the_host():
     bad = _lib.conv_desc(1, 8, 8, 8, 8, 8, 8, 5, 1, 2, 0, 0)
     assert L.sf_conv2d_forward_noalloc(ctypes.byref(bad), dummy, dummy, None, ctypes.c_float(1e-6), dummy,
                                        None) == _lib.SF_ERR_UNSUPPORTED
+
+
+def test_bitmap_layout_query_follows_the_stage2_choice():
+    P, M = _lib.SF_BITMAP_PLANES, _lib.SF_BITMAP_PIXEL_MAJOR
+
+    def q(n, ci, h, w, co, ho, wo, k, s, p):
+        return _lib.conv2d_bitmap_layout(_lib.conv_desc(n, ci, h, w, co, ho, wo, k, s, p, 0, 0))
+
+    # Pixel-tile 3x3 (layer1, layer2, the stride-2 layers) and the K-chunked
+    # row kernel (layer3 at 14x14) read word planes.
+    assert q(512, 64, 56, 56, 64, 56, 56, 3, 1, 1) == P
+    assert q(512, 128, 28, 28, 128, 28, 28, 3, 1, 1) == P
+    assert q(512, 256, 14, 14, 256, 14, 14, 3, 1, 1) == P
+    assert q(512, 512, 14, 14, 512, 7, 7, 3, 2, 1) == P
+    # The row-band kernel (32-wide frames, C_in <= 64), the matrix-core stem
+    # and the 1x1 kernels read pixel-major words.
+    assert q(32, 64, 32, 32, 64, 32, 32, 3, 1, 1) == M
+    assert q(64, 3, 32, 32, 384, 32, 32, 3, 1, 1) == M
+    assert q(512, 256, 56, 56, 64, 56, 56, 1, 1, 0) == M
+    assert q(0, 64, 56, 56, 64, 56, 56, 3, 1, 1) == P  # no frames: still the shape's choice
+    with pytest.raises(_lib.SparseFlowLibError):       # inconsistent output size
+        q(4, 64, 56, 56, 64, 9, 9, 3, 1, 1)
+    d = _lib.conv_desc(4, 64, 56, 56, 64, 9, 9, 3, 1, 1, 0, 0)
+    assert _lib.lib().sf_conv2d_bitmap_layout(ctypes.byref(d)) == -_lib.SF_ERR_INVALID
+
+
+def test_layout_entry_points_reject_unknown_layouts_before_launching():
+    L = _lib.lib()
+    d = _lib.conv_desc(2, 64, 8, 8, 64, 8, 8, 3, 1, 1, 0, 0)
+    dummy = ctypes.c_void_p(16)
+    assert L.sf_conv2d_sparse_layout(ctypes.byref(d), dummy, 7, dummy, dummy, dummy, None, dummy, None) == \
+        _lib.SF_ERR_INVALID
+    lif = _lib.LifParams(2.0, 1.0, 0.0, 1, 1)
+    assert L.sf_lif_multistep_layout(dummy, None, 0, 2, 1, 64, 64, ctypes.byref(lif), None, dummy, 0, dummy, dummy,
+                                     dummy, 5, None) == _lib.SF_ERR_INVALID
+    d1 = _lib.conv_desc(2, 64, 8, 8, 64, 8, 8, 1, 1, 0, 0, 0)
+    assert L.sf_conv1x1_lif_sparse_layout(ctypes.byref(d1), 2, dummy, dummy, dummy, dummy, None, None,
+                                          ctypes.byref(lif), None, dummy, dummy, dummy, dummy, -1, None) == \
+        _lib.SF_ERR_INVALID
+
+
+def test_layout_requests_pick_planes_only_when_every_consumer_asks():
+    from sparseflow_amd.Kernels.spike_map import PIXEL_MAJOR, PLANES, LayoutRequests
+
+    r = LayoutRequests()
+    assert r.layout == PIXEL_MAJOR                    # nobody asked yet
+    r.note("conv2", PLANES)
+    assert r.layout == PLANES
+    r.note("pool", PIXEL_MAJOR)
+    assert r.layout == PIXEL_MAJOR                    # one consumer reads pixel-major words
+    r.note("pool", PLANES)
+    assert r.layout == PLANES
+    for i in range(40):                               # bounded: old consumers drop out
+        r.note(("c", i), PLANES)
+    assert r.layout == PLANES and len(r._wants) == LayoutRequests._MAX
+    r.clear()
+    assert r.layout == PIXEL_MAJOR
