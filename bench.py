@@ -284,6 +284,12 @@ def spike_spread(x, stride, T):
     tiles = flat[:n64].reshape(-1, 64)
     tm = tiles.mean(1)
     busy = tm > 0
+    # Tiles the pixel-tile kernel hands to the matrix cores (C_in > 128): a
+    # pixel with 16 or more active (tap, channel) pairs among channels 0..31.
+    rf32 = torch.nn.functional.conv2d(x[:, :32].sum(1, keepdim=True), torch.ones(1, 1, 3, 3), stride=stride,
+                                      padding=1)[:, 0].reshape(-1)
+    hot = (rf32 >= 16).float()
+    hot = torch.nn.functional.pad(hot, (0, (-hot.numel()) % 64)).reshape(-1, 64).amax(1)
     return {
         "density": round(dens, 6),
         "frame_density_cv": round(float(pf.std() / max(pf.mean(), 1e-12)), 3),
@@ -295,6 +301,8 @@ def spike_spread(x, stride, T):
         "rf_count_p99": round(float(torch.quantile(flat[:1 << 22], 0.99)), 1),
         "rf_count_max": int(flat.max()),
         "tile_max_over_mean": round(float((tiles.max(1).values[busy] / tm[busy]).mean()), 2) if busy.any() else 0.0,
+        "dense_tiles": int(hot.sum()) if C > 128 else 0,
+        "tiles": int(hot.numel()),
     }
 
 
@@ -337,7 +345,8 @@ def live_layer_study(model, img, dev, steps, T):
             "kernels_us_iid": {k: round(v[1] * 1e3, 1) for k, v in ki.items()},
             "spread_live": live,
             "spread_iid": {k: iid[k] for k in ("frame_density_cv", "dead_channel_frac", "top10pct_channel_spike_share",
-                                               "rf_count_mean", "rf_count_p99", "rf_count_max", "tile_max_over_mean")},
+                                               "rf_count_mean", "rf_count_p99", "rf_count_max", "tile_max_over_mean",
+                                               "dense_tiles")},
         }
         log(f"[bench] live layer {name}: live {live_us:.1f} us, iid {iid_us:.1f} us; "
             f"tile max/mean live {live['tile_max_over_mean']} iid {iid['tile_max_over_mean']}")

@@ -411,7 +411,8 @@ int sf_spike_attention(const void* q, const void* k, const void* v,
  * ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows",
  * "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3", "lif_multistep",
  * "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
- * "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma", "conv_rows_fused").
+ * "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma", "conv_rows_fused",
+ * "conv_dense_mfma").
  * Returns the
  * number of launches recorded for that kernel. */
 int sf_timing_enable(int32_t enable);

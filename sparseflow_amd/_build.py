@@ -20,7 +20,7 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libsparseflow_hip.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ("sf_prescan.hip", "sf_conv.hip", "sf_rows.hip", "sf_flat.hip", "sf_px3.hip", "sf_lif.hip", "sf_bmm.hip", "sf_attn.hip", "sf_linmfma.hip", "sf_mfma_conv.hip", "sf_band.hip", "sf_rows_fused.hip", "sf_capi.hip")
+SOURCES = ("sf_prescan.hip", "sf_conv.hip", "sf_rows.hip", "sf_flat.hip", "sf_px3.hip", "sf_lif.hip", "sf_bmm.hip", "sf_attn.hip", "sf_linmfma.hip", "sf_mfma_conv.hip", "sf_band.hip", "sf_rows_fused.hip", "sf_dense_mfma.hip", "sf_capi.hip")
 
 ARCH = "gfx950"
 # Packed-FP32 VALU ops are disabled on purpose: the library's float math is

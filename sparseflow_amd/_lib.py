@@ -530,7 +530,7 @@ def spike_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: fl
 
 KERNEL_NAMES = ("prescan_pack", "prescan_tiles", "conv_gather", "conv_lif", "conv_rows", "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                 "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse", "spike_attention",
-                "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma", "conv_rows_fused")
+                "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma", "conv_rows_fused", "conv_dense_mfma")
 
 
 def timing_enable(on: bool) -> None:

@@ -256,7 +256,7 @@ const char* g_names[sf::K_COUNT] = {"prescan_pack", "prescan_tiles", "conv_gathe
                                      "conv_rows_kc", "conv_flat", "conv_px3", "conv_lif_px3",
                                      "lif_multistep", "prescan_rows", "linear_flat", "bmm_sparse",
                                      "spike_attention", "linear_mfma", "bmm_mfma", "conv_lif_flat", "conv_mfma",
-                                     "conv_rows_fused"};
+                                     "conv_rows_fused", "conv_dense_mfma"};
 
 }  // namespace
 

@@ -122,6 +122,32 @@ int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
 // (C_in * 9 <= 32, f32 input): the whole K is one dense tile.
 bool mfma_conv_applicable(const ConvArgs& a);
 int launch_conv_mfma(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+// Dense-tile branch of the streamed pixel-tile kernel (k_conv_px3s): wave-tiles
+// whose first chunk is dense go to a queue (per 64-output-channel group, the
+// tile's index in the flattened 64-pixel tiling) and are computed on the
+// matrix cores by launch_conv_dense_mfma, launched right after on the same
+// stream; its last workgroup clears the counts.  One queue slot per stream
+// (library-owned static device memory); dense_queue_for returns the
+// stream's slot, or NULL when every slot is taken (then nothing is deferred).
+constexpr int kDenseQueueSlots = 8;
+constexpr int kDenseQueueGroups = 32;   // C_out <= 2048
+constexpr int kDenseQueueCap = 4096;    // tiles per group; more are walked
+struct DenseQueue {
+  uint32_t count[kDenseQueueGroups];
+  uint32_t done;
+  uint32_t pad[31];
+  uint32_t start[kDenseQueueGroups][kDenseQueueCap];
+};
+DenseQueue* dense_queue_for(hipStream_t stream);
+int launch_conv_dense_mfma(const ConvArgs& a, DenseQueue* dq, int out_dtype, hipStream_t stream);
+// Deferral test on a wave-tile's first chunk: some pixel of it has at least
+// kDenseLaneSpikes active (tap, channel) pairs there.  The walk lasts as long
+// as the busiest pixel's count in every chunk, while the matrix cores' cost
+// is fixed (about that of a 16-round chunk walk); i.i.d. input at 1%
+// density has 2.9 per pixel on average and a tile passes with probability
+// ~6e-5, at 3% most tiles pass, and so does any tile with a hot pixel.
+constexpr int kDenseLaneSpikes = 16;
+
 // Fused conv + multi-step LIF on the pixel-tile formulation (3x3 s1; same
 // applicability as px3_applicable with stride 1).
 int launch_conv_lif_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
@@ -239,7 +265,7 @@ void conv_geometry(ConvArgs& a, bool lif);
 // Per-kernel event timing hooks used by the launchers.
 void timing_begin(int kernel_id, hipStream_t stream);
 void timing_end(int kernel_id, hipStream_t stream);
-enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_LIF_FLAT = 16, K_MFMA_CONV = 17, K_ROWS_FUSED = 18, K_COUNT = 19 };
+enum KernelId { K_PACK = 0, K_TILES = 1, K_CONV = 2, K_LIF = 3, K_ROWS = 4, K_ROWS_KC = 5, K_FLAT = 6, K_PX3 = 7, K_LIF_PX3 = 8, K_LIF_MS = 9, K_PACK_ROWS = 10, K_LINEAR = 11, K_BMM = 12, K_ATTN = 13, K_LINEAR_MFMA = 14, K_BMM_MFMA = 15, K_LIF_FLAT = 16, K_MFMA_CONV = 17, K_ROWS_FUSED = 18, K_DENSE_MFMA = 19, K_COUNT = 20 };
 
 // ---------------------------------------------------------------------------
 // Device helpers.

@@ -478,26 +478,16 @@ __device__ __forceinline__ void load_chunk_px3_nw(char* buf, const float* __rest
   }
 }
 
-// px3_load_words with the frame's start as a per-lane byte offset into one
-// buffer resource over every frame's bitmap (below 2^31 bytes).
-__device__ __forceinline__ void px3_load_words_at(uint32_t (&w)[9], __amdgpu_buffer_rsrc_t rs, uint32_t fbase,
-                                                  const ConvArgs& a, int ih0, int iw0, int c) {
-  const uint32_t cofs = (uint32_t)c * (uint32_t)a.bm_ws;
-#pragma unroll
-  for (int tp = 0; tp < 9; ++tp) {
-    const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
-    const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
-    const uint32_t off = in ? fbase + ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.bm_ps + cofs) * 4u : 0x80000000u;
-    w[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
-  }
-}
-
+// dq (nullable): the dense-tile queue.  A binary wave-tile with a pixel of
+// kDenseLaneSpikes or more spikes in the first chunk is appended to its
+// group's queue and neither walked nor stored here: the matrix-core kernel
+// launched next computes it (sf_dense_mfma.hip).
 template <typename TIn, typename TOut>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                const uint32_t* __restrict__ flags,
                                                                const TIn* __restrict__ x, const float* __restrict__ wt,
                                                                const float* __restrict__ bias_p, TOut* __restrict__ y,
-                                                               int groups, int nchunks) {
+                                                               int groups, int nchunks, DenseQueue* __restrict__ dq) {
   typedef Px3Layout<64> LY;
   extern __shared__ __align__(16) char smem[];
   __shared__ float s_seed[64];
@@ -537,7 +527,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const
     // start past the end of y.
     constexpr uint32_t B = (uint32_t)sizeof(TOut);
     const uint32_t yrange = (uint32_t)total_px * (uint32_t)a.c_out * B;
-    const uint32_t ybase =
+    uint32_t ybase =
         mine ? (((uint32_t)sample * (uint32_t)a.c_out + (uint32_t)co0) * (uint32_t)hwo + (uint32_t)q) * B : yrange;
     // This pass's first words, in flight during the first chunk's load.
     uint32_t wn[9];
@@ -545,6 +535,25 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const
     // The multiply-by-x path for the whole tile when any lane's input rows
     // hold a non-binary value.
     const bool value = __ballot(mine && rows_value_path(a, flags, sample, ih0, ih0 + 2)) != 0ull;
+    // Dense-tile branch: a binary wave-tile whose first chunk is dense is
+    // queued for the matrix cores instead of walked (its lanes then store
+    // nothing here).
+    bool walk = mine;
+    if (dq != nullptr && !value) {
+      uint32_t cnt = 0u;
+#pragma unroll
+      for (int tp = 0; tp < 9; ++tp) cnt += (uint32_t)__popc(wn[tp]);
+      if (__ballot(mine && cnt >= (uint32_t)kDenseLaneSpikes) != 0ull) {
+        uint32_t slot = 0u;
+        if (lane == 0) slot = atomicAdd(&dq->count[grp], 1u);
+        slot = __builtin_amdgcn_readfirstlane(slot);
+        if (slot < (uint32_t)kDenseQueueCap) {
+          if (lane == 0) dq->start[grp][slot] = (uint32_t)t;
+          walk = false;
+          ybase = yrange;
+        }
+      }
+    }
     __syncthreads();  // the previous pass is done with both buffers (and s_seed is written)
     {
       int ll = lane;
@@ -572,7 +581,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const
       asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(w[4]), "+v"(w[5]), "+v"(w[6]),
                    "+v"(w[7]), "+v"(w[8]));
       if (c + 1 < nchunks) px3_load_words_at(wn, rs_bits, fbase, a, ih0, iw0, c + 1);
-      if (mine) {
+      if (walk) {
         uint32_t nz = 0u;
 #pragma unroll
         for (int tp = 0; tp < 9; ++tp) nz |= (w[tp] != 0u ? 1u : 0u) << tp;
@@ -960,7 +969,7 @@ int launch_px3_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
 }
 
 template <typename TIn, typename TOut>
-int launch_px3s_to(const ConvArgs& a, hipStream_t stream) {
+int launch_px3s_to(const ConvArgs& a, hipStream_t stream, DenseQueue** dense) {
   typedef Px3Layout<64> LY;
   const int groups = (a.c_out + 63) / 64;
   const int nchunks = (a.c_in + kPx3Ch - 1) / kPx3Ch;
@@ -971,16 +980,19 @@ int launch_px3s_to(const ConvArgs& a, hipStream_t stream) {
   constexpr auto kern = k_conv_px3s<TIn, TOut>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
+  DenseQueue* dq = groups <= kDenseQueueGroups ? dense_queue_for(stream) : nullptr;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), (size_t)2 * LY::chunk_bytes, stream, a, a.bits, a.flags,
-                     static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, nchunks);
-  return (int)hipGetLastError();
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, nchunks, dq);
+  const int rc = (int)hipGetLastError();
+  if (rc == (int)hipSuccess) *dense = dq;
+  return rc;
 }
 
 template <typename TIn>
-int launch_px3s_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
-  if (out_dtype == SF_F16) return launch_px3s_to<TIn, __half>(a, stream);
-  if (out_dtype == SF_BF16) return launch_px3s_to<TIn, __hip_bfloat16>(a, stream);
-  return launch_px3s_to<TIn, float>(a, stream);
+int launch_px3s_t(const ConvArgs& a, int out_dtype, hipStream_t stream, DenseQueue** dense) {
+  if (out_dtype == SF_F16) return launch_px3s_to<TIn, __half>(a, stream, dense);
+  if (out_dtype == SF_BF16) return launch_px3s_to<TIn, __hip_bfloat16>(a, stream, dense);
+  return launch_px3s_to<TIn, float>(a, stream, dense);
 }
 
 template <int CO>
@@ -995,7 +1007,7 @@ int launch_px3_co(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t st
 // chunk streaming and its barriers at the cost of walking the spikes once
 // per slice.  (A 16-channel slice, resident up to C_in = 256, walks too
 // often: slower than streaming.)
-int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream, DenseQueue** dense) {
   // C_in <= 64: one 64-channel super-chunk, every weight row resident, 64
   // output channels; 64 < C_in <= 128: 32-channel slices of all 128 input
   // channels' rows, two super-chunks.  (One sample's output planes must be
@@ -1021,9 +1033,9 @@ int launch_px3_conv(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
   // resource each.
   if (nch > Px3Layout<32>::resident_chunks && a.n * (int64_t)a.hw_in * a.cwp * 4 < 0x7fffffffLL &&
       a.n * (int64_t)(a.c_out + 64) * a.hw_out * out_bytes < 0x7fffffffLL) {
-    if (in_dtype == SF_F16) return launch_px3s_t<__half>(a, out_dtype, stream);
-    if (in_dtype == SF_BF16) return launch_px3s_t<__hip_bfloat16>(a, out_dtype, stream);
-    return launch_px3s_t<float>(a, out_dtype, stream);
+    if (in_dtype == SF_F16) return launch_px3s_t<__half>(a, out_dtype, stream, dense);
+    if (in_dtype == SF_BF16) return launch_px3s_t<__hip_bfloat16>(a, out_dtype, stream, dense);
+    return launch_px3s_t<float>(a, out_dtype, stream, dense);
   }
   return launch_px3_co<64>(a, in_dtype, out_dtype, stream);
 }
@@ -1068,9 +1080,12 @@ bool px3_applicable(const ConvArgs& a) {
 }
 
 int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  DenseQueue* dense = nullptr;
   timing_begin(K_PX3, stream);
-  const int rc = launch_px3_conv(a, in_dtype, out_dtype, stream);
+  int rc = launch_px3_conv(a, in_dtype, out_dtype, stream, &dense);
   timing_end(K_PX3, stream);
+  // The tiles the walk queued for the matrix cores, right after it.
+  if (rc == (int)hipSuccess && dense != nullptr) rc = launch_conv_dense_mfma(a, dense, out_dtype, stream);
   return rc;
 }
 

@@ -269,6 +269,25 @@ struct BufIO<__hip_bfloat16> {
   }
 };
 
+// Bitmap word c of each of a lane's nine 3x3 input taps (stride / padding of
+// a, top-left tap at (ih0, iw0); 0 outside the frame), through one buffer
+// resource over every frame's bitmap (below 2^31 bytes) with the frame's
+// start as the per-lane byte offset fbase.  Word c of pixel q sits at
+// q * bm_ps + c * bm_ws words from the frame's start (pixel-major words or
+// word planes).  A tap outside the frame gets an offset past num_records,
+// which the hardware returns as 0.
+__device__ __forceinline__ void px3_load_words_at(uint32_t (&w)[9], __amdgpu_buffer_rsrc_t rs, uint32_t fbase,
+                                                  const ConvArgs& a, int ih0, int iw0, int c) {
+  const uint32_t cofs = (uint32_t)c * (uint32_t)a.bm_ws;
+#pragma unroll
+  for (int tp = 0; tp < 9; ++tp) {
+    const int ih = ih0 + tp / 3, iw = iw0 + tp % 3;
+    const bool in = ih >= 0 && ih < a.h_in && iw >= 0 && iw < a.w_in;
+    const uint32_t off = in ? fbase + ((uint32_t)(ih * a.w_in + iw) * (uint32_t)a.bm_ps + cofs) * 4u : 0x80000000u;
+    w[tp] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)off, 0, 0);
+  }
+}
+
 // Four consecutive 0/1 values (bits 0..3 of q) as one 16-byte (f32) or
 // 8-byte (f16 / bf16) buffer store.  The whole offset goes in the VGPR and
 // soffset is the constant 0: with an SGPR soffset the compiler adds no wait

@@ -1,0 +1,148 @@
+"""Dense-tile branch of the streamed pixel-tile kernel (C_in > 128).
+
+Wave-tiles whose first chunk is dense are queued by k_conv_px3s and computed
+on the matrix cores (k_conv_dense_mfma: implicit GEMM, spikes exact in bf16,
+W split into bf16 hi + lo, f32 accumulation).  Bar: fp32 within 1e-4 abs +
+1e-4 rel of float64 F.conv2d, fp16/bf16 outputs within 1e-2; the kernel
+pair is deterministic (repeats are bit-identical) and leaves its queue
+clear (a following call without dense tiles runs no matrix-core work and is
+still exact); inputs whose tiles are all dense, tiles that span frames,
+partial channel groups and chunks, value-path (non-binary) tiles, which are
+never deferred, and more dense tiles than the queue holds (the rest are
+walked) are covered.  Inputs mix bursts of dense frames (a time step where
+most neurons fire) with sparse ones, as a live spiking network does.
+"""
+
+import pytest
+import torch
+
+from oracle import conv as oconv
+from sparseflow_amd import _lib
+from sparseflow_amd.Kernels.conv2d import sparse_conv2d_forward
+from tests.gpu_helpers import DEV, announce, close, native_loaded
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = dict(atol=1e-4, rtol=1e-4)
+
+
+def _weights(c_out, c_in, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(c_out, c_in, 3, 3, generator=g) * (2.0 / (c_in * 9)) ** 0.5
+
+
+def _bursty(shape, dense_frames, p_dense=0.12, p_sparse=0.005, seed=0):
+    """Binary spikes: the listed frames at p_dense, the rest at p_sparse."""
+    g = torch.Generator().manual_seed(seed)
+    n = shape[0]
+    p = torch.full((n, 1, 1, 1), p_sparse)
+    p[list(dense_frames)] = p_dense
+    return (torch.rand(shape, generator=g) < p).float()
+
+
+def _run(x, w, b, stride, **kw):
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        y = sparse_conv2d_forward(x, w, b, kernel_size=3, stride=stride, padding=1, **kw)[0]
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return y, {k: c for k, (c, _) in stats.items() if c > 0}
+
+
+CASES = [
+    # (N, C_in, H, W, C_out, stride, dense frames)
+    (24, 256, 28, 28, 256, 2, range(8, 16)),       # layer3.0 conv2 shape, a burst of 8 frames
+    (24, 512, 14, 14, 512, 2, range(16, 24)),      # layer4.0 conv2 (49-pixel planes: tiles span frames)
+    (12, 200, 15, 13, 100, 1, (1, 5, 6, 7, 11)),   # partial last chunk, partial last group
+    (6, 160, 9, 31, 68, 2, (0, 1, 2, 3, 4, 5)),    # every frame dense
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_dense_tiles_match_dense_conv(case):
+    N, C, H, W, Co, s, dense = case
+    announce(f"dense tiles {case[:6]}")
+    x = _bursty((N, C, H, W), dense, seed=C + H)
+    w = _weights(Co, C, seed=Co)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(2)) * 0.1
+    xd = x.to(DEV)
+    y, kernels = _run(xd, w.to(DEV), b.to(DEV), s)
+    assert "conv_px3" in kernels and "conv_dense_mfma" in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, s, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    y2, _ = _run(xd, w.to(DEV), b.to(DEV), s)
+    assert torch.equal(y, y2)  # deterministic, and the queue was clear again
+    assert native_loaded()
+
+
+def test_row_kernel_shape_with_bursts_stays_exact():
+    N, C, H, W, Co = 16, 256, 14, 14, 256
+    announce("row-kernel shape bursty")
+    x = _bursty((N, C, H, W), range(4, 8), seed=5)
+    w = _weights(Co, C, seed=6)
+    y, kernels = _run(x.to(DEV), w.to(DEV), None, 1)
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_queue_is_clear_after_a_dense_call():
+    N, C, H, W, Co = 16, 256, 28, 28, 128
+    announce("dense then sparse")
+    w = _weights(Co, C, seed=7).to(DEV)
+    xd = _bursty((N, C, H, W), range(N), seed=8)          # all dense
+    xs = _bursty((N, C, H, W), (), seed=9)                # all sparse
+    yd, kd = _run(xd.to(DEV), w, None, 2)
+    ys, ks = _run(xs.to(DEV), w, None, 2)
+    assert "conv_dense_mfma" in kd
+    ok, err, _ = close(ys, oconv.sparse_conv2d_ref(xs, w.cpu(), None, 2, 1), **FP32_TOL)
+    assert ok, f"sparse call after a dense one: max abs err {err}"
+    ok, err, _ = close(yd, oconv.sparse_conv2d_ref(xd, w.cpu(), None, 2, 1), **FP32_TOL)
+    assert ok, f"dense call: max abs err {err}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_dense_tiles_half_precision(dtype):
+    N, C, H, W, Co = 8, 192, 14, 14, 128
+    announce(f"dense tiles {dtype}")
+    x = _bursty((N, C, H, W), (2, 3, 4), seed=10)
+    w = _weights(Co, C, seed=11)
+    b = torch.linspace(-0.3, 0.3, Co)
+    y, kernels = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), 2)
+    assert y.dtype == dtype and "conv_dense_mfma" in kernels
+    ok, err, _ = close(y, oconv.conv2d_ref(x, w, b, 2, 1), atol=1e-2, rtol=1e-2)
+    assert ok, f"max abs err {err}"
+    y32, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), 2, output_dtype=torch.float32)
+    ok, err, _ = close(y32, oconv.conv2d_ref(x, w, b, 2, 1), **FP32_TOL)
+    assert ok, f"f32 output: max abs err {err}"
+
+
+def test_value_path_tiles_are_walked_not_deferred():
+    N, C, H, W, Co = 8, 256, 14, 14, 64
+    announce("dense value tiles")
+    x = _bursty((N, C, H, W), range(N), seed=12)
+    g = torch.Generator().manual_seed(13)
+    x[3] = x[3] * torch.randn(C, H, W, generator=g)   # a non-binary frame: multiplied, never deferred
+    w = _weights(Co, C, seed=14)
+    y, kernels = _run(x.to(DEV), w.to(DEV), None, 2)
+    assert "conv_dense_mfma" in kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, 2, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_more_dense_tiles_than_the_queue_holds():
+    # 84 frames of 56 x 56 outputs = 4116 wave-tiles in one group, all dense:
+    # 4096 go to the queue, the rest are walked.  (Four output channels keep
+    # the float64 reference quick.)
+    N, C, H, W, Co = 84, 160, 56, 56, 4
+    announce("queue overflow")
+    x = _bursty((N, C, H, W), range(N), p_dense=0.06, seed=15)
+    w = _weights(Co, C, seed=16)
+    y, kernels = _run(x.to(DEV), w.to(DEV), None, 1)
+    assert "conv_dense_mfma" in kernels
+    ref = oconv.sparse_conv2d_ref(x, w, None, 1, 1)
+    ok, err, _ = close(y, ref, **FP32_TOL)
+    assert ok, f"max abs err {err}"
