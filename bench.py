@@ -38,6 +38,10 @@ WORKLOADS = {
     "resnet50_layer3_0_conv3x3_s2": (512, 256, 28, 28, 256, 3, 2, "iid", 0.01, 32),
     "resnet50_layer4_0_conv3x3_s2": (512, 512, 14, 14, 512, 3, 2, "iid", 0.01, 32),
     "config2_conv1x1": (512, 256, 56, 56, 64, 1, 1, "clustered", 0.0, 32),
+    # Time-step bursts as in the live network (one step of 16 dense): the
+    # dense-tile branch's workloads.
+    "resnet50_layer3_0_conv3x3_s2_bursty": (512, 256, 28, 28, 256, 3, 2, "bursty", 0.01, 32),
+    "resnet50_layer4_0_conv3x3_s2_bursty": (512, 512, 14, 14, 512, 3, 2, "bursty", 0.01, 32),
 }
 LIF_WORKLOAD = "config4_conv3x3_lif"  # T=8, N=64, C 128->128, 28x28, Bernoulli(0.005)
 
@@ -50,6 +54,15 @@ def make_input(shape, gen, density, dev, seed=0):
     g = torch.Generator(device=dev).manual_seed(seed)
     if gen == "iid":
         return (torch.rand(shape, generator=g, device=dev) < density).float()
+    if gen == "bursty":
+        # Frames t * 32 + n of T = 16 steps: step 11 at 10x the mean density,
+        # step 5 at 3.2x, the other fourteen at 0.2x (mean = density).
+        n = shape[0]
+        p = torch.full((n, 1, 1, 1), 0.2 * density, device=dev)
+        per = n // 16
+        p[11 * per:12 * per] = 10.0 * density
+        p[5 * per:6 * per] = 3.2 * density
+        return (torch.rand(shape, generator=g, device=dev) < p).float()
     # Clustered: 16x16 blocks active with p=0.03,
     # Bernoulli(0.3) inside active blocks.
     n, c, h, w = shape

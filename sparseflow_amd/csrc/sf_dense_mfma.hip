@@ -69,15 +69,15 @@ constexpr int kDmPair = 2;                           // queued tiles per workgro
 constexpr int kDmXcds = 8;                           // accelerator complex dies (each with its own L2)
 
 // LDS placement of (row r, 16-byte piece p): row r (64 bytes) sits at line
-// dm_row(r) = r ^ (r3 | (r3 ^ r4) << 1) (bits of r; the low two bits only,
-// so a row stays in its group of four), its piece p at p ^ ((r >> 1) & 3).
-// Then, for a 128- and a 256-byte bank period alike, the rows that one lane
-// group of a fragment read touches (16 consecutive rows, one piece) and the
-// rows that one lane group of a staging write touches (16 rows of one
-// parity, both 8-byte halves of one piece) fall in distinct 16-byte bank
-// slots: neither conflicts.
-__device__ __forceinline__ int dm_row(int r) { return r ^ (((r >> 3) & 1) | ((((r >> 3) ^ (r >> 4)) & 1) << 1)); }
-__device__ __forceinline__ int dm_piece(int r, int p) { return p ^ ((r >> 1) & 3); }
+// dm_row(r) = r ^ (r4 | r5 << 1) (bits of r; the low two bits only, so a
+// row stays in its group of four and the placement does not depend on the
+// tap), its piece p at p ^ (r2 | (r1 ^ r3) << 1).  Then, for a 128- and a
+// 256-byte bank period alike, the rows that one lane group of a fragment
+// read touches (16 consecutive rows, one piece) and those that one lane
+// group of a staging write touches (rows 4 q + j for 16 consecutive q, one
+// piece) fall in distinct 16-byte bank slots: neither conflicts.
+__device__ __forceinline__ int dm_row(int r) { return r ^ (((r >> 4) & 1) | (((r >> 5) & 1) << 1)); }
+__device__ __forceinline__ int dm_piece(int r, int p) { return p ^ (((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1)); }
 
 // Two floats to bf16 (round to nearest even) packed in one word, low half =
 // v0 (one conversion instruction for the pair).
