@@ -200,7 +200,10 @@ int sf_conv2d_forward(const sf_conv_desc* desc, const void* x, const float* wt,
  * 12.9 MB).  Every call on one GPU uses that GPU's single scratch area:
  * calls that overlap on one GPU (several streams or host threads) race;
  * calls ordered on one stream do not.  Results equal sf_conv2d_forward's bit
- * for bit (same kernels). */
+ * for bit (same kernels).  The first call on each GPU looks up the device
+ * addresses of the library's scratch and queue arrays (which may load the
+ * library's code objects on that GPU): make that first call outside graph
+ * capture; every later call on the GPU only launches kernels. */
 int sf_conv2d_forward_noalloc(const sf_conv_desc* desc, const void* x,
                               const float* wt, const float* bias,
                               float threshold, void* y, void* stream);

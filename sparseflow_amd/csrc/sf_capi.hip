@@ -701,7 +701,9 @@ int sf_conv2d_forward(const sf_conv_desc* d, const void* x, const float* wt, con
 // looked up once per GPU with hipGetSymbolAddress (with that GPU current) and
 // only that address reaches a kernel.  k_pack writes every bitmap word and
 // every flag of the frames it covers, so the previous call's contents need no
-// clearing.
+// clearing.  The first call on a GPU does these lookups (the scratch and the
+// dense-tile queue), which may load the library's code objects there; later
+// calls only launch.
 static __device__ __align__(256) uint32_t scratch[SF_NOALLOC_SCRATCH_BYTES / 4];
 
 namespace {
@@ -721,6 +723,11 @@ int scratch_of_current_device(void** out) {
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return hip_fail((int)e, "hipGetSymbolAddress(scratch)");
     if (p == nullptr) return fail(SF_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+    // The dense-tile queue of the 3x3 pixel-tile kernels is library device
+    // memory too: look it up now, with the scratch, so that no later call
+    // on this GPU does a lookup (which may load a code object).
+    e = (hipError_t)sf::dense_queue_prepare();
+    if (e != hipSuccess) return hip_fail((int)e, "dense-tile queue lookup");
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];

@@ -455,10 +455,11 @@ std::map<uintptr_t, int> g_dq_slot[kDqMaxDevices];
 
 }  // namespace
 
-DenseQueue* dense_queue_for(hipStream_t stream) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDqMaxDevices) return nullptr;
-  std::lock_guard<std::mutex> lk(g_dq_mu);
+namespace {
+
+// The queue array's device address on GPU `dev` (looked up once per GPU,
+// with it current); nullptr if the lookup fails.  Caller holds g_dq_mu.
+DenseQueue* dq_base_locked(int dev) {
   if (g_dq_base[dev] == nullptr) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(g_dense_queue)) != hipSuccess || p == nullptr) {
@@ -467,6 +468,25 @@ DenseQueue* dense_queue_for(hipStream_t stream) {
     }
     g_dq_base[dev] = static_cast<DenseQueue*>(p);
   }
+  return g_dq_base[dev];
+}
+
+}  // namespace
+
+int dense_queue_prepare() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kDqMaxDevices) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_dq_mu);
+  return dq_base_locked(dev) != nullptr ? (int)hipSuccess : (int)hipErrorInvalidSymbol;
+}
+
+DenseQueue* dense_queue_for(hipStream_t stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDqMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_dq_mu);
+  if (dq_base_locked(dev) == nullptr) return nullptr;
   auto& slots = g_dq_slot[dev];
   const uintptr_t key = reinterpret_cast<uintptr_t>(stream);
   auto it = slots.find(key);

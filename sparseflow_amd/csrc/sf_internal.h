@@ -139,6 +139,9 @@ struct DenseQueue {
   uint32_t start[kDenseQueueGroups][kDenseQueueCap];
 };
 DenseQueue* dense_queue_for(hipStream_t stream);
+// Looks up the queue array's device address on the current GPU (once; it
+// may load the code object there).  hipError_t as int.
+int dense_queue_prepare();
 int launch_conv_dense_mfma(const ConvArgs& a, DenseQueue* dq, int out_dtype, hipStream_t stream);
 // Deferral test on a wave-tile's first chunk: some pixel of it has at least
 // kDenseLaneSpikes active (tap, channel) pairs there.  The walk lasts as long

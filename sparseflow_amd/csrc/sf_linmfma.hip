@@ -11,14 +11,18 @@
 // One workgroup (4 wavefronts, 2 x 2) computes a 128-row x 128-column tile;
 // each wavefront 64 x 64 = 4 x 4 MFMA 16x16x32 bf16 tiles (64 f32
 // accumulators per lane).  K is walked in 32-wide steps: the x tile (128 x
-// 32, read once from HBM, converted to bf16 hi/lo in registers) and the W
-// tile (128 columns x 32 of the [c_out][kp] bf16 rows, from L2) are staged
-// in LDS, double-buffered with one barrier per step; the next step's loads
-// are in flight during the current step's MFMAs.  The MFMAs run
-// unconditionally: a data-dependent branch around them makes the compiler
-// copy the 64 accumulators between AGPRs and VGPRs every step, which costs
-// more than the products it would skip (an all-zero 128 x 32 slice of x is
-// vanishingly rare at these densities; the spike walk serves sparse inputs).
+// 32, converted to bf16 in registers) and the W tiles (128 columns x 32 of
+// the [c_out][kp] bf16 hi and lo rows, from L2) are staged in LDS,
+// double-buffered with one barrier per step; the next step's loads are in
+// flight during the current step's MFMAs.  The main walk computes xh @ hi^T
+// + xh @ lo^T and notes whether any staged element of x has a non-zero xl;
+// only a workgroup that saw one walks K a second time for xl @ hi^T (for
+// spikes, the transformer case, the third product is never formed).  The
+// MFMAs of a walk run unconditionally: a data-dependent branch around them
+// makes the compiler copy the 64 accumulators between AGPRs and VGPRs every
+// step, which costs more than the products it would skip (an all-zero 128 x
+// 32 slice of x is vanishingly rare at these densities; the spike walk
+// serves sparse inputs).
 // Row blocks are the slow index of the grid and workgroups are placed
 // XCD-locally, so the column blocks of one row block run together on one
 // XCD and share its x tile through that XCD's L2.
@@ -26,6 +30,8 @@
 // Replaces the reference's sparse_linear_grouped_kernel (Kernels/linear.py:
 // 360-457: fp16 tl.dot over active groups, dense tiles when all groups are
 // live) for such inputs.
+#include <type_traits>
+
 #include "sf_tile.h"
 
 namespace sf {
@@ -113,10 +119,10 @@ __device__ __forceinline__ float lm_value(float raw) {
 
 template <typename TIn, typename TOut, bool VEC>
 __global__ __launch_bounds__(256) void k_linear_mfma(LinMfmaArgs a) {
-  // Double-buffered LDS tiles (bf16 bit patterns): x hi / lo [128 rows][32],
-  // W hi / lo [128 columns][32]; 64 KB, so two workgroups fit a CU.
+  // Double-buffered LDS tiles (bf16 bit patterns): x [128 rows][32] (its hi
+  // part in the main walk, its lo part in the second), W hi / lo [128
+  // columns][32]; 48 KB.
   __shared__ __align__(16) uint16_t s_xh[2][kLmRows * kLmLda];
-  __shared__ __align__(16) uint16_t s_xl[2][kLmRows * kLmLda];
   __shared__ __align__(16) uint16_t s_wh[2][kLmCols * kLmLda];
   __shared__ __align__(16) uint16_t s_wl[2][kLmCols * kLmLda];
   const int tid = threadIdx.x;
@@ -143,16 +149,23 @@ __global__ __launch_bounds__(256) void k_linear_mfma(LinMfmaArgs a) {
   float v[16];
   int v_valid = 0;
   uint4 wh0, wh1, wl0, wl1;
-  auto load_step = [&](int step) {
+  // LO = false: the main walk (x hi, W hi and lo); LO = true: the second walk
+  // (x lo, W hi).
+  auto load_step = [&](int step, auto lo_walk) {
+    constexpr bool LO = decltype(lo_walk)::value;
     const int kb = step * kLmK;  // 16-byte units: kb / 8
     wh0 = wh_src[kb / 8];
     wh1 = wh_src[kb / 8 + 1];
-    wl0 = wl_src[kb / 8];
-    wl1 = wl_src[kb / 8 + 1];
+    if constexpr (!LO) {
+      wl0 = wl_src[kb / 8];
+      wl1 = wl_src[kb / 8 + 1];
+    }
     v_valid = lm_load_x<TIn, VEC>(X, a.m, a.k, (int)(r0 + sr), kb + 16 * sh, v);  // r0 + sr < 2^30 + 128
   };
-  auto stage = [&](int buf) {
-    uint32_t hi[8], lo[8];
+  bool inexact = false;  // some staged element of x has a non-zero lo part
+  auto stage = [&](int buf, auto lo_walk) {
+    constexpr bool LO = decltype(lo_walk)::value;
+    uint32_t hx[8];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const float t = lm_value<TIn, VEC>(v[j]);
@@ -161,23 +174,26 @@ __global__ __launch_bounds__(256) void k_linear_mfma(LinMfmaArgs a) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint16_t h0 = bf16_bits(v[2 * j]), h1 = bf16_bits(v[2 * j + 1]);
-      const uint16_t l0 = bf16_bits(v[2 * j] - bf16_value(h0)), l1 = bf16_bits(v[2 * j + 1] - bf16_value(h1));
-      hi[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-      lo[j] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+      const float r0v = v[2 * j] - bf16_value(h0), r1v = v[2 * j + 1] - bf16_value(h1);
+      if constexpr (LO) {
+        hx[j] = (uint32_t)bf16_bits(r0v) | ((uint32_t)bf16_bits(r1v) << 16);
+      } else {
+        inexact |= (r0v != 0.f) | (r1v != 0.f);
+        hx[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+      }
     }
     const int p0 = 8 * lm_piece(sr, 2 * sh), p1 = 8 * lm_piece(sr, 2 * sh + 1);  // bf16 offsets
-    uint16_t* rxh = &s_xh[buf][sr * kLmLda];
-    uint16_t* rxl = &s_xl[buf][sr * kLmLda];
+    uint16_t* rx = &s_xh[buf][sr * kLmLda];
     uint16_t* rwh = &s_wh[buf][sr * kLmLda];
-    uint16_t* rwl = &s_wl[buf][sr * kLmLda];
-    *reinterpret_cast<uint4*>(rxh + p0) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-    *reinterpret_cast<uint4*>(rxh + p1) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-    *reinterpret_cast<uint4*>(rxl + p0) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-    *reinterpret_cast<uint4*>(rxl + p1) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+    *reinterpret_cast<uint4*>(rx + p0) = make_uint4(hx[0], hx[1], hx[2], hx[3]);
+    *reinterpret_cast<uint4*>(rx + p1) = make_uint4(hx[4], hx[5], hx[6], hx[7]);
     *reinterpret_cast<uint4*>(rwh + p0) = wh0;
     *reinterpret_cast<uint4*>(rwh + p1) = wh1;
-    *reinterpret_cast<uint4*>(rwl + p0) = wl0;
-    *reinterpret_cast<uint4*>(rwl + p1) = wl1;
+    if constexpr (!LO) {
+      uint16_t* rwl = &s_wl[buf][sr * kLmLda];
+      *reinterpret_cast<uint4*>(rwl + p0) = wl0;
+      *reinterpret_cast<uint4*>(rwl + p1) = wl1;
+    }
   };
 
   f32x4 acc[4][4];
@@ -186,54 +202,60 @@ __global__ __launch_bounds__(256) void k_linear_mfma(LinMfmaArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  load_step(0);
-  stage(0);
-  __syncthreads();
-
   const int g = lane >> 4, li = lane & 15;
-  for (int step = 0; step < nsteps; ++step) {
-    const int buf = step & 1;
-    // Next step's tiles are in flight during this step's MFMAs; the staging
-    // after them is their first use.
-    if (step + 1 < nsteps) load_step(step + 1);
-    // Keep the scheduler from pulling the staging math (which waits for
-    // those loads) above the MFMAs.
-    __builtin_amdgcn_sched_barrier(0);
-    {
-      bf16x8 ah[4], al[4], bh[4], bl[4];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int r = 64 * wc + 16 * ct + li;
-        const int c = r * kLmLda + 8 * lm_piece(r, g);
-        bh[ct] = *reinterpret_cast<const bf16x8*>(&s_wh[buf][c]);
-        bl[ct] = *reinterpret_cast<const bf16x8*>(&s_wl[buf][c]);
-      }
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        const int r = 64 * wr + 16 * rt + li;
-        ah[rt] = *reinterpret_cast<const bf16x8*>(&s_xh[buf][r * kLmLda + 8 * lm_piece(r, g)]);
-        al[rt] = *reinterpret_cast<const bf16x8*>(&s_xl[buf][r * kLmLda + 8 * lm_piece(r, g)]);
-      }
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[rt], bh[ct], acc[rt][ct], 0, 0, 0);
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[rt], bl[ct], acc[rt][ct], 0, 0, 0);
-#pragma unroll
-      for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[rt], bh[ct], acc[rt][ct], 0, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (step + 1 < nsteps) stage(buf ^ 1);
+  // One walk over K: per step, x [128 x 32] times W^T [32 x 128] as the
+  // products of the staged x tile with the staged W hi (and, in the main
+  // walk, W lo) tiles.
+  auto walk = [&](auto lo_walk) {
+    constexpr bool LO = decltype(lo_walk)::value;
+    load_step(0, lo_walk);
+    stage(0, lo_walk);
     __syncthreads();
-  }
+    for (int step = 0; step < nsteps; ++step) {
+      const int buf = step & 1;
+      // Next step's tiles are in flight during this step's MFMAs; the staging
+      // after them is their first use.
+      if (step + 1 < nsteps) load_step(step + 1, lo_walk);
+      // Keep the scheduler from pulling the staging math (which waits for
+      // those loads) above the MFMAs.
+      __builtin_amdgcn_sched_barrier(0);
+      {
+        bf16x8 ax[4], bh[4], bl[4];
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const int r = 64 * wc + 16 * ct + li;
+          const int c = r * kLmLda + 8 * lm_piece(r, g);
+          bh[ct] = *reinterpret_cast<const bf16x8*>(&s_wh[buf][c]);
+          if constexpr (!LO) bl[ct] = *reinterpret_cast<const bf16x8*>(&s_wl[buf][c]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+          const int r = 64 * wr + 16 * rt + li;
+          ax[rt] = *reinterpret_cast<const bf16x8*>(&s_xh[buf][r * kLmLda + 8 * lm_piece(r, g)]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+          for (int ct = 0; ct < 4; ++ct)
+            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[rt], bh[ct], acc[rt][ct], 0, 0, 0);
+        if constexpr (!LO) {
+#pragma unroll
+          for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct)
+              acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[rt], bl[ct], acc[rt][ct], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (step + 1 < nsteps) stage(buf ^ 1, lo_walk);
+      __syncthreads();
+    }
+  };
+  walk(std::false_type{});
+  // Every staged element's lo part was zero in every thread: done (the
+  // barrier's result is the same in every wavefront, so the branch is
+  // uniform).
+  if (__syncthreads_or(inexact ? 1 : 0)) walk(std::true_type{});
 
   // Accumulator (rt, ct) element i of lane l: row 16 rt + 4 (l >> 4) + i,
   // column 16 ct + (l & 15) of the wavefront's 64 x 64 tile.

@@ -91,6 +91,28 @@ def test_value_path_inputs(kernel):
     assert ok, f"max abs err {err}"
 
 
+def test_mfma_second_walk_only_where_x_is_inexact():
+    # The matrix-core kernel walks K a second time (x's bf16 lo part times W
+    # hi) only in the 128-row blocks whose x has an element that bf16 does
+    # not hold exactly.  One such element in rows 256..383: that block is
+    # exact to the fp32 bar, every other row equals the all-spikes result
+    # bit for bit.
+    x = spikes((1024, 384), 0.1, seed=31)
+    w = _w(384, 384, seed=32)
+    b = torch.randn(384, generator=torch.Generator().manual_seed(33)) * 0.1
+    announce("linear mfma second walk")
+    y0, _ = _run(x.to(DEV), w.to(DEV), b.to(DEV), kernel="mfma")
+    x1 = x.clone()
+    x1[300, 17] = 0.3                                       # 0.3 is not a bf16 value
+    y1, _ = _run(x1.to(DEV), w.to(DEV), b.to(DEV), kernel="mfma")
+    ok, err, _ = close(y1, olin.linear_ref(x1, w, b), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    ok, err, _ = close(y0, olin.linear_ref(x, w, b), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    assert torch.equal(y1[:256], y0[:256]) and torch.equal(y1[384:], y0[384:])
+    assert not torch.equal(y1[256:384], y0[256:384])
+
+
 def test_mfma_bf16_split_keeps_fp32_accuracy():
     # Weights with full fp32 mantissas and large K: the hi + lo split keeps
     # the error far inside 1e-4 (one bf16 alone would not).

@@ -54,7 +54,32 @@ def test_noalloc_equals_workspace_entry_point_twice_second_smaller():
     announce("noalloc call 3: 1x1 s1 2x40x5x7 f32")
     _, _, _, ref3, out3 = _run(2, 40, 5, 7, 36, 1, 1, torch.float32, seed=3)
     assert torch.equal(out3, ref3)
+    # Call 4: the matrix-core stem path (f32, C_in = 3: one bitmap word per
+    # pixel, read from the scratch).
+    announce("noalloc call 4: 3x3 s1 4x3x32x32 f32 (stem)")
+    _, _, _, ref4, out4 = _run(4, 3, 32, 32, 24, 3, 1, torch.float32, seed=4)
+    assert not torch.isnan(out4).any()
+    assert torch.equal(out4, ref4)
     assert native_loaded()
+
+
+def test_noalloc_warm_call_allocates_nothing():
+    n, c, h, w, co = 8, 64, 28, 28, 64
+    announce("noalloc warm call: memory unchanged")
+    x = spikes((n, c, h, w), 0.05, seed=5).to(DEV)
+    wt = _lib.tap_major_weight((torch.randn(co, c, 3, 3, generator=torch.Generator().manual_seed(5)) * 0.1).to(DEV))
+    desc = _lib.conv_desc(n, c, h, w, co, h, w, 3, 1, 1, 0, 0)
+    y = torch.empty((n, co, h, w), device=DEV)
+    _lib.conv2d_forward_noalloc(desc, x, wt, None, 1e-6, y)  # the first call on this GPU may look up and load
+    torch.cuda.synchronize()
+    y0 = y.clone()
+    alloc, (free, total) = torch.cuda.memory_allocated(), torch.cuda.mem_get_info()
+    for _ in range(3):
+        _lib.conv2d_forward_noalloc(desc, x, wt, None, 1e-6, y)
+    torch.cuda.synchronize()
+    assert torch.cuda.memory_allocated() == alloc
+    assert torch.cuda.mem_get_info() == (free, total)
+    assert torch.equal(y, y0)
 
 
 def test_noalloc_rejects_more_than_the_scratch_before_launching():
