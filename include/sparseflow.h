@@ -359,6 +359,21 @@ int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k,
                    const float* bias, int32_t c_out, float threshold, void* y,
                    int32_t out_dtype, void* stream);
 
+/* sf_linear_mfma over sf_linear_prescan's row bitmap and flags (computed
+ * from the same x and threshold): a 128-row block whose flag words are all
+ * zero (spikes, the transformer case) takes its A operand from the bitmap
+ * (4 bytes of x per row per 32-wide K step instead of 128), a flagged block
+ * reads x; same products, same results as sf_linear_mfma to rounding
+ * (bit-identical for binary rows).  Replaces the reference's
+ * sparse_linear_grouped_kernel (Kernels/linear.py:360-457) after its
+ * group-bitmask metadata (Kernels/linear.py:110-357);
+ * m * words_per_row * 4 < 2^31. */
+int sf_linear_mfma_bits(const uint32_t* bits, const uint32_t* flags,
+                        const void* x, int32_t in_dtype, int64_t m, int32_t k,
+                        const uint16_t* w_hi, const uint16_t* w_lo, int32_t kp,
+                        const float* bias, int32_t c_out, float threshold,
+                        void* y, int32_t out_dtype, void* stream);
+
 /* ---- sparse batched matmul -------------------------------------------------- */
 
 /* c[b] = alpha * (a[b] @ B[b]) for b < batches: a [batches, m, k] contiguous and

@@ -7,12 +7,18 @@
   "walk"  sf_linear_prescan  x [m, k] -> row bitmap (+ non-binary flags)
           sf_linear_sparse   bitmap -> y [m, c_out] (lane = row walk of the
                              active elements, weight rows from LDS)
-  "mfma"  sf_linear_mfma     one pass on the matrix cores with W and x split
-                             into bf16 hi + lo parts (dense tiles)
+  "mfma"  sf_linear_mfma     the matrix cores with W split into bf16 hi + lo
+                             parts (dense tiles), x read and split in the
+                             kernel
+  "mfma_bits" sf_linear_prescan, then sf_linear_mfma_bits: the same product
+                             with the A operand of spike row blocks from the
+                             bitmap (flagged blocks read x, split the same
+                             way); the row prescan costs more than the x
+                             reads it saves unless the output is wide
 
 The walk does ~density x the MACs on the VALU; the MFMA tile path does them
 all on the matrix cores and wins once every 32-wide K slice of a 128-row tile
-is live (transformer densities, p ~ 0.1).  `kernel="auto"` takes the MFMA
+is live (transformer densities, p ~ 0.1).  `kernel="auto"` takes the "mfma"
 path for k >= 32 (the walk for narrower inputs).
 
 Weights stay fp32 and the sum is fp32 (the reference casts x and W to fp16
@@ -119,7 +125,8 @@ def sparse_linear_forward(
 ):
     """Sparse linear y = x @ weight^T + bias for x [N, C_IN].
 
-    `kernel` picks "walk", "mfma" or "auto" (see the module docstring);
+    `kernel` picks "walk", "mfma", "mfma_bits" or "auto" (see the module
+    docstring);
     `w_split` may carry the cached (hi, lo) of split_weight_bf16.
 
     `w_t` may carry a cached weight^T [C_IN, C_OUT] (f32 is used as is,
@@ -171,7 +178,8 @@ def sparse_linear_forward(
 
     x = x.contiguous()
     lib_out = out_dtype if out_dtype in (x.dtype, torch.float32) else torch.float32
-    use_mfma = kernel == "mfma" or (kernel == "auto" and C_IN >= 32)
+    use_mfma = kernel in ("mfma", "mfma_bits") or (kernel == "auto" and C_IN >= 32)
+    mfma_bits = kernel == "mfma_bits"
     wt = None
     if not use_mfma:
         if w_t is not None and tuple(w_t.shape) == (C_IN, C_OUT):
@@ -196,13 +204,17 @@ def sparse_linear_forward(
     if use_mfma:
         if w_split is None or tuple(w_split[0].shape) != (C_OUT, -(-C_IN // 32) * 32):
             w_split = split_weight_bf16(weight)
-        meta["reason"] = "linear_mfma_bf16x2"
+        meta["reason"] = "linear_mfma_bitmap" if mfma_bits else "linear_mfma_bf16x2"
         meta["launch_count"] = int(-(-N // 128) * -(-C_OUT // 128))
     if use_mfma and not need_stats:
         if return_ms:
             se, ee = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             se.record()
-        _lib.linear_mfma(x, w_split[0], w_split[1], b, y, threshold)
+        if mfma_bits:
+            bits, flags = _lib.linear_prescan(x, threshold)
+            _lib.linear_mfma_bits(bits, flags, x, w_split[0], w_split[1], b, y, threshold)
+        else:
+            _lib.linear_mfma(x, w_split[0], w_split[1], b, y, threshold)
         if return_ms:
             ee.record()
             torch.cuda.synchronize(x.device)
@@ -240,7 +252,9 @@ def sparse_linear_forward(
         if return_ms:
             se, ee = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             se.record()
-        if use_mfma:
+        if mfma_bits:
+            _lib.linear_mfma_bits(bits, flags, x, w_split[0], w_split[1], b, y, threshold)
+        elif use_mfma:
             _lib.linear_mfma(x, w_split[0], w_split[1], b, y, threshold)
         else:
             _lib.linear_sparse(bits, flags, x, wt, b, y)

@@ -73,6 +73,8 @@ EXPORTS = {
                                   _P]),
     "sf_linear_mfma": (c_int, [_P, c_int32, c_int64, c_int32, _P, _P, c_int32, _P, c_int32, c_float, _P, c_int32,
                                _P]),
+    "sf_linear_mfma_bits": (c_int, [_P, _P, _P, c_int32, c_int64, c_int32, _P, _P, c_int32, _P, c_int32, c_float, _P,
+                                    c_int32, _P]),
     "sf_bmm_supported": (c_int, [c_int32, c_int32]),
     "sf_bmm_sparse": (c_int, [_P, _P, c_int32, c_int64, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_float,
                               c_float, _P, c_int32, _P]),
@@ -477,6 +479,21 @@ def linear_mfma(x2d: torch.Tensor, w_hi: torch.Tensor, w_lo: torch.Tensor, bias:
     rc = lib().sf_linear_mfma(_ptr(x2d), dtype_code(x2d.dtype), m, k, _ptr(w_hi), _ptr(w_lo), kp, _ptr(bias), c_out,
                               float(threshold), _ptr(y), dtype_code(y.dtype), _stream(x2d.device))
     _check(rc, "sf_linear_mfma")
+    return y
+
+
+def linear_mfma_bits(bits: torch.Tensor, flags: torch.Tensor, x2d: torch.Tensor, w_hi: torch.Tensor,
+                     w_lo: torch.Tensor, bias: Optional[torch.Tensor], y: torch.Tensor,
+                     threshold: float = 1e-6) -> torch.Tensor:
+    """linear_mfma over linear_prescan's (bits, flags) of the same x and
+    threshold (sf_linear_mfma_bits): spike row blocks read the bitmap."""
+    _require_device(x2d, "x")
+    m, k = (int(v) for v in x2d.shape)
+    c_out, kp = (int(v) for v in w_hi.shape)
+    rc = lib().sf_linear_mfma_bits(_ptr(bits), _ptr(flags), _ptr(x2d), dtype_code(x2d.dtype), m, k, _ptr(w_hi),
+                                   _ptr(w_lo), kp, _ptr(bias), c_out, float(threshold), _ptr(y), dtype_code(y.dtype),
+                                   _stream(x2d.device))
+    _check(rc, "sf_linear_mfma_bits")
     return y
 
 

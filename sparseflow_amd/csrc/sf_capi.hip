@@ -544,6 +544,38 @@ int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k, const 
   return SF_OK;
 }
 
+int sf_linear_mfma_bits(const uint32_t* bits, const uint32_t* flags, const void* x, int32_t in_dtype, int64_t m,
+                        int32_t k, const uint16_t* w_hi, const uint16_t* w_lo, int32_t kp, const float* bias,
+                        int32_t c_out, float threshold, void* y, int32_t out_dtype, void* stream) {
+  if (m < 0 || k < 1 || c_out < 1) return fail(SF_ERR_INVALID, "bad linear shape");
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(SF_ERR_INVALID, "unknown dtype");
+  if (out_dtype != in_dtype && out_dtype != SF_F32)
+    return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
+  if (kp % 32 != 0 || kp < k || kp - k >= 32) return fail(SF_ERR_INVALID, "kp must be k rounded up to a multiple of 32");
+  if (kp > sf::linear_mfma_max_kp()) return fail(SF_ERR_UNSUPPORTED, "k > 8192");
+  const int cwp = sf::linear_words_per_row(k);
+  if (m * (int64_t)cwp * 4 >= (1ll << 31)) return fail(SF_ERR_UNSUPPORTED, "bitmap of 2^31 bytes or more");
+  if (m == 0) return SF_OK;
+  if (bits == nullptr || flags == nullptr || x == nullptr || w_hi == nullptr || w_lo == nullptr || y == nullptr)
+    return fail(SF_ERR_INVALID, "NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(w_hi) | reinterpret_cast<uintptr_t>(w_lo)) & 15)
+    return fail(SF_ERR_INVALID, "w_hi / w_lo must be 16-byte aligned");
+  sf::LinMfmaArgs a{};
+  a.x = x;
+  a.wh = w_hi;
+  a.wl = w_lo;
+  a.bias = bias;
+  a.y = y;
+  a.m = m;
+  a.k = k;
+  a.kp = kp;
+  a.c_out = c_out;
+  a.cutoff = sf_activity_cutoff(threshold);
+  const int rc = sf::launch_linear_bits_mfma(a, bits, flags, cwp, in_dtype, out_dtype, static_cast<hipStream_t>(stream));
+  if (rc != hipSuccess) return hip_fail(rc, "linear_bits_mfma launch");
+  return SF_OK;
+}
+
 int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k, const float* wt, const float* bias,
                       int32_t c_out, float threshold, void* workspace, size_t workspace_bytes, void* y,
                       int32_t out_dtype, void* stream) {

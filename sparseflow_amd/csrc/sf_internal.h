@@ -228,6 +228,10 @@ struct LinMfmaArgs {
 };
 int linear_mfma_max_kp();
 int launch_linear_mfma(const LinMfmaArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
+// The same product over sf_linear_prescan's row bitmap (cwp words per row)
+// and its non-binary flags (one per kLinearRowChunk rows).
+int launch_linear_bits_mfma(const LinMfmaArgs& a, const uint32_t* bits, const uint32_t* flags, int cwp, int in_dtype,
+                            int out_dtype, hipStream_t stream);
 
 // Fused spike attention core y = (q @ k^T * scale) @ v = q @ (k^T v) * scale
 // per (frame, head); element (tb, m, h, d) at tb*s_tb + m*s_m + h*s_h + d.

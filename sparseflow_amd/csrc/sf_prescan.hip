@@ -231,6 +231,59 @@ __global__ __launch_bounds__(256) void k_pack_rows(PackArgs a) {
   if (lane == 0) a.flags[chunk] = bal != 0ull ? 1u : 0u;
 }
 
+// k_pack_rows with 16-byte loads (f32 rows, k % 4 == 0, x 16-byte
+// aligned): each load covers 256 consecutive elements of a row, lane l
+// elements 4 l .. 4 l + 3; a lane's 4-bit nibble, shifted to its place and
+// OR-ed across eight lanes (three xor shuffles), is one bitmap word, stored
+// by the group's first lane.  Words past the row's last element come out
+// zero (the elements past k load as 0), up to 8 x ceil(k / 256) >= cwp.
+__global__ __launch_bounds__(256) void k_pack_rows4(PackArgs a) {
+  const int lane = lane_id();
+  const int64_t chunk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (chunk >= a.total_chunks) return;  // the kernel has no block-level barrier
+  const int64_t r0 = chunk * kLinearRowChunk;
+  const int rows = (int)min((int64_t)kLinearRowChunk, a.n - r0);
+  const int k = a.c, cwp = a.cwp;
+  const int nseg = (k + 255) / 256;
+  const int items = rows * nseg;
+  const float* __restrict__ x = static_cast<const float*>(a.x) + r0 * (int64_t)k;
+  uint32_t* __restrict__ bits = a.bits + r0 * (int64_t)cwp;
+  const float cut = a.cutoff;
+  uint32_t nb = 0u;
+  int r = 0, sg = 0;  // item i0 = r * nseg + sg
+  for (int i0 = 0; i0 < items; i0 += 8) {
+    float4 v[8];
+    int rr[8], ss[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      rr[u] = r;
+      ss[u] = sg;
+      const int kk = sg * 256 + 4 * lane;
+      v[u] = (i0 + u < items && kk < k) ? *reinterpret_cast<const float4*>(x + (int64_t)r * k + kk)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+      if (++sg == nseg) { sg = 0; ++r; }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+      uint32_t nib = 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        nib |= (fabsf(e[j]) >= cut ? 1u : 0u) << j;
+        nb |= (e[j] != 0.f && e[j] != 1.f) ? 1u : 0u;
+      }
+      uint32_t wv = nib << (4 * (lane & 7));
+      wv |= __shfl_xor(wv, 1, kWave);
+      wv |= __shfl_xor(wv, 2, kWave);
+      wv |= __shfl_xor(wv, 4, kWave);
+      const int w = 8 * ss[u] + (lane >> 3);
+      if (i0 + u < items && (lane & 7) == 0 && w < cwp) bits[(int64_t)rr[u] * cwp + w] = wv;
+    }
+  }
+  const uint64_t bal = __ballot(nb != 0u);
+  if (lane == 0) a.flags[chunk] = bal != 0ull ? 1u : 0u;
+}
+
 // One wavefront per output tile.  Requires cwp <= 64 (a power of two), so
 // lane l always reads word (l % cwp) of the pixels it visits.
 __global__ __launch_bounds__(256) void k_tiles(TilesArgs a) {
@@ -415,7 +468,12 @@ int launch_pack_rows(const PackArgs& a, int dtype, hipStream_t stream) {
     case SF_BF16:
       hipLaunchKernelGGL(k_pack_rows<__hip_bfloat16>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
       break;
-    default: hipLaunchKernelGGL(k_pack_rows<float>, dim3((unsigned)blocks), dim3(256), 0, stream, a); break;
+    default:
+      if (a.c % 4 == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0)
+        hipLaunchKernelGGL(k_pack_rows4, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL(k_pack_rows<float>, dim3((unsigned)blocks), dim3(256), 0, stream, a);
+      break;
   }
   timing_end(K_PACK_ROWS, stream);
   return (int)hipGetLastError();

@@ -46,7 +46,7 @@ CASES = [
 
 @pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("density", [0.0, 0.1, 0.5])
-@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+@pytest.mark.parametrize("kernel", ["walk", "mfma", "mfma_bits"])
 def test_linear_fp32_matches_dense(case, density, kernel):
     m, k, co = case
     announce(f"linear {kernel} {case} p={density}")
@@ -57,19 +57,29 @@ def test_linear_fp32_matches_dense(case, density, kernel):
     if kernel == "walk":
         assert "linear_flat" in kernels and "prescan_rows" in kernels, kernels
     else:
-        assert set(kernels) == {"linear_mfma"}, kernels
+        assert set(kernels) == ({"prescan_rows", "linear_mfma"} if kernel == "mfma_bits" else {"linear_mfma"}), kernels
     ok, err, _ = close(y, olin.linear_ref(x, w, b), **FP32_TOL)
     assert ok, f"max abs err {err}"
     assert native_loaded()
 
 
-@pytest.mark.parametrize("m,k", [(5, 20), (40, 64), (33, 100), (300, 384), (17, 1536)])
-def test_row_bitmap_and_flags_bit_exact(m, k):
-    announce(f"linear bitmap {m}x{k}")
+@pytest.mark.parametrize("m,k", [(5, 20), (40, 64), (33, 100), (300, 384), (17, 1536), (33, 37), (9, 258),
+                                 (64, 260)])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_row_bitmap_and_flags_bit_exact(m, k, aligned):
+    # f32 rows with k % 4 == 0 at a 16-byte aligned address take the 16-byte
+    # load kernel, the rest the per-element one: both bit-exact.
+    announce(f"linear bitmap {m}x{k} aligned={aligned}")
     x = spikes((m, k), 0.2, seed=k)
     x[m // 2, k // 3] = 2.5          # non-binary chunk
     x[0, 0] = 4e-7                   # below the threshold
-    bits, flags = _lib.linear_prescan(x.to(DEV), 1e-6)
+    if aligned:
+        xd = x.to(DEV)
+    else:  # one element past a 16-byte boundary
+        buf = torch.zeros(m * k + 1, device=DEV)
+        buf[1:] = x.reshape(-1).to(DEV)
+        xd = buf[1:].view(m, k)
+    bits, flags = _lib.linear_prescan(xd, 1e-6)
     words = olin.linear_words_per_row(k)
     got = bits[: m * words].cpu().numpy().view(np.uint32).reshape(m, words)
     assert np.array_equal(got, olin.row_bitmap(x.numpy(), 1e-6))
@@ -77,7 +87,7 @@ def test_row_bitmap_and_flags_bit_exact(m, k):
     assert np.array_equal(nb, olin.row_chunk_nonbinary(x.numpy()))
 
 
-@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+@pytest.mark.parametrize("kernel", ["walk", "mfma", "mfma_bits"])
 def test_value_path_inputs(kernel):
     g = torch.Generator().manual_seed(7)
     x = spikes((256, 384), 0.1, seed=8)
@@ -91,26 +101,46 @@ def test_value_path_inputs(kernel):
     assert ok, f"max abs err {err}"
 
 
-def test_mfma_second_walk_only_where_x_is_inexact():
-    # The matrix-core kernel walks K a second time (x's bf16 lo part times W
-    # hi) only in the 128-row blocks whose x has an element that bf16 does
-    # not hold exactly.  One such element in rows 256..383: that block is
-    # exact to the fp32 bar, every other row equals the all-spikes result
-    # bit for bit.
+@pytest.mark.parametrize("kernel", ["mfma", "mfma_bits"])
+def test_mfma_value_rows_only_where_x_is_not_binary(kernel):
+    # One element that bf16 does not hold (0.3) in row 300.  The direct
+    # kernel ("mfma") walks K a second time (x's bf16 lo part times W hi)
+    # only in that 128-row block; the bitmap kernel ("mfma_bits") reads x instead
+    # of the bitmap only in its 256-row block (the row chunk's non-binary
+    # flag).  The result is exact to the fp32 bar and every other row equals
+    # the all-spikes result bit for bit (binary rows of a value block too:
+    # their third product adds zeros).
     x = spikes((1024, 384), 0.1, seed=31)
     w = _w(384, 384, seed=32)
     b = torch.randn(384, generator=torch.Generator().manual_seed(33)) * 0.1
     announce("linear mfma second walk")
-    y0, _ = _run(x.to(DEV), w.to(DEV), b.to(DEV), kernel="mfma")
+    y0, _ = _run(x.to(DEV), w.to(DEV), b.to(DEV), kernel=kernel)
     x1 = x.clone()
     x1[300, 17] = 0.3                                       # 0.3 is not a bf16 value
-    y1, _ = _run(x1.to(DEV), w.to(DEV), b.to(DEV), kernel="mfma")
+    y1, _ = _run(x1.to(DEV), w.to(DEV), b.to(DEV), kernel=kernel)
     ok, err, _ = close(y1, olin.linear_ref(x1, w, b), **FP32_TOL)
     assert ok, f"max abs err {err}"
     ok, err, _ = close(y0, olin.linear_ref(x, w, b), **FP32_TOL)
     assert ok, f"max abs err {err}"
-    assert torch.equal(y1[:256], y0[:256]) and torch.equal(y1[384:], y0[384:])
-    assert not torch.equal(y1[256:384], y0[256:384])
+    assert torch.equal(y1[:300], y0[:300]) and torch.equal(y1[301:], y0[301:])
+    assert not torch.equal(y1[300], y0[300])
+
+
+@pytest.mark.parametrize("case", [(1000, 384, 384), (4096, 1536, 384), (777, 200, 1540)])
+def test_mfma_bitmap_and_direct_kernels_agree_on_spikes(case):
+    # Both accumulate, per 32-wide K step, x_hi @ W_hi then x_hi @ W_lo into
+    # the same 16 x 16 tiles: on binary x they agree bit for bit.
+    m, k, co = case
+    announce(f"linear mfma bitmap vs direct {case}")
+    x = spikes((m, k), 0.1, seed=m + k).to(DEV)
+    w = _w(co, k, seed=co).to(DEV)
+    b = (torch.randn(co, generator=torch.Generator().manual_seed(34)) * 0.1).to(DEV)
+    yb, kb = _run(x, w, b, kernel="mfma_bits")
+    yx, kx = _run(x, w, b, kernel="mfma")
+    assert "prescan_rows" in kb and "prescan_rows" not in kx
+    assert torch.equal(yb, yx)
+    ok, err, _ = close(yb, olin.linear_ref(x.cpu(), w.cpu(), b.cpu()), **FP32_TOL)
+    assert ok, f"max abs err {err}"
 
 
 def test_mfma_bf16_split_keeps_fp32_accuracy():
@@ -127,7 +157,7 @@ def test_mfma_bf16_split_keeps_fp32_accuracy():
     assert err < 2e-5
 
 
-@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+@pytest.mark.parametrize("kernel", ["walk", "mfma", "mfma_bits"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_linear_half(dtype, kernel):
     x = spikes((512, 384), 0.1, seed=10)
@@ -145,7 +175,7 @@ def test_linear_half(dtype, kernel):
     assert ok, f"max abs err {err}"
 
 
-@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+@pytest.mark.parametrize("kernel", ["walk", "mfma", "mfma_bits"])
 def test_linear_deterministic_and_stats_path(kernel):
     x = spikes((2048, 384), 0.05, seed=12).to(DEV)
     w = _w(384, 384, seed=13).to(DEV)
@@ -195,7 +225,7 @@ def _random_linear_cases(n, seed):
 
 
 @pytest.mark.parametrize("case", _random_linear_cases(20, 909))
-@pytest.mark.parametrize("kernel", ["walk", "mfma"])
+@pytest.mark.parametrize("kernel", ["walk", "mfma", "mfma_bits"])
 def test_linear_random_shapes(case, kernel):
     # Random (m, k, c_out): ragged row and column blocks, grids of every size
     # (the matrix-core kernel's XCD-local placement is a bijection for any
