@@ -353,7 +353,8 @@ int sf_linear_forward(const void* x, int32_t in_dtype, int64_t m, int32_t k,
  * in the kernel (exact for spikes and small integers; ~16 bits otherwise);
  * elements with f16(|x|) <= f16(threshold) count as zero.  Every product is
  * computed (dense tiles, the reference's all-groups-active case).  No
- * prescan, no workspace.  k <= 8192. */
+ * prescan, no workspace.  k <= 8192; c_out a multiple of 4 (the output is
+ * stored as 16-byte row pieces). */
 int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k,
                    const uint16_t* w_hi, const uint16_t* w_lo, int32_t kp,
                    const float* bias, int32_t c_out, float threshold, void* y,
@@ -367,7 +368,7 @@ int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k,
  * (bit-identical for binary rows).  Replaces the reference's
  * sparse_linear_grouped_kernel (Kernels/linear.py:360-457) after its
  * group-bitmask metadata (Kernels/linear.py:110-357);
- * m * words_per_row * 4 < 2^31. */
+ * m * words_per_row * 4 < 2^31; c_out a multiple of 4. */
 int sf_linear_mfma_bits(const uint32_t* bits, const uint32_t* flags,
                         const void* x, int32_t in_dtype, int64_t m, int32_t k,
                         const uint16_t* w_hi, const uint16_t* w_lo, int32_t kp,

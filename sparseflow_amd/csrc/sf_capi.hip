@@ -523,6 +523,7 @@ int sf_linear_mfma(const void* x, int32_t in_dtype, int64_t m, int32_t k, const 
     return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
   if (kp % 32 != 0 || kp < k || kp - k >= 32) return fail(SF_ERR_INVALID, "kp must be k rounded up to a multiple of 32");
   if (kp > sf::linear_mfma_max_kp()) return fail(SF_ERR_UNSUPPORTED, "k > 8192");
+  if (c_out % 4 != 0) return fail(SF_ERR_UNSUPPORTED, "c_out must be a multiple of 4");
   if (m >= (1ll << 30)) return fail(SF_ERR_UNSUPPORTED, "m >= 2^30 rows");
   if (m == 0) return SF_OK;
   if (x == nullptr || w_hi == nullptr || w_lo == nullptr || y == nullptr) return fail(SF_ERR_INVALID, "NULL pointer");
@@ -553,6 +554,7 @@ int sf_linear_mfma_bits(const uint32_t* bits, const uint32_t* flags, const void*
     return fail(SF_ERR_UNSUPPORTED, "out_dtype must equal in_dtype or be f32");
   if (kp % 32 != 0 || kp < k || kp - k >= 32) return fail(SF_ERR_INVALID, "kp must be k rounded up to a multiple of 32");
   if (kp > sf::linear_mfma_max_kp()) return fail(SF_ERR_UNSUPPORTED, "k > 8192");
+  if (c_out % 4 != 0) return fail(SF_ERR_UNSUPPORTED, "c_out must be a multiple of 4");
   const int cwp = sf::linear_words_per_row(k);
   if (m * (int64_t)cwp * 4 >= (1ll << 31)) return fail(SF_ERR_UNSUPPORTED, "bitmap of 2^31 bytes or more");
   if (m == 0) return SF_OK;

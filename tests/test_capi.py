@@ -145,6 +145,11 @@ def test_linear_bmm_attention_sizes_and_validation():
     assert L.sf_linear_mfma_bits(p, p, p, 0, 8, 9000, p, p, 9024, None, 8, 1e-6, p, 0, None) == _lib.SF_ERR_UNSUPPORTED
     assert L.sf_linear_mfma_bits(None, p, p, 0, 8, 40, p, p, 64, None, 8, 1e-6, p, 0, None) == _lib.SF_ERR_INVALID
     assert L.sf_linear_mfma_bits(p, p, p, 0, 0, 40, p, p, 64, None, 8, 1e-6, p, 0, None) == _lib.SF_OK
+    # The output leaves as 16-byte row pieces: c_out must be a multiple of 4
+    # (rejected before any launch).
+    for c_out in (1, 130):
+        assert L.sf_linear_mfma(p, 0, 8, 40, p, p, 64, None, c_out, 1e-6, p, 0, None) == _lib.SF_ERR_UNSUPPORTED
+        assert L.sf_linear_mfma_bits(p, p, p, 0, 8, 40, p, p, 64, None, c_out, 1e-6, p, 0, None) == _lib.SF_ERR_UNSUPPORTED
     # Batched matmul: B's 64-column block of k rows must fit 64 KB of LDS.
     assert L.sf_bmm_supported(252, 10) and not L.sf_bmm_supported(253, 10)
     assert L.sf_bmm_sparse(p, p, 0, 2, 4, 300, 8, 0, 1, 300, 1e-6, 1.0, p, 0, None) == _lib.SF_ERR_UNSUPPORTED
