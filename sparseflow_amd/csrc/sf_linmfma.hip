@@ -304,32 +304,48 @@ __global__ __launch_bounds__(256) void k_linear_mfma(LinMfmaArgs a) {
 // ---- the same product over the prescan's row bitmap --------------------
 //
 // For spike inputs the x tile is one bit per element: a lane's A fragment
-// (8 consecutive k of one row) is one byte of that row's bitmap word, turned
-// into bf16 0 / 1 values by a 16-entry nibble table, so x costs 4 bytes per
-// row per 32-wide K step instead of 128 (f32) and needs no staging.  One
-// workgroup of 8 wavefronts computes a 256-row x 128-column tile (each
-// wavefront 64 x 64 as above); per step only the W tiles (bf16 hi and lo,
-// 16 KB) are staged, with direct global->LDS loads two steps ahead into
-// three LDS buffers, and each lane's bitmap words two steps ahead in
-// registers.  Row blocks whose non-binary flag is set (a value other than 0
-// and 1 in some row) read their x tiles instead: A fragments from x split
-// into bf16 hi + lo, three products per step (the exactness of the direct
+// (8 consecutive k of one row) is one byte of that row's bitmap word, its
+// bits turned into bf16 0 / 1 values on the VALU, so x costs 4 bytes per row
+// per 32-wide K step instead of 128 (f32) and needs no staging.  A
+// workgroup of 4 wavefronts computes one 256 x 128 tile, each wavefront
+// 128 x 64 (8 x 4 MFMA tiles: a step's 8 W fragment reads serve 64
+// products); per step the W tiles (bf16 hi and lo, 16 KB) and the rows'
+// bitmap words (1 KB) go from global memory straight into a ring of three
+// LDS buffers, requested two steps ahead and waited for by count.
+// The barrier that ends a step waits for no load (in-kernel timestamps of a
+// __syncthreads() version showed every step waiting for all of them), and
+// 66.5 KB of LDS let two workgroups share a CU: their barriers are
+// independent, so one's fragment reads and waits overlap the other's
+// MFMAs, and a finished workgroup's stores drain while the next one on the
+// CU starts (a persistent version with one 8-wavefront workgroup per CU
+// stored every tile in lockstep on all CUs, ~6 us a round with the matrix
+// cores idle).  Row blocks whose non-binary flag is set (a value other than 0 and
+// 1 in some row) read their x tiles instead: A fragments from x split into
+// bf16 hi + lo, three products per step (the exactness of the direct
 // kernel).
-constexpr int kLbRows = 256;    // rows per workgroup tile
-constexpr int kLbWaves = 8;
-constexpr int kLbBufs = 3;      // W stage buffers
+// Barrier for LDS hand-offs: this wavefront's LDS accesses are complete
+// before it, and the compiler moves no memory access across it.  Unlike
+// __syncthreads() (whose release fence waits for every outstanding load,
+// the direct LDS loads included) it leaves the loads of later steps in
+// flight; their consumers wait for them by count.
+__device__ __forceinline__ void ws_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// W tiles of step s (both parts) into LDS buffer b with direct loads: 1 KB
-// blocks, wavefront w loading blocks 2 w and 2 w + 1 (blocks 0..7 the hi part,
-// 8..15 the lo part); LDS position q of a part holds row q >> 2, stored piece
-// q & 3, i.e. logical piece (q & 3) ^ ((row >> 1) & 3) (lm_piece is its own
-// inverse).  Rows past c_out load row 0 (never stored).
+constexpr int kLbRows = 256;    // rows per workgroup tile
+constexpr int kLbWaves = 4;
+constexpr int kLbRT = 8;        // 16-row MFMA tiles per wavefront (128 rows)
+constexpr int kLbBufs = 3;      // stage buffers (W tiles and words of one 32-wide K step)
+
+// W tiles of step s (both parts) into LDS buffers (sh, sl) with direct
+// loads: 1 KB blocks, wavefront w loading blocks 4 w .. 4 w + 3 (blocks 0..7
+// the hi part, 8..15 the lo part); LDS position q of a part holds row q >> 2,
+// stored piece q & 3, i.e. logical piece lm_piece(row, q & 3) (lm_piece is
+// its own inverse).  Rows past c_out load row 0 (never stored).
 __device__ __forceinline__ void lb_load_w(uint16_t* __restrict__ sh, uint16_t* __restrict__ sl,
                                           const uint16_t* __restrict__ wh, const uint16_t* __restrict__ wl, int kp,
                                           int c0, int c_out, int s, int wave, int lane) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int u = 2 * wave + j;
+  for (int j = 0; j < 16 / kLbWaves; ++j) {
+    const int u = (16 / kLbWaves) * wave + j;
     const int q = (u & 7) * 64 + lane;
     const int r = q >> 2;
     const int p = lm_piece(r, q & 3);
@@ -339,17 +355,26 @@ __device__ __forceinline__ void lb_load_w(uint16_t* __restrict__ sh, uint16_t* _
     __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)dst, 16, 0, 0);
   }
 }
+constexpr int kLbLoads = 16 / kLbWaves + 1;  // direct loads per wavefront and step (W blocks, words)
 
-// A wavefront's 64 x 64 tile as rows of 16-byte pieces (lm_store_tile's
-// staging) through buffer stores: every lane issues exactly 16 stores (rows
-// past m and columns past c_out fall outside the buffer range and are
-// dropped), so a following wait for loads issued before them can name its
-// count.  The whole offset rides in the VGPR, soffset stays 0 (with an SGPR
-// soffset the compiler adds no wait state between a 16-byte store and a
-// VALU write of its data registers, and on gfx950 the last lanes of each
-// 16-lane group then store the overwritten value).
-template <typename TOut>
-__device__ __forceinline__ void lb_store_tile(const f32x4 (&acc)[4][4], float* __restrict__ stile,
+// Eight spikes (bits 0..7 of byte) as bf16 0 / 1 values, element i = bit i.
+__device__ __forceinline__ bf16x8 spike_bf16x8(uint32_t byte) {
+  uint32_t p[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    p[j] = (((byte >> (2 * j)) & 1u) * 0x3F80u) | (((byte >> (2 * j + 1)) & 1u) * 0x3F800000u);
+  return __builtin_bit_cast(bf16x8, make_uint4(p[0], p[1], p[2], p[3]));
+}
+
+// A wavefront's (16 RT) x 64 tile as rows of 16-byte pieces (lm_store_tile's
+// staging) through buffer stores: rows past m and columns past c_out fall
+// outside the buffer range and are dropped.  The whole offset rides in the
+// VGPR, soffset stays 0 (with an SGPR soffset the compiler adds no wait
+// state between a 16-byte store and a VALU write of its data registers, and
+// on gfx950 the last lanes of each 16-lane group then store the overwritten
+// value).
+template <int RT, typename TOut>
+__device__ __forceinline__ void lb_store_tile(const f32x4 (&acc)[RT][4], float* __restrict__ stile,
                                               const float* __restrict__ bias, __amdgpu_buffer_rsrc_t ry, int64_t m,
                                               int c_out, int64_t r_0, int c_0, int lane) {
   constexpr int kS = 68;
@@ -364,7 +389,7 @@ __device__ __forceinline__ void lb_store_tile(const f32x4 (&acc)[4][4], float* _
   const int col = c_0 + cq;
   constexpr uint32_t B = (uint32_t)sizeof(TOut);
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -390,55 +415,41 @@ __device__ __forceinline__ void lb_store_tile(const f32x4 (&acc)[4][4], float* _
   }
 }
 
-// Persistent: workgroup i takes tiles i, i + grid, ... (the grid a multiple
-// of 8, so a tile runs on XCD tile % 8 and xcd_range_block keeps a row
-// block's column tiles on one XCD).  The next tile's first W tiles and
-// bitmap words are requested before this tile's output is stored, so the
-// stores drain while the next tile starts.
+// One workgroup per 256 x 128 tile (placed XCD-locally: the column blocks
+// of a row block run on one XCD and share its rows' words through L2).
 template <typename TIn, typename TOut>
-__global__ __launch_bounds__(64 * kLbWaves) void k_linear_bits_mfma(LinMfmaArgs a, const uint32_t* __restrict__ bits,
+__global__ __launch_bounds__(64 * kLbWaves, 2) void k_linear_bits_mfma(LinMfmaArgs a, const uint32_t* __restrict__ bits,
                                                                     const uint32_t* __restrict__ flags, int cwp) {
-  // W hi tiles (buffers 0..2), then W lo tiles; the output staging (16 rows
-  // of 68 floats per wavefront) apart, so that the next tile's loads may
-  // land while this one's output is staged.
-  __shared__ __align__(16) uint16_t s_wbuf[2 * kLbBufs * kLmCols * kLmLda];
+  __shared__ __align__(16) uint16_t s_wh[kLbBufs][kLmCols * kLmLda];
+  __shared__ __align__(16) uint16_t s_wl[kLbBufs][kLmCols * kLmLda];
+  __shared__ __align__(16) uint32_t s_words[kLbBufs][kLbRows];  // bitmap word of each row, per step
   __shared__ __align__(16) float s_out[kLbWaves * 16 * 68];
-  __shared__ __align__(16) uint2 s_tab[16];
-  uint16_t (*s_wh)[kLmCols * kLmLda] = reinterpret_cast<uint16_t (*)[kLmCols * kLmLda]>(&s_wbuf[0]);
-  uint16_t (*s_wl)[kLmCols * kLmLda] = reinterpret_cast<uint16_t (*)[kLmCols * kLmLda]>(&s_wbuf[kLbBufs * kLmCols * kLmLda]);
-  const int tid = threadIdx.x;
   const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wr = wave >> 1, wc = wave & 1;
   const int g = lane >> 4, li = lane & 15;
   const int ncb = (a.c_out + kLmCols - 1) / kLmCols;
-  const int64_t ntiles = ((a.m + kLbRows - 1) / kLbRows) * ncb;
   const int nsteps = a.kp / kLmK;
   const int64_t nchunks = (a.m + kLinearRowChunk - 1) / kLinearRowChunk;
-  if (tid < 16) {
-    const uint32_t b = (uint32_t)tid;
-    s_tab[tid] = make_uint2(((b & 1u) ? 0x3F80u : 0u) | ((b & 2u) ? 0x3F800000u : 0u),
-                            ((b & 4u) ? 0x3F80u : 0u) | ((b & 8u) ? 0x3F800000u : 0u));
-  }
-  const auto rs_b = buf_rsrc(bits, (uint32_t)((uint64_t)a.m * (uint64_t)cwp * 4u));
-  const auto rs_y = buf_rsrc(a.y, (uint32_t)((uint64_t)a.m * (uint64_t)a.c_out * sizeof(TOut)));
-  float* stile = &s_out[wave * 16 * 68];
+  const int bid = xcd_range_block((int)blockIdx.x, (int)gridDim.x);
+  const int64_t rb = bid / ncb;
+  const int64_t r0 = rb * kLbRows;
+  const int c0 = (int)(bid - rb * ncb) * kLmCols;
   const TIn* __restrict__ X = static_cast<const TIn*>(a.x);
 
-  int64_t r0 = 0;
-  int c0 = 0;
-  uint32_t rowoff[4];
-  auto place = [&](int64_t tile) {
-    const int bid = xcd_range_block((int)tile, (int)ntiles);
-    const int64_t rb = bid / ncb;
-    r0 = rb * kLbRows;
-    c0 = (int)(bid - rb * ncb) * kLmCols;
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) rowoff[rt] = (uint32_t)(r0 + 64 * wr + 16 * rt + li) * (uint32_t)cwp * 4u;
-  };
-  auto load_words = [&](uint32_t (&w)[4], int s) {
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) w[rt] = __builtin_amdgcn_raw_buffer_load_b32(rs_b, (int)(rowoff[rt] + 4u * s), 0, 0);
+  // Step t's bitmap words for the tile's 256 rows (wavefront w: LDS
+  // positions 64 w .. 64 w + 63, one word per lane).  Position q holds tile
+  // row 128 (q >> 7) + 16 (q & 7) + ((q >> 3) & 15): the words of a lane's
+  // eight row tiles (lane li of wavefront row wr: rows 128 wr + 16 rt + li)
+  // are consecutive, two 16-byte reads.  Rows past m load row 0's word:
+  // their outputs are never stored.
+  auto load_step = [&](int t) {
+    const int b = t % kLbBufs;
+    lb_load_w(s_wh[b], s_wl[b], a.wh, a.wl, a.kp, c0, a.c_out, t, wave, lane);
+    const int q = 64 * wave + lane;
+    const int64_t row = r0 + 128 * (q >> 7) + 16 * (q & 7) + ((q >> 3) & 15);
+    const uint32_t* src = bits + (row < a.m ? row : 0) * (int64_t)cwp + t;
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)&s_words[b][64 * wave], 4, 0, 0);
   };
   auto bfrags = [&](int b, bf16x8 (&bh)[4], bf16x8 (&bl)[4]) {
 #pragma unroll
@@ -449,128 +460,112 @@ __global__ __launch_bounds__(64 * kLbWaves) void k_linear_bits_mfma(LinMfmaArgs 
       bl[ct] = *reinterpret_cast<const bf16x8*>(&s_wl[b][c]);
     }
   };
-  // A tile's first loads: W tiles of steps 0 and 1 (2 + 2 per lane) and the
-  // words of steps 0 and 1 (4 + 4).
-  uint32_t wa[4], wb[4];
-  auto first_loads = [&]() {
-    lb_load_w(s_wh[0], s_wl[0], a.wh, a.wl, a.kp, c0, a.c_out, 0, wave, lane);
-    if (nsteps > 1) lb_load_w(s_wh[1], s_wl[1], a.wh, a.wl, a.kp, c0, a.c_out, 1, wave, lane);
-    load_words(wa, 0);
-    if (nsteps > 1) load_words(wb, 1);
-  };
+  // Every global load of the spike path is a direct LDS load, waited for by
+  // count (the compiler would wait for all of them before the first use of
+  // any register load): steps 0 and 1 first, step 0's are waited for.
+  load_step(0);
+  if (nsteps > 1) load_step(1);
+  if (nsteps > 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLbLoads) : "memory");
+  else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // The row block's non-binary flags (one per 16 rows, read by every
+  // wavefront with uniform loads) decide its A operand.
+  uint32_t fl = 0u;
+  const int64_t ch0 = r0 / kLinearRowChunk;
+#pragma unroll
+  for (int i = 0; i < kLbRows / kLinearRowChunk; ++i)
+    if (ch0 + i < nchunks) fl |= flags[ch0 + i];
+  const bool value = fl != 0u;
+  ws_barrier();  // step 0's tiles of every wavefront
 
-  int64_t tile = blockIdx.x;
-  if (tile < ntiles) {
-    place(tile);
-    first_loads();
-  }
-  bool first = true;
-  for (; tile < ntiles; tile += gridDim.x) {
-    // The first loads of this tile have landed (the previous tile's 16
-    // stores per lane were issued after them); the barrier publishes the W
-    // tiles (and, on the first tile, the table).  The row block's
-    // non-binary flags (one per 16 rows) decide its A operand.
-    if (first) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    else __builtin_amdgcn_s_waitcnt(0x4F70);        // vmcnt(16)
-    first = false;
-    const int64_t ch = r0 / kLinearRowChunk + tid;
-    const bool value = __syncthreads_or(tid < kLbRows / kLinearRowChunk && ch < nchunks && flags[ch] != 0u) != 0;
-    f32x4 acc[4][4];
+  f32x4 acc[kLbRT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < kLbRT; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // Before the barrier that ends step s: the W tiles of step s + 1 have
-    // landed (the only loads issued after them are those of step s + 2, at
-    // most 2 + 4 per lane, and the words of step s + 1, 4).
-    auto wait_next_w = [&](int s) {
-      if (s + 2 < nsteps) __builtin_amdgcn_s_waitcnt(0x0F7A);  // vmcnt(10)
-      else __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0)
-    };
-    if (!value) {
-      auto step = [&](int s, uint32_t (&w)[4]) {
-        if (s + 2 < nsteps)
-          lb_load_w(s_wh[(s + 2) % kLbBufs], s_wl[(s + 2) % kLbBufs], a.wh, a.wl, a.kp, c0, a.c_out, s + 2, wave, lane);
-        bf16x8 af[4];
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (!value) {
+    for (int s = 0; s < nsteps; ++s) {
+      const int b = s % kLbBufs;
+      // A fragments: byte g of each row tile's word, its 8 bits turned into
+      // bf16 0 / 1 on the VALU; B fragments from the W tiles.
+      const uint4 w0 = *reinterpret_cast<const uint4*>(&s_words[b][8 * (16 * wr + li)]);
+      const uint4 w1 = *reinterpret_cast<const uint4*>(&s_words[b][8 * (16 * wr + li) + 4]);
+      const uint32_t wd[kLbRT] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+      bf16x8 af[kLbRT];
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-          const uint32_t byte = __builtin_amdgcn_ubfe(w[rt], 8 * g, 8);
-          const uint2 lo = s_tab[byte & 15u], hi = s_tab[byte >> 4];
-          af[rt] = __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-        }
-        if (s + 2 < nsteps) load_words(w, s + 2);
-        bf16x8 bh[4], bl[4];
-        bfrags(s % kLbBufs, bh, bl);
+      for (int rt = 0; rt < kLbRT; ++rt) af[rt] = spike_bf16x8(__builtin_amdgcn_ubfe(wd[rt], 8 * g, 8));
+      bf16x8 bh[4], bl[4];
+      bfrags(b, bh, bl);
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
+      for (int rt = 0; rt < kLbRT; ++rt)
 #pragma unroll
-          for (int ct = 0; ct < 4; ++ct)
-            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rt], bh[ct], acc[rt][ct], 0, 0, 0);
+        for (int ct = 0; ct < 4; ++ct)
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rt], bh[ct], acc[rt][ct], 0, 0, 0);
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
+      for (int rt = 0; rt < kLbRT; ++rt)
 #pragma unroll
-          for (int ct = 0; ct < 4; ++ct)
-            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rt], bl[ct], acc[rt][ct], 0, 0, 0);
-        wait_next_w(s);
-        __syncthreads();
-      };
-      for (int s = 0; s < nsteps; s += 2) {
-        step(s, wa);
-        if (s + 1 < nsteps) step(s + 1, wb);
+        for (int ct = 0; ct < 4; ++ct)
+          acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rt], bl[ct], acc[rt][ct], 0, 0, 0);
+      // Step s + 2's loads, behind the MFMAs (its buffer was last read by
+      // step s - 1, before the previous barrier); then step s + 1's have
+      // landed (only the ones just issued may still be in flight).
+      if (s + 2 < nsteps) {
+        load_step(s + 2);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kLbLoads) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
-    } else {
-      // x tiles: lane (li, g) reads k = 32 s + 8 g .. + 7 of its rows; past
-      // k and past m the elements are 0; |x| < cutoff counts as 0.
-      for (int s = 0; s < nsteps; ++s) {
-        if (s + 2 < nsteps)
-          lb_load_w(s_wh[(s + 2) % kLbBufs], s_wl[(s + 2) % kLbBufs], a.wh, a.wl, a.kp, c0, a.c_out, s + 2, wave, lane);
-        bf16x8 ah[4], al[4];
+      ws_barrier();
+    }
+  } else {
+    // x tiles: lane (li, g) reads k = 32 s + 8 g .. + 7 of its rows; past k
+    // and past m the elements are 0; |x| < cutoff counts as 0.  The eight
+    // row tiles in two halves (registers).
+    for (int s = 0; s < nsteps; ++s) {
+      if (s + 2 < nsteps) load_step(s + 2);  // its buffer was last read by step s - 1
+      bf16x8 bh[4], bl[4];
+      bfrags(s % kLbBufs, bh, bl);
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-          const int64_t row = r0 + 64 * wr + 16 * rt + li;
-          const int kk0 = 32 * s + 8 * g;
-          uint32_t hx[4], lx[4];
+      for (int half = 0; half < 2; ++half) {
+      bf16x8 ah[4], al[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float v2[2];
+      for (int rt = 0; rt < 4; ++rt) {
+        const int64_t row = r0 + 128 * wr + 16 * (4 * half + rt) + li;
+        const int kk0 = 32 * s + 8 * g;
+        uint32_t hx[4], lx[4];
 #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-              const int kk = kk0 + 2 * j + e;
-              const float t = (row < a.m && kk < a.k) ? to_f32<TIn>(X[row * a.k + kk]) : 0.f;
-              v2[e] = fabsf(t) >= a.cutoff ? t : 0.f;
-            }
-            const uint16_t h0 = bf16_bits(v2[0]), h1 = bf16_bits(v2[1]);
-            hx[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
-            lx[j] = (uint32_t)bf16_bits(v2[0] - bf16_value(h0)) | ((uint32_t)bf16_bits(v2[1] - bf16_value(h1)) << 16);
+        for (int j = 0; j < 4; ++j) {
+          float v2[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const int kk = kk0 + 2 * j + e;
+            const float t = (row < a.m && kk < a.k) ? to_f32<TIn>(X[row * a.k + kk]) : 0.f;
+            v2[e] = fabsf(t) >= a.cutoff ? t : 0.f;
           }
-          ah[rt] = __builtin_bit_cast(bf16x8, make_uint4(hx[0], hx[1], hx[2], hx[3]));
-          al[rt] = __builtin_bit_cast(bf16x8, make_uint4(lx[0], lx[1], lx[2], lx[3]));
+          const uint16_t h0 = bf16_bits(v2[0]), h1 = bf16_bits(v2[1]);
+          hx[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+          lx[j] = (uint32_t)bf16_bits(v2[0] - bf16_value(h0)) | ((uint32_t)bf16_bits(v2[1] - bf16_value(h1)) << 16);
         }
-        bf16x8 bh[4], bl[4];
-        bfrags(s % kLbBufs, bh, bl);
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-          for (int ct = 0; ct < 4; ++ct) {
-            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[rt], bh[ct], acc[rt][ct], 0, 0, 0);
-            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[rt], bl[ct], acc[rt][ct], 0, 0, 0);
-            acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[rt], bh[ct], acc[rt][ct], 0, 0, 0);
-          }
-        __builtin_amdgcn_s_waitcnt(0x0F70);  // the W tiles of step s + 1 (the x loads are waited for already)
-        __syncthreads();
+        ah[rt] = __builtin_bit_cast(bf16x8, make_uint4(hx[0], hx[1], hx[2], hx[3]));
+        al[rt] = __builtin_bit_cast(bf16x8, make_uint4(lx[0], lx[1], lx[2], lx[3]));
       }
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          f32x4& c = acc[4 * half + rt][ct];
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[rt], bh[ct], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[rt], bl[ct], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[rt], bh[ct], c, 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // the tiles of step s + 1 (the x loads are waited for already)
+      __syncthreads();
     }
-    // The last step's barrier: every wavefront is done with the W buffers.
-    // Request the next tile's first loads, then store this one.
-    const int64_t r0_this = r0;
-    const int c0_this = c0;
-    const int64_t next = tile + gridDim.x;
-    if (next < ntiles) {
-      place(next);
-      first_loads();
-    }
-    lb_store_tile<TOut>(acc, stile, a.bias, rs_y, a.m, a.c_out, r0_this + 64 * wr, c0_this + 64 * wc, lane);
   }
+  // The last step's barrier: every wavefront is done with the buffers.
+  const auto rs_y = buf_rsrc(a.y, (uint32_t)((uint64_t)a.m * (uint64_t)a.c_out * sizeof(TOut)));
+  lb_store_tile<kLbRT, TOut>(acc, &s_out[wave * 16 * 68], a.bias, rs_y, a.m, a.c_out, r0 + 128 * wr, c0 + 64 * wc,
+                             lane);
 }
 
 template <typename TIn>
@@ -578,15 +573,11 @@ int launch_lb_d(const LinMfmaArgs& a, const uint32_t* bits, const uint32_t* flag
                 hipStream_t stream) {
   const int64_t tiles = ((a.m + kLbRows - 1) / kLbRows) * ((a.c_out + kLmCols - 1) / kLmCols);
   if (tiles == 0) return (int)hipSuccess;
-  // One workgroup per CU (a multiple of 8, at most one per tile rounded up
-  // to 8): every CU loops over its tiles.
-  const int64_t cus = (num_cus() + 7) / 8 * 8;
-  const int64_t grid = tiles < cus ? (tiles + 7) / 8 * 8 : cus;
   if (out_dtype == SF_F32)
-    hipLaunchKernelGGL((k_linear_bits_mfma<TIn, float>), dim3((unsigned)grid), dim3(64 * kLbWaves), 0, stream, a,
+    hipLaunchKernelGGL((k_linear_bits_mfma<TIn, float>), dim3((unsigned)tiles), dim3(64 * kLbWaves), 0, stream, a,
                        bits, flags, cwp);
   else
-    hipLaunchKernelGGL((k_linear_bits_mfma<TIn, TIn>), dim3((unsigned)grid), dim3(64 * kLbWaves), 0, stream, a, bits,
+    hipLaunchKernelGGL((k_linear_bits_mfma<TIn, TIn>), dim3((unsigned)tiles), dim3(64 * kLbWaves), 0, stream, a, bits,
                        flags, cwp);
   return (int)hipGetLastError();
 }
