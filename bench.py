@@ -514,7 +514,8 @@ def bench_attn(steps, warmup, dev, with_dense=True, T=4, N=64, tokens=196, dim=3
     ws = torch.empty(_lib.linear_workspace_size(bt * tokens, 4 * dim), dtype=torch.uint8, device=dev)
 
     def lin_case(m, x):
-        return (lambda: sparse_linear_forward(x, m.weight, m.bias, w_split=splits[id(m)], kernel="mfma"),
+        # The library's own kernel choice ("auto": the row bitmap for the wide fc1).
+        return (lambda: sparse_linear_forward(x, m.weight, m.bias, w_split=splits[id(m)], kernel="auto"),
                 lambda: torch.nn.functional.linear(x, m.weight, m.bias),
                 x.numel() * 4 + m.weight.numel() * 4 + x.shape[0] * m.out_features * 4)
     scale = hd ** -0.5

@@ -56,7 +56,8 @@ class SparseLinear(OpReporting, nn.Module):
         self.return_ms = bool(return_ms)
         self.fallback_ratio = float(fallback_ratio)
         self.launch_all_tiles = bool(launch_all_tiles)
-        # Stage-2 kernel: "auto" (matrix cores for in_features >= 32), "mfma"
+        # Stage-2 kernel: "auto" (matrix cores for in_features >= 32, over the
+        # row bitmap when out_features >= 2 in_features), "mfma", "mfma_bits"
         # or "walk" (the spike walk; fewer MACs at very low densities).
         self.kernel = "auto"
         self.policy = FallbackPolicy(_config.ENABLE_RUNTIME_FALLBACK_POLICY, warmup_steps, calib_every, ema_decay,

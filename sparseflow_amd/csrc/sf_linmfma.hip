@@ -520,6 +520,7 @@ __global__ __launch_bounds__(64 * kLbWaves, 2) void k_linear_bits_mfma(LinMfmaAr
     // x tiles: lane (li, g) reads k = 32 s + 8 g .. + 7 of its rows; past k
     // and past m the elements are 0; |x| < cutoff counts as 0.  The eight
     // row tiles in two halves (registers).
+    const bool vec4 = sizeof(TIn) == 4 && (a.k & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
     for (int s = 0; s < nsteps; ++s) {
       if (s + 2 < nsteps) load_step(s + 2);  // its buffer was last read by step s - 1
       bf16x8 bh[4], bl[4];
@@ -531,16 +532,33 @@ __global__ __launch_bounds__(64 * kLbWaves, 2) void k_linear_bits_mfma(LinMfmaAr
       for (int rt = 0; rt < 4; ++rt) {
         const int64_t row = r0 + 128 * wr + 16 * (4 * half + rt) + li;
         const int kk0 = 32 * s + 8 * g;
+        float v8[8];
+        if (vec4) {
+          // f32 rows, k % 4 == 0, 16-byte aligned: two 16-byte loads, each
+          // wholly inside or past the row.
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const bool ok = row < a.m && kk0 + 4 * h < a.k;
+            const float4 t = *reinterpret_cast<const float4*>(ok ? reinterpret_cast<const float*>(X) + row * a.k + kk0 + 4 * h
+                                                                 : reinterpret_cast<const float*>(X));
+            v8[4 * h] = ok ? t.x : 0.f;
+            v8[4 * h + 1] = ok ? t.y : 0.f;
+            v8[4 * h + 2] = ok ? t.z : 0.f;
+            v8[4 * h + 3] = ok ? t.w : 0.f;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int kk = kk0 + e;
+            v8[e] = (row < a.m && kk < a.k) ? to_f32<TIn>(X[row * a.k + kk]) : 0.f;
+          }
+        }
         uint32_t hx[4], lx[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float v2[2];
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int kk = kk0 + 2 * j + e;
-            const float t = (row < a.m && kk < a.k) ? to_f32<TIn>(X[row * a.k + kk]) : 0.f;
-            v2[e] = fabsf(t) >= a.cutoff ? t : 0.f;
-          }
+          for (int e = 0; e < 2; ++e) v2[e] = fabsf(v8[2 * j + e]) >= a.cutoff ? v8[2 * j + e] : 0.f;
           const uint16_t h0 = bf16_bits(v2[0]), h1 = bf16_bits(v2[1]);
           hx[j] = (uint32_t)h0 | ((uint32_t)h1 << 16);
           lx[j] = (uint32_t)bf16_bits(v2[0] - bf16_value(h0)) | ((uint32_t)bf16_bits(v2[1] - bf16_value(h1)) << 16);
