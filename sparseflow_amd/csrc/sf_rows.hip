@@ -120,7 +120,7 @@ __device__ __forceinline__ void kc_rows(float (&acc)[64], const KcTile& k) {
 }
 
 // Chunk c's words of the tile's halo positions (rows oh0 - 1 .. oh0 + TH of
-// the frame; rows outside it read position 0 and are never walked).  Word c
+// the frame; rows outside it read position 0 and come back as 0).  Word c
 // of pixel q at q * ps + c * ws words from the frame's start: with word
 // planes (ps = 1) the 64 lanes of a load read one run.
 template <int TH, int W>
@@ -133,6 +133,39 @@ __device__ __forceinline__ void kc_load_words(uint32_t& v0, uint32_t& v1, const 
   const int64_t q0 = ok0 ? (int64_t)(oh0 - 1) * W + p0 : 0, q1 = ok1 ? (int64_t)(oh0 - 1) * W + p1 : 0;
   v0 = fbits[q0 * ps + (int64_t)c * ws];
   v1 = fbits[q1 * ps + (int64_t)c * ws];
+  // Positions outside the halo or the frame hold no spikes (the walk never
+  // reads them; the dense-tile branch counts every lane).
+  v0 = ok0 ? v0 : 0u;
+  v1 = ok1 ? v1 : 0u;
+}
+
+// Dense-tile branch of the row kernel: a binary tile whose first chunk (32
+// input channels) holds kRowsDenseSpikes or more spikes in its halo rows
+// (3-4x the mean at 1% density, 10+ standard deviations above it for i.i.d.
+// spikes) is not walked.  Its walk would last several times an ordinary
+// tile's, and since every chunk step ends at a barrier it would hold its
+// whole pass: live spikes burst in a few time steps, and a pass covers
+// consecutive frames of one step.  The 64-pixel tiles of the
+// flattened (frame, pixel) axis that cover it go to the matrix-core queue
+// instead (k_conv_dense_mfma, launched right after on the same stream),
+// provided every input row those tiles read is binary: the dense kernel
+// computes whole 64-pixel tiles, so it also rewrites neighbouring tiles'
+// pixels (with their values to the dense kernel's rounding).
+constexpr int kRowsDenseSpikes = 96;
+
+// Whether input rows ih_a .. ih_b (clamped to the frame) of frame f are all
+// binary: the prescan's per-chunk flags over those rows.  A frame's pixel
+// offsets fit 32 bits, so the chunk bounds are 32-bit divisions.
+__device__ __forceinline__ bool kc_rows_binary(const ConvArgs& a, const uint32_t* __restrict__ flags, int64_t f,
+                                               int ih_a, int ih_b) {
+  ih_a = max(0, ih_a);
+  ih_b = min(a.h_in - 1, ih_b);
+  const uint32_t ch = (uint32_t)a.chunk;
+  const uint32_t c_a = (uint32_t)(ih_a * a.w_in) / ch, c_b = (uint32_t)(ih_b * a.w_in + a.w_in - 1) / ch;
+  const uint32_t* __restrict__ fl = flags + f * a.chunks_per_frame;
+  uint32_t v = 0u;
+  for (uint32_t q = c_a; q <= c_b; ++q) v |= fl[q];
+  return v == 0u;
 }
 
 template <int TH, int W>
@@ -142,7 +175,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
                                                                   const float* __restrict__ wt,
                                                                   const float* __restrict__ bias_p,
                                                                   void* __restrict__ y, int groups, int nchunks,
-                                                                  int in_dtype, int out_dtype) {
+                                                                  int in_dtype, int out_dtype,
+                                                                  DenseQueue* __restrict__ dq) {
   // Launched only for planes with h*w % 4 == 0, so every tile's run (TH*W, or
   // an even number of 14-wide rows for the last tile) is whole quads.
   static_assert(TH * W <= 64 && (TH * W) % 4 == 0, "tile must be a whole number of quads within 64 pixels");
@@ -189,6 +223,43 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
     const uint32_t* __restrict__ fbits = bits + (int64_t)frame * a.hw_in * a.cwp;
     uint32_t nw0 = 0u, nw1 = 0u;
     if (valid) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.bm_ps, a.bm_ws, lane, 0);
+    bool walk = valid;
+    if (dq != nullptr && valid && !k.value) {
+      int cnt = __popc(nw0) + __popc(nw1);
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+      // Every lane holds the sum; read it as a scalar so that the walk below
+      // stays a uniform branch.
+      cnt = __builtin_amdgcn_readfirstlane(cnt);
+      // Frames of at least 64 pixels: the 64-pixel tiles covering the tile
+      // reach at most into the frames either side.  Offsets s_lo .. s_hi of
+      // those tiles' pixels are relative to this frame's first pixel.
+      // (Stride 1, same size: hw_out = hw_in; the last frame's tiles are the
+      // last tpf.)
+      if (cnt >= kRowsDenseSpikes && a.hw_in >= 64) {
+        const int hw = a.hw_in;
+        const int e0 = oh0 * W, e1 = e0 + min(TH, h - oh0) * W - 1;
+        const int base = (int)((((uint32_t)frame & 63u) * ((uint32_t)hw & 63u)) & 63u);  // frame * hw mod 64
+        const int s_lo = e0 - ((base + e0) & 63);
+        int s_hi = e1 + 63 - ((base + e1) & 63);
+        if (t >= total - tpf) s_hi = min(s_hi, hw - 1);
+        bool binary = kc_rows_binary(a, flags, frame, max(s_lo, 0) / W - 1, min(s_hi, hw - 1) / W + 1);
+        if (s_lo < 0) binary = binary && kc_rows_binary(a, flags, frame - 1, (hw + s_lo) / W - 1, h);
+        if (s_hi >= hw) binary = binary && kc_rows_binary(a, flags, frame + 1, -1, (s_hi - hw) / W + 1);
+        if (binary) {
+          const uint32_t t0 = (uint32_t)(((int64_t)frame * hw + s_lo) >> 6);
+          const uint32_t nt = (uint32_t)(((e1 - s_lo) >> 6) + 1);
+          uint32_t slot = 0u;
+          if (lane == 0) slot = atomicAdd(&dq->count[grp], nt);
+          slot = __builtin_amdgcn_readfirstlane(slot);
+          // Entries past the queue's capacity are not written (nor read);
+          // the tile is walked unless all of its entries fit.
+          if ((uint32_t)lane < nt && slot + (uint32_t)lane < (uint32_t)kDenseQueueCap)
+            dq->start[grp][slot + lane] = t0 + (uint32_t)lane;
+          if (slot + nt <= (uint32_t)kDenseQueueCap) walk = false;
+        }
+      }
+    }
     if (!resident) {
       __syncthreads();  // the previous pass is done with both buffers
       load_chunk(smem, wt, 0, krows, a.c_out, co0, wave, lane);
@@ -200,7 +271,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
       // chunk c-1, which every wavefront finished before the last barrier.
       if (!resident && c + 1 < nchunks)
         load_chunk(smem + ((c + 1) & 1) * kChunkBytes, wt, c + 1, krows, a.c_out, co0, wave, lane);
-      if (valid) {
+      if (walk) {
         k.vw0 = nw0;
         k.vw1 = nw1;
         if (c + 1 < nchunks) kc_load_words<TH, W>(nw0, nw1, fbits, oh0, h, a.bm_ps, a.bm_ws, lane, c + 1);
@@ -213,7 +284,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
         __syncthreads();
       }
     }
-    if (valid) {
+    if (walk) {
       const int npx = min(TH, h - oh0) * W;
       butterfly<1, 16>(acc, lane);
       butterfly<2, 16>(acc, lane);
@@ -227,7 +298,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
 }
 
 template <int TH, int W>
-int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream, DenseQueue** dense) {
   const int groups = (a.c_out + 63) / 64;
   const int nchunks = (a.c_in + 31) / 32;
   const size_t lds = (size_t)2 * kChunkBytes;
@@ -238,9 +309,12 @@ int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stre
   constexpr auto kern = k_conv_rows_kc<TH, W>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
   if (e != (int)hipSuccess) return e;
+  DenseQueue* dq = groups <= kDenseQueueGroups ? dense_queue_for(stream) : nullptr;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags, a.x, a.wt, a.bias,
-                     a.y, groups, nchunks, in_dtype, out_dtype);
-  return (int)hipGetLastError();
+                     a.y, groups, nchunks, in_dtype, out_dtype, dq);
+  const int rc = (int)hipGetLastError();
+  if (rc == (int)hipSuccess) *dense = dq;
+  return rc;
 }
 
 }  // namespace
@@ -267,10 +341,13 @@ bool rows_kc_applicable(const ConvArgs& a) {
 }
 
 int launch_conv_rows_kc(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  DenseQueue* dense = nullptr;
   timing_begin(K_ROWS_KC, stream);
-  const int rc = a.w_out == 28 ? launch_kc_t<2, 28>(a, in_dtype, out_dtype, stream)
-                               : launch_kc_t<4, 14>(a, in_dtype, out_dtype, stream);
+  int rc = a.w_out == 28 ? launch_kc_t<2, 28>(a, in_dtype, out_dtype, stream, &dense)
+                         : launch_kc_t<4, 14>(a, in_dtype, out_dtype, stream, &dense);
   timing_end(K_ROWS_KC, stream);
+  // The tiles the walk queued for the matrix cores, right after it.
+  if (rc == (int)hipSuccess && dense != nullptr) rc = launch_conv_dense_mfma(a, dense, out_dtype, stream);
   return rc;
 }
 

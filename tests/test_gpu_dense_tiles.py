@@ -1,6 +1,8 @@
-"""Dense-tile branch of the streamed pixel-tile kernel (C_in > 128).
+"""Dense-tile branch of the streamed pixel-tile kernel and of the row kernel
+(C_in > 128).
 
-Wave-tiles whose first chunk is dense are queued by k_conv_px3s and computed
+Wave-tiles whose first chunk is dense are queued by k_conv_px3s (and the
+64-pixel tiles covering a heavy row tile by k_conv_rows_kc) and computed
 on the matrix cores (k_conv_dense_mfma: implicit GEMM, spikes exact in bf16,
 W split into bf16 hi + lo, f32 accumulation).  Bar: fp32 within 1e-4 abs +
 1e-4 rel of float64 F.conv2d, fp16/bf16 outputs within 1e-2; the kernel
@@ -79,12 +81,45 @@ def test_dense_tiles_match_dense_conv(case):
     assert native_loaded()
 
 
-def test_row_kernel_shape_with_bursts_stays_exact():
-    N, C, H, W, Co = 16, 256, 14, 14, 256
-    announce("row-kernel shape bursty")
-    x = _bursty((N, C, H, W), range(4, 8), seed=5)
+ROW_CASES = [
+    # (N, C_in, H, W, C_out, dense frames): the row kernel's 14- and 28-wide
+    # planes (C_in > 128, stride 1); 14 x 14 planes put 64-pixel tiles across
+    # frame boundaries.
+    (16, 256, 14, 14, 256, range(4, 8)),
+    (8, 192, 28, 28, 128, (2, 3, 6)),
+]
+
+
+@pytest.mark.parametrize("case", ROW_CASES)
+def test_row_kernel_dense_tiles_match_dense_conv(case):
+    # The row kernel queues its heavy tiles' 64-pixel tiles for the matrix
+    # cores instead of walking them.
+    N, C, H, W, Co, dense = case
+    announce(f"row-kernel dense tiles {case[:5]}")
+    x = _bursty((N, C, H, W), dense, seed=5 + W)
     w = _weights(Co, C, seed=6)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(3)) * 0.1
+    xd = x.to(DEV)
+    y, kernels = _run(xd, w.to(DEV), b.to(DEV), 1)
+    assert "conv_rows_kc" in kernels and "conv_dense_mfma" in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    y2, _ = _run(xd, w.to(DEV), b.to(DEV), 1)
+    assert torch.equal(y, y2)  # deterministic, and the queue was clear again
+
+
+def test_row_kernel_keeps_tiles_next_to_value_frames():
+    # Every frame dense, frame 3 non-binary: the 64-pixel tiles reaching into
+    # frame 3 (14 x 14 planes: tiles span frames) must not be deferred, since
+    # the matrix-core kernel takes its input as spikes.
+    N, C, H, W, Co = 8, 256, 14, 14, 64
+    announce("row-kernel dense tiles beside a value frame")
+    x = _bursty((N, C, H, W), range(N), seed=21)
+    g = torch.Generator().manual_seed(22)
+    x[3] = x[3] * torch.randn(C, H, W, generator=g)
+    w = _weights(Co, C, seed=23)
     y, kernels = _run(x.to(DEV), w.to(DEV), None, 1)
+    assert "conv_rows_kc" in kernels and "conv_dense_mfma" in kernels, kernels
     ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
     assert ok, f"max abs err {err}"
 
