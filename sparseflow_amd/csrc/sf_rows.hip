@@ -63,6 +63,20 @@ __device__ __forceinline__ void kc_position(float (&acc)[64], uint32_t m, const 
     float xv = 1.f;
     if (k.value) xv = load_x(k.x, k.in_dtype, (int64_t)(k.c0 + bit) * k.hw + k.xrow + IA * W + IB);
     const char* base = k.wlb + bit * (9 * 256);
+    // All of the spike's weight rows are read before the first FMA, so their
+    // LDS round trips overlap (one wait per spike, not one per pair of rows).
+    float wv[9];
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh) {
+      const int r = IA - kh;
+#pragma unroll
+      for (int kw = 0; kw < 3; ++kw) {
+        const int xo = IB + 1 - kw;
+        wv[kh * 3 + kw] = (r < 0 || r >= TH || xo < 0 || xo >= W)
+                              ? 0.f
+                              : *reinterpret_cast<const float*>(base + (kh * 3 + kw) * 256);
+      }
+    }
 #pragma unroll
     for (int kh = 0; kh < 3; ++kh) {
       const int r = IA - kh;
@@ -71,7 +85,7 @@ __device__ __forceinline__ void kc_position(float (&acc)[64], uint32_t m, const 
       for (int kw = 0; kw < 3; ++kw) {
         const int xo = IB + 1 - kw;
         if (xo < 0 || xo >= W) continue;
-        acc[r * W + xo] = fmaf(xv, *reinterpret_cast<const float*>(base + (kh * 3 + kw) * 256), acc[r * W + xo]);
+        acc[r * W + xo] = fmaf(xv, wv[kh * 3 + kw], acc[r * W + xo]);
       }
     }
   }
