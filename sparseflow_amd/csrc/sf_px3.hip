@@ -89,10 +89,25 @@ __device__ __forceinline__ void load_chunk_px3(char* buf, const float* __restric
 }
 
 // Add the weight row at rowp (piece swizzle key for CO = 32), times xv, to
-// the CO accumulators.
-template <int CO>
+// the CO accumulators.  WHOLE (CO = 32 kernels with registers to spare, not
+// the fused LIF kernels, which use all 128): all eight pieces are read
+// before the first FMA, one LDS wait per spike instead of one per pair.
+template <int CO, bool WHOLE = false>
 __device__ __forceinline__ void px3_add_row_at(float (&acc)[CO], const char* rowp, int key, float xv) {
   typedef Px3Layout<CO> L;
+  if constexpr (CO == 32 && WHOLE) {
+    float4 v[L::pieces];
+#pragma unroll
+    for (int s = 0; s < L::pieces; ++s) v[s] = *reinterpret_cast<const float4*>(rowp + ((s << 4) ^ key));
+#pragma unroll
+    for (int s = 0; s < L::pieces; ++s) {
+      acc[4 * s] = fmaf(xv, v[s].x, acc[4 * s]);
+      acc[4 * s + 1] = fmaf(xv, v[s].y, acc[4 * s + 1]);
+      acc[4 * s + 2] = fmaf(xv, v[s].z, acc[4 * s + 2]);
+      acc[4 * s + 3] = fmaf(xv, v[s].w, acc[4 * s + 3]);
+    }
+    return;
+  }
 #pragma unroll
   for (int s = 0; s < L::pieces; ++s) {
     // Groups of four pieces: the scheduler may not hoist more than 16
@@ -108,10 +123,10 @@ __device__ __forceinline__ void px3_add_row_at(float (&acc)[CO], const char* row
 }
 
 // Add weight row r of the chunk, times xv, to the CO accumulators.
-template <int CO>
+template <int CO, bool WHOLE = false>
 __device__ __forceinline__ void px3_add_row(float (&acc)[CO], const char* chunk, int r, float xv) {
   typedef Px3Layout<CO> L;
-  px3_add_row_at<CO>(acc, chunk + (r * L::stride) * 16, CO == 64 ? 0 : ((r >> 1) & L::xmask) << 4, xv);
+  px3_add_row_at<CO, WHOLE>(acc, chunk + (r * L::stride) * 16, CO == 64 ? 0 : ((r >> 1) & L::xmask) << 4, xv);
 }
 
 // Rows (ci, tap) of a 64-channel chunk (272-byte rows, row ci * 9 + tap):
@@ -410,7 +425,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3(ConvArgs a, const 
               // include the next chunk's streamed rows and bitmap words.
               __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
             }
-            px3_add_row<CO>(acc, chunk, bit * 9 + tap, xv);
+            px3_add_row<CO, !LIF>(acc, chunk, bit * 9 + tap, xv);
           }
         }
         if (!resident) {
@@ -870,7 +885,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
               __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
             }
             if constexpr (CO == 64) px3_add_row_at<64>(acc, px3_spike_row(trows, bit), 0, xv);
-            else px3_add_row<CO>(acc, smem, row0 + bit * 9 + tap, xv);
+            else px3_add_row<CO, !LIF>(acc, smem, row0 + bit * 9 + tap, xv);
           }
         }
       }
