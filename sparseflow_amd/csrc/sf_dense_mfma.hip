@@ -6,9 +6,12 @@
 // carries two thirds of a deep layer's spikes at ~10% density, so a few
 // wave-tiles hold most of the work, walk for several times longer than the
 // rest and hold their workgroup at every chunk barrier.  Such tiles are dense
-// enough for the matrix cores: k_conv_px3s hands them (by a test on the
-// first chunk's tap words) to a per-channel-group queue instead of walking
-// them, and k_conv_dense_mfma below computes them as an implicit GEMM,
+// enough for the matrix cores: k_conv_px3s (and the row kernel,
+// k_conv_rows_kc, for its row tiles) hands them (by a test on the first
+// chunk's tap words) to a per-channel-group queue instead of walking them,
+// each as a run of at most 64 output pixels of the flattened (frame, pixel)
+// axis, and k_conv_dense_mfma below computes the 64 pixels from each run's
+// first (storing the run's own) as an implicit GEMM,
 //   y[px, co] = bias[co] + sum_k S[px, k] W[k, co],  k = (tap, ci),
 // with the 0/1 spikes exact in bf16 and W split into bf16 hi + lo parts
 // (W = hi + lo + O(2^-17 |W|)), accumulated in f32: the reference's
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         const int grp = p.col / kDmCols;
         const int e0 = kDmTiles * p.k;
         const int e = e0 + sv < s_tiles[grp] ? e0 + sv : e0;
-        const int gp = (int)dq->start[grp][e] * 64 + lane;
+        const int gp = (int)dq->start[grp][e] + lane;
         const int gc = gp < total_px ? gp : total_px - 1;
         const int sample = gc / hwo;
         const int q = gc - sample * hwo;
@@ -340,7 +343,8 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         const int grp = it.col / kDmCols;
         const int e0 = kDmTiles * it.k;
         const bool has = e0 + wave < s_tiles[grp];
-        const int t = (int)dq->start[grp][has ? e0 + wave : e0];
+        const int p0 = (int)dq->start[grp][has ? e0 + wave : e0];  // the run's first output pixel
+        const int npx = has ? (int)dq->npx[grp][e0 + wave] : 0;
         const int co0 = grp * kDmGroupCo + (it.col % kDmCols) * kDmCo;
         f32x4 acc[4][2];
 #pragma unroll
@@ -400,7 +404,8 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
           __syncthreads();  // stage st & 1 free for step st + 2; stage (st + 1) & 1 written
         }
         // Accumulator (rt, ct) element i of lane (li, g): output pixel
-        // t*64 + 16 rt + 4 g + i, output channel co0 + 16 ct + li.
+        // p0 + 16 rt + 4 g + i (stored for the run's first npx), output
+        // channel co0 + 16 ct + li.
         if (has) {
           float bv[2];
 #pragma unroll
@@ -412,8 +417,8 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
           for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int pix = t * 64 + 16 * rt + 4 * g + i;
-              if (pix >= total_px) continue;
+              const int pix = p0 + 16 * rt + 4 * g + i;
+              if (16 * rt + 4 * g + i >= npx || pix >= total_px) continue;
               const int smp = pix / hwo;
               const int64_t ybase = (int64_t)smp * a.c_out * hwo + (pix - smp * hwo);
 #pragma unroll

@@ -122,21 +122,24 @@ int launch_conv_px3(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t 
 // (C_in * 9 <= 32, f32 input): the whole K is one dense tile.
 bool mfma_conv_applicable(const ConvArgs& a);
 int launch_conv_mfma(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream);
-// Dense-tile branch of the streamed pixel-tile kernel (k_conv_px3s): wave-tiles
-// whose first chunk is dense go to a queue (per 64-output-channel group, the
-// tile's index in the flattened 64-pixel tiling) and are computed on the
-// matrix cores by launch_conv_dense_mfma, launched right after on the same
-// stream; its last workgroup clears the counts.  One queue slot per stream
-// (library-owned static device memory); dense_queue_for returns the
-// stream's slot, or NULL when every slot is taken (then nothing is deferred).
+// Dense-tile branch of the streamed pixel-tile kernel (k_conv_px3s) and of
+// the row kernel (k_conv_rows_kc): tiles whose first chunk is dense go to a
+// queue (per 64-output-channel group, a run of at most 64 output pixels of
+// the flattened (frame, pixel) axis: its first pixel and its length) and are
+// computed on the matrix cores by launch_conv_dense_mfma, launched right
+// after on the same stream; its last workgroup clears the counts.  One queue
+// slot per stream (library-owned static device memory); dense_queue_for
+// returns the stream's slot, or NULL when every slot is taken (then nothing
+// is deferred).
 constexpr int kDenseQueueSlots = 8;
 constexpr int kDenseQueueGroups = 32;   // C_out <= 2048
-constexpr int kDenseQueueCap = 4096;    // tiles per group; more are walked
+constexpr int kDenseQueueCap = 4096;    // runs per group; more are walked
 struct DenseQueue {
   uint32_t count[kDenseQueueGroups];
   uint32_t done;
   uint32_t pad[31];
-  uint32_t start[kDenseQueueGroups][kDenseQueueCap];
+  uint32_t start[kDenseQueueGroups][kDenseQueueCap];  // first output pixel of the run
+  uint8_t npx[kDenseQueueGroups][kDenseQueueCap];     // its pixels (1 .. 64)
 };
 DenseQueue* dense_queue_for(hipStream_t stream);
 // Looks up the queue array's device address on the current GPU (once; it

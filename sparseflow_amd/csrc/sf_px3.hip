@@ -563,7 +563,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3s(ConvArgs a, const
         if (lane == 0) slot = atomicAdd(&dq->count[grp], 1u);
         slot = __builtin_amdgcn_readfirstlane(slot);
         if (slot < (uint32_t)kDenseQueueCap) {
-          if (lane == 0) dq->start[grp][slot] = (uint32_t)t;
+          if (lane == 0) {
+            dq->start[grp][slot] = (uint32_t)t * 64u;
+            dq->npx[grp][slot] = 64;  // the last tile's pixels past the end are not stored
+          }
           walk = false;
           ybase = yrange;
         }
@@ -995,7 +998,9 @@ int launch_px3s_to(const ConvArgs& a, hipStream_t stream, DenseQueue** dense) {
   constexpr auto kern = k_conv_px3s<TIn, TOut>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
-  DenseQueue* dq = groups <= kDenseQueueGroups ? dense_queue_for(stream) : nullptr;
+  // (Queue entries hold a run's first pixel of the flattened axis in 31 bits.)
+  DenseQueue* dq =
+      groups <= kDenseQueueGroups && a.n * (int64_t)a.hw_out < (1ll << 31) ? dense_queue_for(stream) : nullptr;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), (size_t)2 * LY::chunk_bytes, stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups, nchunks, dq);
   const int rc = (int)hipGetLastError();

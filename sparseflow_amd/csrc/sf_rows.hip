@@ -159,28 +159,13 @@ __device__ __forceinline__ void kc_load_words(uint32_t& v0, uint32_t& v1, const 
 // spikes) is not walked.  Its walk would last several times an ordinary
 // tile's, and since every chunk step ends at a barrier it would hold its
 // whole pass: live spikes burst in a few time steps, and a pass covers
-// consecutive frames of one step.  The 64-pixel tiles of the
-// flattened (frame, pixel) axis that cover it go to the matrix-core queue
-// instead (k_conv_dense_mfma, launched right after on the same stream),
-// provided every input row those tiles read is binary: the dense kernel
-// computes whole 64-pixel tiles, so it also rewrites neighbouring tiles'
-// pixels (with their values to the dense kernel's rounding).
+// consecutive frames of one step.  The tile's run of output pixels (TH rows
+// of one frame, at most 64 pixels, contiguous on the flattened (frame,
+// pixel) axis) goes to the matrix-core queue instead (k_conv_dense_mfma,
+// launched right after on the same stream), which computes the 64 pixels
+// from the run's first and stores the run's own.  A binary tile's halo rows
+// are all the input rows those pixels read.
 constexpr int kRowsDenseSpikes = 96;
-
-// Whether input rows ih_a .. ih_b (clamped to the frame) of frame f are all
-// binary: the prescan's per-chunk flags over those rows.  A frame's pixel
-// offsets fit 32 bits, so the chunk bounds are 32-bit divisions.
-__device__ __forceinline__ bool kc_rows_binary(const ConvArgs& a, const uint32_t* __restrict__ flags, int64_t f,
-                                               int ih_a, int ih_b) {
-  ih_a = max(0, ih_a);
-  ih_b = min(a.h_in - 1, ih_b);
-  const uint32_t ch = (uint32_t)a.chunk;
-  const uint32_t c_a = (uint32_t)(ih_a * a.w_in) / ch, c_b = (uint32_t)(ih_b * a.w_in + a.w_in - 1) / ch;
-  const uint32_t* __restrict__ fl = flags + f * a.chunks_per_frame;
-  uint32_t v = 0u;
-  for (uint32_t q = c_a; q <= c_b; ++q) v |= fl[q];
-  return v == 0u;
-}
 
 template <int TH, int W>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, const uint32_t* __restrict__ bits,
@@ -245,32 +230,18 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_rows_kc(ConvArgs a, co
       // Every lane holds the sum; read it as a scalar so that the walk below
       // stays a uniform branch.
       cnt = __builtin_amdgcn_readfirstlane(cnt);
-      // Frames of at least 64 pixels: the 64-pixel tiles covering the tile
-      // reach at most into the frames either side.  Offsets s_lo .. s_hi of
-      // those tiles' pixels are relative to this frame's first pixel.
-      // (Stride 1, same size: hw_out = hw_in; the last frame's tiles are the
-      // last tpf.)
-      if (cnt >= kRowsDenseSpikes && a.hw_in >= 64) {
-        const int hw = a.hw_in;
-        const int e0 = oh0 * W, e1 = e0 + min(TH, h - oh0) * W - 1;
-        const int base = (int)((((uint32_t)frame & 63u) * ((uint32_t)hw & 63u)) & 63u);  // frame * hw mod 64
-        const int s_lo = e0 - ((base + e0) & 63);
-        int s_hi = e1 + 63 - ((base + e1) & 63);
-        if (t >= total - tpf) s_hi = min(s_hi, hw - 1);
-        bool binary = kc_rows_binary(a, flags, frame, max(s_lo, 0) / W - 1, min(s_hi, hw - 1) / W + 1);
-        if (s_lo < 0) binary = binary && kc_rows_binary(a, flags, frame - 1, (hw + s_lo) / W - 1, h);
-        if (s_hi >= hw) binary = binary && kc_rows_binary(a, flags, frame + 1, -1, (s_hi - hw) / W + 1);
-        if (binary) {
-          const uint32_t t0 = (uint32_t)(((int64_t)frame * hw + s_lo) >> 6);
-          const uint32_t nt = (uint32_t)(((e1 - s_lo) >> 6) + 1);
-          uint32_t slot = 0u;
-          if (lane == 0) slot = atomicAdd(&dq->count[grp], nt);
-          slot = __builtin_amdgcn_readfirstlane(slot);
-          // Entries past the queue's capacity are not written (nor read);
-          // the tile is walked unless all of its entries fit.
-          if ((uint32_t)lane < nt && slot + (uint32_t)lane < (uint32_t)kDenseQueueCap)
-            dq->start[grp][slot + lane] = t0 + (uint32_t)lane;
-          if (slot + nt <= (uint32_t)kDenseQueueCap) walk = false;
+      if (cnt >= kRowsDenseSpikes) {
+        uint32_t slot = 0u;
+        if (lane == 0) slot = atomicAdd(&dq->count[grp], 1u);
+        slot = __builtin_amdgcn_readfirstlane(slot);
+        // A slot past the queue's capacity is not written (nor read); the
+        // tile is walked.
+        if (slot < (uint32_t)kDenseQueueCap) {
+          if (lane == 0) {
+            dq->start[grp][slot] = (uint32_t)((int64_t)frame * a.hw_out + (int64_t)oh0 * W);
+            dq->npx[grp][slot] = (uint8_t)(min(TH, h - oh0) * W);
+          }
+          walk = false;
         }
       }
     }
@@ -323,7 +294,9 @@ int launch_kc_t(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stre
   constexpr auto kern = k_conv_rows_kc<TH, W>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes);
   if (e != (int)hipSuccess) return e;
-  DenseQueue* dq = groups <= kDenseQueueGroups ? dense_queue_for(stream) : nullptr;
+  // (Queue entries hold a run's first pixel of the flattened axis in 31 bits.)
+  DenseQueue* dq =
+      groups <= kDenseQueueGroups && a.n * (int64_t)a.hw_out < (1ll << 31) ? dense_queue_for(stream) : nullptr;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * kRowsWaves), lds, stream, a, a.bits, a.flags, a.x, a.wt, a.bias,
                      a.y, groups, nchunks, in_dtype, out_dtype, dq);
   const int rc = (int)hipGetLastError();

@@ -124,6 +124,34 @@ def test_row_kernel_keeps_tiles_next_to_value_frames():
     assert ok, f"max abs err {err}"
 
 
+def test_row_kernel_more_dense_tiles_than_the_queue_holds():
+    # 1400 dense 14 x 14 frames = 4288 64-pixel tiles in one group: the row
+    # kernel queues what fits (4096) and walks the rest.  (Four output
+    # channels keep the float64 reference quick.)
+    N, C, H, W, Co = 1400, 160, 14, 14, 4
+    announce("row-kernel queue overflow")
+    x = _bursty((N, C, H, W), range(N), seed=31)
+    w = _weights(Co, C, seed=32)
+    y, kernels = _run(x.to(DEV), w.to(DEV), None, 1)
+    assert "conv_rows_kc" in kernels and "conv_dense_mfma" in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
+def test_row_kernel_small_frames_walk_dense_tiles():
+    # Frames of 4 x 14 = 56 pixels: a 64-pixel tile would reach past both
+    # neighbouring frames, so the branch keeps such tiles on the walk.
+    N, C, H, W, Co = 24, 192, 4, 14, 64
+    announce("row-kernel dense tiles, frames under 64 pixels")
+    x = _bursty((N, C, H, W), range(N), seed=33)
+    w = _weights(Co, C, seed=34)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(35)) * 0.1
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV), 1)
+    assert "conv_rows_kc" in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+
+
 def test_queue_is_clear_after_a_dense_call():
     N, C, H, W, Co = 16, 256, 28, 28, 128
     announce("dense then sparse")
