@@ -108,6 +108,23 @@ def test_row_kernel_dense_tiles_match_dense_conv(case):
     assert torch.equal(y, y2)  # deterministic, and the queue was clear again
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_row_kernel_dense_tiles_half_precision(dtype):
+    # Half-precision spikes and output through the row kernel's runs.
+    N, C, H, W, Co = 8, 192, 14, 14, 128
+    announce(f"row-kernel dense tiles {dtype}")
+    x = _bursty((N, C, H, W), (2, 3), seed=41)
+    w = _weights(Co, C, seed=42)
+    b = torch.linspace(-0.3, 0.3, Co)
+    y, kernels = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), 1)
+    assert y.dtype == dtype and "conv_rows_kc" in kernels and "conv_dense_mfma" in kernels, kernels
+    ok, err, _ = close(y, oconv.conv2d_ref(x, w, b, 1, 1), atol=1e-2, rtol=1e-2)
+    assert ok, f"max abs err {err}"
+    y32, _ = _run(x.to(DEV, dtype), w.to(DEV), b.to(DEV), 1, output_dtype=torch.float32)
+    ok, err, _ = close(y32, oconv.conv2d_ref(x, w, b, 1, 1), **FP32_TOL)
+    assert ok, f"f32 output: max abs err {err}"
+
+
 def test_row_kernel_keeps_tiles_next_to_value_frames():
     # Every frame dense, frame 3 non-binary: the 64-pixel tiles reaching into
     # frame 3 (14 x 14 planes: tiles span frames) must not be deferred, since
