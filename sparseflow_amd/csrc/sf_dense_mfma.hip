@@ -120,12 +120,21 @@ struct DmItems {
   }
 };
 
-template <typename TOut>
+// ONE: a 1x1 stride-1 convolution (k_conv_flat's dense tiles): the nine K
+// steps of a stage are nine consecutive 32-channel words of the pixel's own
+// bitmap (pixel-major, as k_conv_flat reads it), and weight row ci (tap-major
+// with one tap) holds channel ci; words and rows past C_in read zero through
+// the buffer resources' bounds.
+template <typename TOut, bool ONE>
 __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_conv_dense_mfma(
     ConvArgs a, DenseQueue* __restrict__ dq, const uint32_t* __restrict__ bits, const float* __restrict__ wt,
     const float* __restrict__ bias_p, TOut* __restrict__ y, int groups, int nchunks) {
-  // [stage buffer][hi / lo][row (tap, co)][32 ci], pieces swizzled.
-  __shared__ __align__(16) uint16_t s_w[2][2][kDmStage];
+  // [stage buffer][part: hi, lo (, lo2)][row (tap, co)][32 ci], pieces
+  // swizzled.  The 1x1 form splits W into three bf16 parts (24 bits of
+  // mantissa: as exact as the f32 walk, which its tiles replace at every
+  // layer of a deep 1x1 stack); the 3x3 form into two.
+  constexpr int NPART = ONE ? 3 : 2;
+  __shared__ __align__(16) uint16_t s_w[2][NPART][kDmStage];
   // [stage buffer][tile][pixel][tap, padded to 12]: the chunk's bitmap word
   // of each tap of each pixel of the item's tiles (48-byte rows: three
   // aligned 16-byte reads per pixel, sixteen consecutive pixels in distinct
@@ -194,14 +203,14 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
       const int tap0 = (sv >> 1) * kDmTapSplit;        // wave-uniform
       const int ntap = sv >> 1 ? 9 - kDmTapSplit : kDmTapSplit;
       const int row4 = a.c_out * 4;
-      const auto rs_w = buf_rsrc(wt, (uint32_t)((int64_t)a.c_in * 9 * a.c_out * 4));
+      const auto rs_w = buf_rsrc(wt, (uint32_t)((int64_t)a.c_in * (ONE ? 1 : 9) * a.c_out * 4));
       // Lanes past the last queued tile take the item's first tile (their
       // rows are computed and never stored).
       const int hwo = a.hw_out;
       const int total_px = (int)(a.n * hwo);
       const uint32_t frame_bytes = (uint32_t)a.hw_in * (uint32_t)a.cwp * 4u;
       const auto rs_bits = buf_rsrc(bits, (uint32_t)((int64_t)a.n * frame_bytes));
-      int ih0 = 0, iw0 = 0;
+      int ih0 = 0, iw0 = 0, qpx = 0;
       uint32_t fbase = 0;
       auto item_pixel = [&](const DmItems& p) {
         const int grp = p.col / kDmCols;
@@ -214,11 +223,32 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
         const int oh = q / a.w_out, ow = q - oh * a.w_out;
         ih0 = oh * a.s - 1;
         iw0 = ow * a.s - 1;
+        qpx = q;
         fbase = (uint32_t)sample * frame_bytes;
       };
       auto load_w = [&](f32x4 (&wv)[kDmWLoads], int col, int c) {
         const int co0 = (col / kDmCols) * kDmGroupCo + (col % kDmCols) * kDmCo;
         const int wcol = co0 + 4 * cq < a.c_out ? co0 + 4 * cq : a.c_out - 4;  // c_out is a multiple of 4
+        if constexpr (ONE) {
+          // Step tp of stage c: word w = 9 c + tap0 + tp, channels 32 w + 16 (v & 1)
+          // + 2 e + j (rows past C_in read zero).
+          uint32_t vo = (uint32_t)wcol * 4u + (uint32_t)(2 * ce * row4);
+          asm volatile("" : "+v"(vo));
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            int so = ((9 * c + tap0) * 32 + 16 * (sv & 1) + j) * row4;
+#pragma unroll
+            for (int tp = 0; tp < kDmTapSplit; ++tp) {
+              if (tp < ntap) {
+                asm volatile("" : "+s"(so));
+                wv[j * kDmTapSplit + tp] =
+                    __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_w, (int)vo, so, 0));
+                so += 32 * row4;
+              }
+            }
+          }
+          return;
+        }
         uint32_t vo = (uint32_t)wcol * 4u + (uint32_t)(2 * ce * 9 * row4);
         asm volatile("" : "+v"(vo));
         // One scalar offset register stepped by a row (opaque, so the row
@@ -276,10 +306,17 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
             if (tp < ntap) {
               const float v0 = wv[tp][j], v1 = wv[kDmTapSplit + tp][j];
               const uint32_t hi = dm_bf16x2(v0, v1);
-              const uint32_t lo = dm_bf16x2(v0 - __uint_as_float(hi << 16), v1 - __uint_as_float(hi & 0xFFFF0000u));
+              // Residues exact in f32 (each part is its value rounded).
+              const float r0 = v0 - __uint_as_float(hi << 16), r1 = v1 - __uint_as_float(hi & 0xFFFF0000u);
+              const uint32_t lo = dm_bf16x2(r0, r1);
               const int el = el0 + (tap0 + tp) * kDmCo * kDmCi;
               *reinterpret_cast<uint32_t*>(&sh[el]) = hi;
               *reinterpret_cast<uint32_t*>(&sl[el]) = lo;
+              if constexpr (ONE) {
+                const uint32_t lo2 =
+                    dm_bf16x2(r0 - __uint_as_float(lo << 16), r1 - __uint_as_float(lo & 0xFFFF0000u));
+                *reinterpret_cast<uint32_t*>(&s_w[sb][NPART - 1][el]) = lo2;
+              }
             }
           }
         }
@@ -292,7 +329,16 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
       DmItems ld = first_item;
       int ldc = 0;
       auto load = [&](f32x4 (&wv)[kDmWLoads], uint32_t (&wd)[9]) {
-        px3_load_words_at(wd, rs_bits, fbase, a, ih0, iw0, ldc);
+        if constexpr (ONE) {
+#pragma unroll
+          for (int t = 0; t < 9; ++t) {
+            const int w = 9 * ldc + t;
+            const uint32_t off = w < a.cwp ? fbase + (uint32_t)(qpx * a.cwp + w) * 4u : 0x80000000u;
+            wd[t] = __builtin_amdgcn_raw_buffer_load_b32(rs_bits, (int)off, 0, 0);
+          }
+        } else {
+          px3_load_words_at(wd, rs_bits, fbase, a, ih0, iw0, ldc);
+        }
         load_w(wv, ld.col, ldc);
         if (++ldc == nchunks) {
           ldc = 0;
@@ -367,7 +413,8 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
           }
           const uint16_t* sh = s_w[st & 1][0];
           const uint16_t* sl = s_w[st & 1][1];
-          bf16x8 bh[2][2], bl[2][2], af[2][4];
+          const uint16_t* sl2 = s_w[st & 1][NPART - 1];
+          bf16x8 bh[2][2], bl[2][2], bl2[2][2], af[2][4];
           auto frags = [&](int tap, int bb) {
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
@@ -375,6 +422,7 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
               const int off = dm_row(r) * kDmCi + 8 * dm_piece(r, g);
               bh[bb][ct] = *reinterpret_cast<const bf16x8*>(&sh[off]);
               bl[bb][ct] = *reinterpret_cast<const bf16x8*>(&sl[off]);
+              if constexpr (ONE) bl2[bb][ct] = *reinterpret_cast<const bf16x8*>(&sl2[off]);
             }
 #pragma unroll
             for (int rt = 0; rt < 4; ++rt) {
@@ -400,6 +448,14 @@ __global__ __launch_bounds__(kDmThreads) __attribute__((amdgpu_waves_per_eu(2, 2
 #pragma unroll
               for (int ct = 0; ct < 2; ++ct)
                 acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[cb][rt], bl[cb][ct], acc[rt][ct], 0, 0, 0);
+            if constexpr (ONE) {
+#pragma unroll
+              for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+                  acc[rt][ct] =
+                      __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[cb][rt], bl2[cb][ct], acc[rt][ct], 0, 0, 0);
+            }
           }
           __syncthreads();  // stage st & 1 free for step st + 2; stage (st + 1) & 1 written
         }
@@ -512,21 +568,28 @@ DenseQueue* dense_queue_for(hipStream_t stream) {
 int launch_conv_dense_mfma(const ConvArgs& a, DenseQueue* dq, int out_dtype, hipStream_t stream) {
   const int groups = (a.c_out + kDmGroupCo - 1) / kDmGroupCo;
   if (groups > kDenseQueueGroups) return (int)hipErrorInvalidValue;
-  const int nchunks = (a.c_in + kDmCi - 1) / kDmCi;
+  const bool one = a.k == 1;
+  // Stages: 32-channel chunks (3x3, nine taps each), or groups of nine
+  // 32-channel words (1x1).
+  const int nchunks = one ? (a.cwp + 8) / 9 : (a.c_in + kDmCi - 1) / kDmCi;
   // One workgroup per CU (the stage fills most of its LDS; the queue sizes
-  // are known only on the device, and workgroups without pairs read the
+  // are known only on the device, and workgroups without items read the
   // counts and leave).
   const int grid = (num_cus() + kDmXcds - 1) / kDmXcds * kDmXcds;
   timing_begin(K_DENSE_MFMA, stream);
-  if (out_dtype == SF_F16)
-    hipLaunchKernelGGL(k_conv_dense_mfma<__half>, dim3(grid), dim3(kDmThreads), 0, stream, a, dq, a.bits, a.wt,
-                       a.bias, static_cast<__half*>(a.y), groups, nchunks);
-  else if (out_dtype == SF_BF16)
-    hipLaunchKernelGGL(k_conv_dense_mfma<__hip_bfloat16>, dim3(grid), dim3(kDmThreads), 0, stream, a, dq, a.bits,
-                       a.wt, a.bias, static_cast<__hip_bfloat16*>(a.y), groups, nchunks);
-  else
-    hipLaunchKernelGGL(k_conv_dense_mfma<float>, dim3(grid), dim3(kDmThreads), 0, stream, a, dq, a.bits, a.wt,
-                       a.bias, static_cast<float*>(a.y), groups, nchunks);
+  auto go = [&](auto kern, auto* yp) {
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kDmThreads), 0, stream, a, dq, a.bits, a.wt, a.bias, yp, groups, nchunks);
+  };
+  if (out_dtype == SF_F16) {
+    if (one) go(k_conv_dense_mfma<__half, true>, static_cast<__half*>(a.y));
+    else go(k_conv_dense_mfma<__half, false>, static_cast<__half*>(a.y));
+  } else if (out_dtype == SF_BF16) {
+    if (one) go(k_conv_dense_mfma<__hip_bfloat16, true>, static_cast<__hip_bfloat16*>(a.y));
+    else go(k_conv_dense_mfma<__hip_bfloat16, false>, static_cast<__hip_bfloat16*>(a.y));
+  } else {
+    if (one) go(k_conv_dense_mfma<float, true>, static_cast<float*>(a.y));
+    else go(k_conv_dense_mfma<float, false>, static_cast<float*>(a.y));
+  }
   const int rc = (int)hipGetLastError();
   timing_end(K_DENSE_MFMA, stream);
   return rc;

@@ -134,6 +134,15 @@ __device__ __forceinline__ void px_store_rows(const float (&acc)[64], TOut* __re
     if (nco >= 64 || 4 * s < nco) store4<TOut>(yp + 4 * s, acc[4 * s], acc[4 * s + 1], acc[4 * s + 2], acc[4 * s + 3]);
 }
 
+// Dense-tile branch of the streamed 1x1 walk (C_in > 256: every chunk step
+// ends at a barrier): a binary tile of which some pixel has kFlatDenseSpikes
+// or more spikes among the first chunk's 128 channels (i.i.d. spikes at 1%
+// density average 1.28 there; a 64-pixel tile reaches 10 with probability ~5e-5)
+// holds its pass for several times an ordinary tile's walk.  Its run of
+// output pixels goes to the matrix-core queue instead (k_conv_dense_mfma in
+// its 1x1 form, launched right after on the same stream).
+constexpr int kFlatDenseSpikes = 10;
+
 template <int CW, typename TIn, bool ROWS>
 __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const uint32_t* __restrict__ bits,
                                                                const uint32_t* __restrict__ flags,
@@ -141,7 +150,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
                                                                const float* __restrict__ wt,
                                                                const float* __restrict__ bias_p,
                                                                void* __restrict__ y, int groups, int nchunks,
-                                                               int out_dtype) {
+                                                               int out_dtype, DenseQueue* __restrict__ dq) {
   typedef typename PxWord<CW>::type WT;
   constexpr int NW = PxWord<CW>::count;          // walk words per pixel and chunk
   constexpr int BITS = 8 * (int)sizeof(WT);
@@ -196,6 +205,31 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
       for (int64_t q = c_a; q <= c_b; ++q) f |= fl[q];
       value = f != 0u;
     }
+    bool walk = mine;
+    if constexpr (!ROWS && CW == kPxChunkWords) {
+      if (dq != nullptr && !resident && valid && !value) {
+        uint32_t cnt = 0u;
+        if (mine) {
+          const uint32_t* __restrict__ bp = bits + ((int64_t)frame * hw + p0 + lane) * a.cwp;
+#pragma unroll
+          for (int j = 0; j < CW; ++j) cnt += (uint32_t)__popc(bp[j]);
+        }
+        if (__ballot(cnt >= (uint32_t)kFlatDenseSpikes) != 0ull) {
+          uint32_t slot = 0u;
+          if (lane == 0) slot = atomicAdd(&dq->count[grp], 1u);
+          slot = __builtin_amdgcn_readfirstlane(slot);
+          // A slot past the queue's capacity is not written (nor read); the
+          // tile is walked.
+          if (slot < (uint32_t)kDenseQueueCap) {
+            if (lane == 0) {
+              dq->start[grp][slot] = (uint32_t)((int64_t)frame * hw + p0);
+              dq->npx[grp][slot] = (uint8_t)npx;
+            }
+            walk = false;
+          }
+        }
+      }
+    }
     // This lane's pixel (row), channel 0, and the distance between channels.
     const TIn* xp = ROWS ? x + (int64_t)(p0 + lane) * a.c_in : x + (int64_t)frame * a.c_in * hw + p0 + lane;
     const int64_t xcs = ROWS ? 1 : hw;
@@ -210,7 +244,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
       // chunk c-1, which every wavefront finished before the last barrier.
       if (!resident && c + 1 < nchunks)
         load_chunk_px_nw(smem + ((c + 1) & 1) * kPxChunkBytes, wt, c + 1, a.c_in, a.c_out, co0, wave, nw, lane);
-      if (mine) {
+      if (walk) {
         WT w[NW];
         const WT* __restrict__ bp =
             reinterpret_cast<const WT*>(bits + ((int64_t)frame * hw + p0 + lane) * a.cwp + c * CW);
@@ -243,13 +277,13 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_flat(ConvArgs a, const
         __syncthreads();
       }
     }
-    if (mine && ROWS) {
+    if (walk && ROWS) {
       const int64_t yb = (int64_t)(p0 + lane) * c_out_t + co0;
       const int nco = min(64, c_out_t - co0);
       if (out_dtype == SF_F16) px_store_rows(acc, static_cast<__half*>(y) + yb, nco);
       else if (out_dtype == SF_BF16) px_store_rows(acc, static_cast<__hip_bfloat16*>(y) + yb, nco);
       else px_store_rows(acc, static_cast<float*>(y) + yb, nco);
-    } else if (mine) {
+    } else if (walk) {
       const int64_t yb = ((int64_t)frame * c_out_t + co0) * hw_t + p0 + lane;
       const int nco = min(64, c_out_t - co0);
       if (out_dtype == SF_F16) px_store(acc, static_cast<__half*>(y) + yb, hw_t, nco);
@@ -586,7 +620,7 @@ int launch_flat_lif_d(const ConvArgs& a, const void* x2, const FlatLifOut& o, hi
 }
 
 template <int CW, typename TIn, bool ROWS>
-int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream, DenseQueue** dense) {
   const int groups = (a.c_out + 63) / 64;
   const int nchunks = CW < kPxChunkWords ? 1 : a.cwp / kPxChunkWords;
   // Resident: the chunks up to the last one's used 1 KB units; streamed: two
@@ -605,17 +639,25 @@ int launch_flat_t(const ConvArgs& a, int out_dtype, hipStream_t stream) {
   // 1 KB of the LDS is left to the kernel's static arrays.
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
+  // The dense-tile queue for the streamed conv (not the Linear), when entries
+  // (a run's first pixel of the flattened axis, 31 bits) can address it.
+  DenseQueue* dq = !ROWS && CW == kPxChunkWords && nchunks > 2 && groups <= kDenseQueueGroups &&
+                           a.n * (int64_t)a.hw_in < (1ll << 31)
+                       ? dense_queue_for(stream)
+                       : nullptr;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), lds, stream, a, a.bits, a.flags,
-                     static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype);
-  return (int)hipGetLastError();
+                     static_cast<const TIn*>(a.x), a.wt, a.bias, a.y, groups, nchunks, out_dtype, dq);
+  const int rc = (int)hipGetLastError();
+  if (rc == (int)hipSuccess && dense != nullptr) *dense = dq;
+  return rc;
 }
 
 template <typename TIn, bool ROWS>
-int launch_flat_d(const ConvArgs& a, int out_dtype, hipStream_t stream) {
+int launch_flat_d(const ConvArgs& a, int out_dtype, hipStream_t stream, DenseQueue** dense = nullptr) {
   switch (a.cwp) {
-    case 1: return launch_flat_t<1, TIn, ROWS>(a, out_dtype, stream);
-    case 2: return launch_flat_t<2, TIn, ROWS>(a, out_dtype, stream);
-    default: return launch_flat_t<4, TIn, ROWS>(a, out_dtype, stream);
+    case 1: return launch_flat_t<1, TIn, ROWS>(a, out_dtype, stream, dense);
+    case 2: return launch_flat_t<2, TIn, ROWS>(a, out_dtype, stream, dense);
+    default: return launch_flat_t<4, TIn, ROWS>(a, out_dtype, stream, dense);
   }
 }
 
@@ -627,11 +669,14 @@ bool flat_applicable(const ConvArgs& a) {
 }
 
 int launch_conv_flat(const ConvArgs& a, int in_dtype, int out_dtype, hipStream_t stream) {
+  DenseQueue* dense = nullptr;
   timing_begin(K_FLAT, stream);
-  const int rc = in_dtype == SF_F16    ? launch_flat_d<__half, false>(a, out_dtype, stream)
-                 : in_dtype == SF_BF16 ? launch_flat_d<__hip_bfloat16, false>(a, out_dtype, stream)
-                                       : launch_flat_d<float, false>(a, out_dtype, stream);
+  int rc = in_dtype == SF_F16    ? launch_flat_d<__half, false>(a, out_dtype, stream, &dense)
+           : in_dtype == SF_BF16 ? launch_flat_d<__hip_bfloat16, false>(a, out_dtype, stream, &dense)
+                                 : launch_flat_d<float, false>(a, out_dtype, stream, &dense);
   timing_end(K_FLAT, stream);
+  // The tiles the walk queued for the matrix cores, right after it.
+  if (rc == (int)hipSuccess && dense != nullptr) rc = launch_conv_dense_mfma(a, dense, out_dtype, stream);
   return rc;
 }
 

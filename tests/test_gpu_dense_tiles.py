@@ -169,6 +169,69 @@ def test_row_kernel_small_frames_walk_dense_tiles():
     assert ok, f"max abs err {err}"
 
 
+def _run1(x, w, b, **kw):
+    torch.cuda.synchronize()
+    _lib.timing_reset()
+    _lib.timing_enable(True)
+    try:
+        y = sparse_conv2d_forward(x, w, b, kernel_size=1, stride=1, padding=0, **kw)[0]
+        torch.cuda.synchronize()
+        stats = _lib.timing_collect()
+    finally:
+        _lib.timing_enable(False)
+    return y, {k: c for k, (c, _) in stats.items() if c > 0}
+
+
+def _weights1(c_out, c_in, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(c_out, c_in, 1, 1, generator=g) * (2.0 / c_in) ** 0.5
+
+
+FLAT_CASES = [
+    # (N, C_in, H, W, C_out, dense frames): the streamed 1x1 walk (C_in > 256)
+    (16, 1024, 14, 14, 256, range(4, 8)),   # the live network's layer3.x conv1 shape
+    (8, 512, 28, 28, 128, (2, 5)),          # layer2.x conv1
+    (6, 600, 9, 11, 100, (1, 2, 3)),        # 19 of 32 words, partial last stage, partial group, 99-pixel planes
+]
+
+
+@pytest.mark.parametrize("case", FLAT_CASES)
+def test_flat_dense_tiles_match_dense_conv(case):
+    # The 1x1 walk queues its heavy tiles' runs for the matrix cores (the
+    # dense kernel's 1x1 form: nine bitmap words per stage).
+    N, C, H, W, Co, dense = case
+    announce(f"1x1 dense tiles {case[:5]}")
+    x = _bursty((N, C, H, W), dense, seed=51 + C)
+    w = _weights1(Co, C, seed=52)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(53)) * 0.1
+    xd = x.to(DEV)
+    y, kernels = _run1(xd, w.to(DEV), b.to(DEV))
+    assert "conv_flat" in kernels and "conv_dense_mfma" in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, b, 1, 0), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    y2, _ = _run1(xd, w.to(DEV), b.to(DEV))
+    assert torch.equal(y, y2)
+
+
+def test_flat_dense_tiles_half_precision_and_value_frames():
+    N, C, H, W, Co = 8, 768, 14, 14, 128
+    announce("1x1 dense tiles f16, a non-binary frame")
+    x = _bursty((N, C, H, W), range(N), seed=54)
+    g = torch.Generator().manual_seed(55)
+    x[5] = x[5] * torch.randn(C, H, W, generator=g)   # multiplied on the walk, never deferred
+    w = _weights1(Co, C, seed=56)
+    y, kernels = _run1(x.to(DEV), w.to(DEV), None)
+    assert "conv_flat" in kernels and "conv_dense_mfma" in kernels, kernels
+    ok, err, _ = close(y, oconv.sparse_conv2d_ref(x, w, None, 1, 0), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    xh = x.clone()
+    xh[5] = (xh[5] != 0).float()                       # all binary again, as f16 spikes
+    y16, _ = _run1(xh.to(DEV, torch.float16), w.to(DEV), None)
+    assert y16.dtype == torch.float16
+    ok, err, _ = close(y16, oconv.conv2d_ref(xh, w, None, 1, 0), atol=1e-2, rtol=1e-2)
+    assert ok, f"f16: max abs err {err}"
+
+
 def test_queue_is_clear_after_a_dense_call():
     N, C, H, W, Co = 16, 256, 28, 28, 128
     announce("dense then sparse")
