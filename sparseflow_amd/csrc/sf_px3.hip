@@ -930,12 +930,23 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
       const uint32_t plane = (uint32_t)hwo_t * B;
       // One offset register stepped by a plane per store (opaque, so the
       // offsets are not precomputed into registers); soffset stays 0.
+      // Planes of whole 128-byte lines (tiles then start on a line) are
+      // streamed out.
       uint32_t off = base;
+      if ((plane & 127u) == 0u) {
 #pragma unroll
-      for (int co = 0; co < CO; ++co) {
-        BufIO<TOut>::store(from_f32<TOut>(acc[co]), rs, (int)off, 0);
-        off += plane;
-        asm volatile("" : "+v"(off));
+        for (int co = 0; co < CO; ++co) {
+          BufIO<TOut>::template store<kStoreStream>(from_f32<TOut>(acc[co]), rs, (int)off, 0);
+          off += plane;
+          asm volatile("" : "+v"(off));
+        }
+      } else {
+#pragma unroll
+        for (int co = 0; co < CO; ++co) {
+          BufIO<TOut>::store(from_f32<TOut>(acc[co]), rs, (int)off, 0);
+          off += plane;
+          asm volatile("" : "+v"(off));
+        }
       }
     }
   }

@@ -239,6 +239,14 @@ __device__ __forceinline__ void tile_store(float (&acc)[64], void* __restrict__ 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)min(bytes, 0x7fffffffu), 0x00020000);
 }
+// Cache policy operand of the buffer stores: 0, or kStoreStream (the NT
+// bit: the line is written through to HBM early instead of being kept for
+// reuse).  Streaming pays for output written once in whole 128-byte lines;
+// where a wavefront's run of a channel plane starts inside a line, the
+// neighbouring run's half arrives after the line has left, and the line is
+// written twice (measured slower at 28 x 28 and 14 x 14 planes).
+constexpr int kStoreStream = 2;
+
 template <typename T>
 struct BufIO;
 template <>
@@ -246,8 +254,9 @@ struct BufIO<float> {
   static __device__ __forceinline__ float load(__amdgpu_buffer_rsrc_t r, int vo, int so) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
   }
+  template <int CP = 0>
   static __device__ __forceinline__ void store(float v, __amdgpu_buffer_rsrc_t r, int vo, int so) {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned int, v), r, vo, so, CP);
   }
 };
 template <>
@@ -255,8 +264,9 @@ struct BufIO<__half> {
   static __device__ __forceinline__ __half load(__amdgpu_buffer_rsrc_t r, int vo, int so) {
     return __builtin_bit_cast(__half, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
   }
+  template <int CP = 0>
   static __device__ __forceinline__ void store(__half v, __amdgpu_buffer_rsrc_t r, int vo, int so) {
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, vo, so, CP);
   }
 };
 template <>
@@ -264,8 +274,9 @@ struct BufIO<__hip_bfloat16> {
   static __device__ __forceinline__ __hip_bfloat16 load(__amdgpu_buffer_rsrc_t r, int vo, int so) {
     return __builtin_bit_cast(__hip_bfloat16, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
   }
+  template <int CP = 0>
   static __device__ __forceinline__ void store(__hip_bfloat16 v, __amdgpu_buffer_rsrc_t r, int vo, int so) {
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, v), r, vo, so, CP);
   }
 };
 
@@ -293,7 +304,8 @@ __device__ __forceinline__ void px3_load_words_at(uint32_t (&w)[9], __amdgpu_buf
 // soffset is the constant 0: with an SGPR soffset the compiler adds no wait
 // state between a 16-byte store and a VALU write of its data registers, and
 // on gfx950 the last lanes of each 16-lane group then store the overwritten
-// value.
+// value.  Spikes are written once, with the streaming policy (the fused
+// conv-LIF forwards measured faster with it).
 typedef unsigned int sf_u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int sf_u32x2 __attribute__((ext_vector_type(2)));
 template <typename T>
@@ -303,12 +315,12 @@ __device__ __forceinline__ void store_bits4(uint32_t q, __amdgpu_buffer_rsrc_t r
   if constexpr (sizeof(T) == 4) {
     constexpr uint32_t one = 0x3f800000u;  // 1.0f
     const sf_u32x4 v = {(q & 1u) ? one : 0u, (q & 2u) ? one : 0u, (q & 4u) ? one : 0u, (q & 8u) ? one : 0u};
-    __builtin_amdgcn_raw_buffer_store_b128(v, r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, vo, so, kStoreStream);
   } else {
     constexpr uint32_t one = std::is_same<T, __half>::value ? 0x3c00u : 0x3f80u;  // 1.0 in f16 / bf16
     const sf_u32x2 v = {((q & 1u) ? one : 0u) | ((q & 2u) ? one << 16 : 0u),
                         ((q & 4u) ? one : 0u) | ((q & 8u) ? one << 16 : 0u)};
-    __builtin_amdgcn_raw_buffer_store_b64(v, r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, vo, so, kStoreStream);
   }
 }
 
