@@ -7,14 +7,16 @@
 // wave-tiles hold most of the work, walk for several times longer than the
 // rest and hold their workgroup at every chunk barrier.  Such tiles are dense
 // enough for the matrix cores: k_conv_px3s (and the row kernel,
-// k_conv_rows_kc, for its row tiles) hands them (by a test on the first
-// chunk's tap words) to a per-channel-group queue instead of walking them,
+// k_conv_rows_kc, for its row tiles, and the streamed 1x1 walk, k_conv_flat,
+// for its pixel tiles) hands them (by a test on the first chunk's words) to a
+// per-channel-group queue instead of walking them,
 // each as a run of at most 64 output pixels of the flattened (frame, pixel)
 // axis, and k_conv_dense_mfma below computes the 64 pixels from each run's
 // first (storing the run's own) as an implicit GEMM,
 //   y[px, co] = bias[co] + sum_k S[px, k] W[k, co],  k = (tap, ci),
 // with the 0/1 spikes exact in bf16 and W split into bf16 hi + lo parts
-// (W = hi + lo + O(2^-17 |W|)), accumulated in f32: the reference's
+// (W = hi + lo + O(2^-17 |W|); the 1x1 form adds a third part, exact to
+// f32), accumulated in f32: the reference's
 // dense-tile tl.dot branch (Kernels/conv2d.py:606-620, the ALL_ONES tile
 // class), taken per tile where the tile is dense, not per whole layer.
 //

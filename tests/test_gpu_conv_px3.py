@@ -87,6 +87,34 @@ def test_px3_fp32_matches_dense(case, density):
     assert native_loaded()
 
 
+@pytest.mark.parametrize("case", [(200, 128, 28, 28, 128, 1), (256, 96, 56, 56, 128, 2)])
+def test_px3_resident_slices_over_passes(case):
+    # 64 < C_in <= 128: 32-channel slices with every input channel's rows
+    # resident and two 64-channel super-chunks per tile.  Enough tiles for
+    # every workgroup to make at least two passes, with non-binary frames
+    # (the value path reads x at the walked super-chunk's channels) in the
+    # first and in the last tiles.  Frames are independent, so a spread of
+    # them is checked against the float64 reference.
+    N, C, H, W, Co, s = case
+    announce(f"px3 passes {case}")
+    x = spikes((N, C, H, W), 0.01, seed=C + N)
+    g = torch.Generator().manual_seed(N)
+    x[0, :, 3:5] = x[0, :, 3:5] * torch.randn(C, 2, W, generator=g)
+    x[N - 1, :, H - 2:] = x[N - 1, :, H - 2:] * torch.randn(C, 2, W, generator=g)
+    w = _weights(Co, C, seed=Co + 5)
+    b = torch.randn(Co, generator=torch.Generator().manual_seed(9)) * 0.1
+    y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV), s)
+    assert "conv_px3" in kernels, kernels
+    Ho, Wo = (H + 2 - 3) // s + 1, (W + 2 - 3) // s + 1
+    waves = (-(-Ho * Wo // 64)) * N * (-(-Co // 32))
+    assert waves > 16 * torch.cuda.get_device_properties(0).multi_processor_count
+    frames = [0, 1, N // 3, (2 * N) // 3, N - 2, N - 1]
+    ok, err, _ = close(y[frames], oconv.sparse_conv2d_ref(x[frames], w, b, s, 1), **FP32_TOL)
+    assert ok, f"max abs err {err}"
+    y2, _ = _run(x.to(DEV), w.to(DEV), b.to(DEV), s)
+    assert torch.equal(y, y2)
+
+
 @pytest.mark.parametrize("stride", [1, 2])
 def test_px3_dense_input(stride):
     x = spikes((2, 96, 12, 12), 0.9, seed=21)
