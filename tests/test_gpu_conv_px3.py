@@ -87,14 +87,17 @@ def test_px3_fp32_matches_dense(case, density):
     assert native_loaded()
 
 
-@pytest.mark.parametrize("case", [(200, 128, 28, 28, 128, 1), (256, 96, 56, 56, 128, 2)])
+@pytest.mark.parametrize("case", [(200, 128, 28, 28, 128, 1), (256, 96, 56, 56, 128, 2), (160, 64, 56, 56, 64, 1)])
 def test_px3_resident_slices_over_passes(case):
-    # 64 < C_in <= 128: 32-channel slices with every input channel's rows
-    # resident and two 64-channel super-chunks per tile.  Enough tiles for
-    # every workgroup to make at least two passes, with non-binary frames
+    # The resident pixel-tile walk (C_in <= 64: 64-channel slices; 64 < C_in
+    # <= 128: 32-channel slices, two 64-channel super-chunks).  Enough tiles for
+    # every workgroup to make at least two passes (the work indices mapped
+    # to tiles by the launch's stride permutation), with non-binary frames
     # (the value path reads x at the walked super-chunk's channels) in the
     # first and in the last tiles.  Frames are independent, so a spread of
-    # them is checked against the float64 reference.
+    # them is checked against the float64 reference, and every frame against
+    # the device's own f32 convolution (a tile left out or taken twice would
+    # show there).
     N, C, H, W, Co, s = case
     announce(f"px3 passes {case}")
     x = spikes((N, C, H, W), 0.01, seed=C + N)
@@ -106,11 +109,14 @@ def test_px3_resident_slices_over_passes(case):
     y, kernels = _run(x.to(DEV), w.to(DEV), b.to(DEV), s)
     assert "conv_px3" in kernels, kernels
     Ho, Wo = (H + 2 - 3) // s + 1, (W + 2 - 3) // s + 1
-    waves = (-(-Ho * Wo // 64)) * N * (-(-Co // 32))
+    waves = (-(-Ho * Wo // 64)) * N * (-(-Co // 64))  # wave-tiles of 64 channels: a lower bound
     assert waves > 16 * torch.cuda.get_device_properties(0).multi_processor_count
     frames = [0, 1, N // 3, (2 * N) // 3, N - 2, N - 1]
     ok, err, _ = close(y[frames], oconv.sparse_conv2d_ref(x[frames], w, b, s, 1), **FP32_TOL)
     assert ok, f"max abs err {err}"
+    with torch.no_grad():
+        yd = torch.nn.functional.conv2d(x.to(DEV), w.to(DEV), b.to(DEV), stride=s, padding=1)
+    assert torch.allclose(y, yd, atol=1e-4, rtol=1e-4), float((y - yd).abs().max())
     y2, _ = _run(x.to(DEV), w.to(DEV), b.to(DEV), s)
     assert torch.equal(y, y2)
 
