@@ -87,11 +87,6 @@ struct ConvArgs {
   int T;                     // fused LIF: time steps
   float tau, v_th, v_reset;
   int hard_reset, decay_input;
-  // k_conv_px3w (not the fused LIF form): work index u takes wave-tile
-  // u * tile_step mod (tiles), tile_step coprime to the tile count, so a
-  // workgroup's tiles sample every frame range; tile_delta = the step of
-  // the tile index between a wavefront's passes.  0: tile = u.
-  int tile_step, tile_delta;
 };
 
 // Launchers (return hipError_t as int).

@@ -35,8 +35,6 @@
 // sparse_conv3x3s2 kernels (Kernels/conv2d.py:564-886) for these shapes.
 #include <type_traits>
 
-#include <numeric>
-
 #include "sf_tile.h"
 
 namespace sf {
@@ -777,17 +775,9 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   // fused LIF form requests a tile's first words at the tile and prefetches
   // per step (the T steps of a tile are its long stretch of work).
   uint32_t nlo[9], nhi[9];
-  // Work index u = pass * nw + wave takes wave-tile t(u): u, or its image
-  // under the host's stride permutation (consecutive tiles hold the same
-  // time step of consecutive frames, and live spikes come in bursts of a
-  // few time steps: without it, the workgroups whose passes cover a burst
-  // take several times the work of the rest and finish last).
-  const bool perm = !LIF && a.tile_step != 0;
-  int tcur = perm ? (int)(((int64_t)((blk / groups) * nw + wave) * a.tile_step) % total) : 0;
   if constexpr (!LIF) {
-    const int u = (blk / groups) * nw + wave;
-    const int t = perm ? tcur : u;
-    if (u < total) {
+    const int t = (blk / groups) * nw + wave;
+    if (t < total) {
       const int sample = t / tpf, p0 = (t - sample * tpf) * 64;
       const int q = p0 + min(lane0, hwo - p0 - 1);
       const int oh = q / a.w_out, ow = q - oh * a.w_out;
@@ -799,9 +789,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
   for (int pass = blk / groups; pass * nw < total; pass += nblk) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
-    const int u = pass * nw + wave;
-    const bool valid = u < total;
-    const int t = perm ? tcur : u;
+    const int t = pass * nw + wave;
+    const bool valid = t < total;
     const int sample = valid ? t / tpf : 0;
     const int p0 = valid ? (t - sample * tpf) * 64 : 0;
     const int npx = min(64, hwo - p0);
@@ -922,14 +911,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void k_conv_px3w(ConvArgs a, const
       }
     } else {
       {
-        const int un = (pass + nblk) * nw + wave;
-        int tn = un;
-        if (perm) {
-          tcur += a.tile_delta;
-          if (tcur >= total) tcur -= total;
-          tn = tcur;
-        }
-        if (un < total) {
+        const int tn = (pass + nblk) * nw + wave;
+        if (tn < total) {
           const int ns = tn / tpf, np0 = (tn - ns * tpf) * 64;
           const int nq = np0 + min(lane, hwo - np0 - 1);
           const int noh = nq / a.w_out, now = nq - noh * a.w_out;
@@ -983,19 +966,7 @@ int launch_px3w_to(const ConvArgs& a, hipStream_t stream) {
   constexpr auto kern = k_conv_px3w<TIn, TOut, CO, LIF>;
   const int e = set_lds_limit_once<kern>(kMaxLdsBytes - 1024);
   if (e != (int)hipSuccess) return e;
-  ConvArgs ap = a;
-  ap.tile_step = ap.tile_delta = 0;
-  if (!LIF && tiles > 2) {
-    // A stride near tiles / golden ratio, coprime to the tile count: runs of
-    // consecutive work indices land on well-spread tiles.
-    int64_t step = (int64_t)((double)tiles * 0.6180339887498949);
-    if (step < 1) step = 1;
-    while (std::gcd(step, tiles) != 1) ++step;
-    const int64_t nblk = grid / groups;
-    ap.tile_step = (int)step;
-    ap.tile_delta = (int)(((nblk * nw) % tiles) * step % tiles);
-  }
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), (size_t)px3w_bytes<CO>(), stream, ap, a.bits, a.flags,
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * nw), (size_t)px3w_bytes<CO>(), stream, a, a.bits, a.flags,
                      static_cast<const TIn*>(a.x), a.wt, a.bias, static_cast<TOut*>(a.y), groups);
   return (int)hipGetLastError();
 }

@@ -91,8 +91,7 @@ def test_px3_fp32_matches_dense(case, density):
 def test_px3_resident_slices_over_passes(case):
     # The resident pixel-tile walk (C_in <= 64: 64-channel slices; 64 < C_in
     # <= 128: 32-channel slices, two 64-channel super-chunks).  Enough tiles for
-    # every workgroup to make at least two passes (the work indices mapped
-    # to tiles by the launch's stride permutation), with non-binary frames
+    # every workgroup to make at least two passes, with non-binary frames
     # (the value path reads x at the walked super-chunk's channels) in the
     # first and in the last tiles.  Frames are independent, so a spread of
     # them is checked against the float64 reference, and every frame against
